@@ -1,0 +1,127 @@
+/*
+ * vgr -- MI355X-native (gfx950) forward/inference renderer of the voronoi-gauss field.
+ *
+ * C ABI of libvgr.so. Every entry point takes raw device pointers (inputs borrowed for the duration of the
+ * asynchronous launch, outputs owned and allocated by the caller), element counts, and the HIP stream as an
+ * opaque pointer (NULL = the default stream). Launches are asynchronous: nothing here synchronises.
+ * Return value: VGR_OK, or an error code with a message available from vgr_last_error() (thread-local).
+ * A count of zero rays / samples / sites is valid and launches nothing, like the reference (outputs untouched).
+ *
+ * Arrays are C-contiguous. Shapes use N sites, E = sum of self-inclusive neighbourhood sizes, M = E - N,
+ * B rays, S samples per ray, m samples.
+ */
+#ifndef VGR_H
+#define VGR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VGR_OK 0
+#define VGR_ERR_INVALID 1 /* bad argument: null pointer, size, mode out of range */
+#define VGR_ERR_LAUNCH 2  /* the HIP runtime reported a launch or device error */
+
+#define VGR_COLOR_LAZY 0  /* "exact": colours in a second pass for segments with weight > w_thresh */
+#define VGR_COLOR_BAKED 1 /* per-view site colours stored in attr[:, 16:19] */
+#define VGR_COLOR_FUSED 2 /* online blend in the density pass */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* vgr_last_error(void);
+
+/* ABI version of this library (incremented on any signature change). */
+int vgr_abi_version(void);
+
+/*
+ * Inference rendering at the ray / Voronoi-face interaction points (thread per ray, wave64 tiles).
+ * Replaces foam_infer() of csrc/foam_infer.cu:376-435 (pybind11 export :437-440), bound by
+ * ext.foam_infer_extension() (ext.py:42-43) and called from render_rays_foam_infer (render.py:251-255).
+ *
+ *   points  f32 (N, 4)            site positions (4th component unused)
+ *   offsets i32 (N + 1)           self-first neighbourhood CSR (offsets[c] is the edge of c itself)
+ *   nbr     i32 (E)               site of every edge
+ *   edge    f32 (E, 4)            (p_j, half2(r2_j, lam_j) bit pattern)
+ *   attr    f32 (N, 20)           dA(6), min(raw, 30), 0, cA(6), 0, 0, baked rgb(3), 0
+ *   sh      f32 (N, 16, 3) or f16 (sh_half = 1); may be NULL in baked mode
+ *   o, d    f32 (B, 3); start i32 (B); near_t, far_t f32 (B)
+ *   cap     i32 (B) per-ray sample budget, or NULL (unbounded)
+ *   orig    i32 (N) original site index for tie-breaking after a renumbering, or NULL
+ *   outputs rgb f32 (B, 3) foreground (no background), T f32 (B), depth f32 (B),
+ *           stats i32 (B, 5) = samples, segments with colour, walk steps, density terms, SH evaluations
+ * color_mode: VGR_COLOR_*; stage: 0 exit faces only, 1 + density, 2 full rendering.
+ * Rays whose start index is outside [0, N) are not traced: rgb = depth = 0, T = 1, stats = 0.
+ */
+int vgr_foam_infer(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                   const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
+                   int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                   const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
+                   int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
+                   float* T, float* depth, int32_t* stats, void* stream);
+
+/*
+ * vgr_foam_infer plus a trace sink: trace i32 (B, trace_cap) receives the cell of every sample, in original
+ * numbering (orig[c] when orig is given), for the first min(stats[:, 0], trace_cap) samples of each ray.
+ * No counterpart in the reference (it has no trace output); used to check visited-cell sequences.
+ */
+int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                          const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
+                          int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                          const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
+                          int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
+                          float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream);
+
+/*
+ * Fused uniform-step march (forward). Replaces march_forward() of csrc/march.cu:383-403 (export :432),
+ * bound by ext.march (ext.py:172-182) and called from render_rays_uniform (render.py:118-119).
+ *   points f32 (N, 3), offsets i32 (N + 1), adj i32 (M) Delaunay CSR; raw f32 (N); dA, cA f32 (N, 6) conics;
+ *   sh f32 (N, 16, 3); o, d f32 (B, 3); start i32 (B); near_t, mid_t, far_t f32 (B)
+ *   outputs rgb f32 (B, 3), T f32 (B), depth f32 (B), stats i32 (B, 3) = samples, samples with colour, walk steps
+ * trace (optional, NULL = none) i32 (B, trace_cap): the site of every sample.
+ */
+int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                      int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                      int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                      const float* mid_t, const float* far_t, int64_t n_rays, double dt, int64_t n_bg,
+                      double t_thresh, double w_thresh, float* rgb, float* T, float* depth, int32_t* stats,
+                      int32_t* trace, int64_t trace_cap, void* stream);
+
+/*
+ * Nearest site of every sorted ray sample o + z d by a greedy walk (strict <). Replaces walk() of
+ * csrc/vgf.cu:438-456 (export :566), bound by Graph.walk (ext.py:54-58).
+ *   z f32 (B, S) sorted per ray; start i32 (B) -> site i32 (B, S), steps i32 (B) (steps may be NULL)
+ */
+int vgr_walk(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj, int64_t n_adj,
+             const float* o, const float* d, const float* z, const int32_t* start, int64_t n_rays, int64_t n_samples,
+             int32_t* site, int32_t* steps, void* stream);
+
+/*
+ * sigma(x) over the Voronoi neighbourhood of site. Replaces density_forward() of csrc/vgf.cu:458-475
+ * (export :567), bound by ext.density (ext.py:78-87).
+ *   raw f32 (N), log_scale f32 (N, 3), quat f32 (N, 4) wxyz; x f32 (m, 3), site i32 (m) -> sigma f32 (m)
+ */
+int vgr_density_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                        int64_t n_adj, const float* raw, const float* log_scale, const float* quat, const float* x,
+                        const int32_t* site, int64_t m, double scale_mult, float* sigma, void* stream);
+
+/*
+ * Normalised blend of max(SH_k(d) + 1/2, 0) over the Voronoi neighbourhood of site. Replaces color_forward()
+ * of csrc/vgf.cu:494-513 (export :569), bound by ext.color (ext.py:108-117).
+ *   log_scale f32 (N, 3), quat f32 (N, 4), sh f32 (N, 16, 3); x, dirs f32 (m, 3), site i32 (m) -> rgb f32 (m, 3)
+ */
+int vgr_color_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                      int64_t n_adj, const float* log_scale, const float* quat, const float* sh, int64_t sh_deg,
+                      const float* x, const float* dirs, const int32_t* site, int64_t m, float* rgb, void* stream);
+
+/*
+ * Conics A = R diag(1 / (s^2 + floor^2)) R^T as (xx, xy, xz, yy, yz, zz). Replaces conic_forward() of
+ * csrc/vgf.cu:535-546 (export :564), bound by ext.conic (ext.py:134-136).
+ *   log_scale f32 (n, 3), quat f32 (n, 4) -> A f32 (n, 6)
+ */
+int vgr_conic_forward(const float* log_scale, const float* quat, int64_t n, double floor, float* A, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VGR_H */

@@ -1,0 +1,690 @@
+/*
+ * CPU oracle of the voronoi-gauss forward/inference path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This file is the parity checker and the reported CPU baseline. Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg load it; the product path (libvgr.so) never links, loads or calls it.
+ *
+ * It restates, in plain C with a declared fp32 arithmetic, the semantics of the reference kernels:
+ *   foam_infer    csrc/foam_infer.cu:50-361   (walk_to :176-194, eval_cell :199-257, color_lazy :260-284,
+ *                                               kernel :286-361, cache :151-168, site_color :121-149)
+ *   march_forward csrc/march.cu:134-262        (load_ray :134-141, sample_at :143-153, walk_to :157-180,
+ *                                               density_at :182-192, color_at :195-219, kernel :221-262)
+ *   walk          csrc/vgf.cu:51-79
+ *   density       csrc/vgf.cu:98-119,152-177
+ *   color         csrc/vgf.cu:202-282
+ *   conic         csrc/vgf.cu:340-380
+ * Arithmetic contract shared with the HIP kernels: fp32, every expression evaluated left to right as
+ * written, no contraction into FMA (-ffp-contract=off), IEEE division and sqrt, fminf/fmaxf. Transcendentals
+ * (expf) are libm's; the kernels call the device exp, so values agree to a few ulps, not bitwise.
+ * The visited-cell sequences depend only on comparisons of non-contracted products/sums and one division,
+ * which both sides evaluate identically, so they agree bit for bit.
+ *
+ * Pinning (what checks this file, tests/test_oracle.py): float64 dense references restated from the
+ * reference tests (test_foam.py:18-37,76-104; test_march.py:14-22,59-79; test_grad.py:21-48,92-104),
+ * brute-force nearest sites, the segment-in-cell invariant, closed forms (SH constants at d=(0,0,1), conic
+ * A*Sigma = I), lazy == fused colours, cache on == cache off, Morton-renumbering invariance.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <limits.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define K_INF 3.402823466e38f
+#define K_WALK_CAP 4096
+#define K_MAX_CELLS 8192
+#define K_CACHE 8
+
+enum { LAZY = 0, BAKED = 1, FUSED = 2 };
+
+/* ------------------------------------------------------------------------------------------ helpers */
+
+/* IEEE binary16 -> binary32, exact (every half is a float). */
+static float half_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s;
+        } else { /* subnormal half: m * 2^-24 */
+            float f = (float)m * 5.9604644775390625e-08f;
+            memcpy(&bits, &f, 4);
+            bits |= s;
+        }
+    } else if (e == 31) {
+        bits = s | 0x7f800000u | (m << 13);
+    } else {
+        bits = s | ((e + 112) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+static inline float bits_float(int32_t i) { float f; memcpy(&f, &i, 4); return f; }
+static inline int32_t float_bits(float f) { int32_t i; memcpy(&i, &f, 4); return i; }
+
+/* (r2, lam) stored as half2 in the 4th float of an edge record: low half r2, high half lam (render.py:197). */
+static inline void cutoffs(float w, float* r2, float* lam) {
+    uint32_t u;
+    memcpy(&u, &w, 4);
+    *r2 = half_to_float((uint16_t)(u & 0xffffu));
+    *lam = half_to_float((uint16_t)(u >> 16));
+}
+
+/* v^T A v with A = (xx, xy, xz, yy, yz, zz); foam_infer.cu:74-77, march.cu:80-84. */
+static inline float maha(float xx, float xy, float xz, float yy, float yz, float zz, float vx, float vy, float vz) {
+    return xx * vx * vx + yy * vy * vy + zz * vz * vz + 2.f * (xy * vx * vy + xz * vx * vz + yz * vy * vz);
+}
+
+/* Real SH basis, 3DGS constants and signs; foam_infer.cu:95-118 = march.cu:97-120 = vgf.cu:205-228. */
+static void sh_basis(float x, float y, float z, int deg, float b[16]) {
+    b[0] = 0.28209479177387814f;
+    for (int i = 1; i < 16; ++i) b[i] = 0.f;
+    if (deg < 1) return;
+    b[1] = -0.4886025119029199f * y;
+    b[2] = 0.4886025119029199f * z;
+    b[3] = -0.4886025119029199f * x;
+    if (deg < 2) return;
+    const float xx = x * x, yy = y * y, zz = z * z;
+    b[4] = 1.0925484305920792f * x * y;
+    b[5] = -1.0925484305920792f * y * z;
+    b[6] = 0.31539156525252005f * (2.f * zz - xx - yy);
+    b[7] = -1.0925484305920792f * x * z;
+    b[8] = 0.5462742152960396f * (xx - yy);
+    if (deg < 3) return;
+    b[9] = -0.5900435899266435f * y * (3.f * xx - yy);
+    b[10] = 2.890611442640554f * x * y * z;
+    b[11] = -0.4570457994644658f * y * (4.f * zz - xx - yy);
+    b[12] = 0.3731763325901154f * z * (2.f * zz - 3.f * xx - 3.f * yy);
+    b[13] = -0.4570457994644658f * x * (4.f * zz - xx - yy);
+    b[14] = 1.445305721320277f * z * (xx - yy);
+    b[15] = -0.5900435899266435f * x * (xx - 3.f * yy);
+}
+
+void oracle_sh_basis(float x, float y, float z, int deg, float* b) { sh_basis(x, y, z, deg, b); }
+
+/* ======================================================================================= foam_infer */
+
+typedef struct {
+    const float* points;   /* (N, 4) */
+    const int32_t* offsets; /* (N + 1), self-first neighbourhoods */
+    const int32_t* nbr;    /* (E) */
+    const float* edge;     /* (E, 4): p_j, half2(r2_j, lam_j) */
+    const float* attr;     /* (N, 20) */
+    const void* sh;        /* (N, 16, 3) f32 or f16 */
+    const int32_t* orig;   /* (N) or NULL */
+    int sh_half;
+} Net;
+
+typedef struct {
+    float t_thresh, w_thresh, color_cut;
+    int sh_deg, color_mode, stage, use_cache;
+} Opt;
+
+typedef struct { float m, a, r, g, b; } Blend;
+
+typedef struct { float rgb[3]; int key; } Slot;
+
+/* k precedes j in the tie-breaking order (smaller original index); foam_infer.cu:61-63. */
+static inline int before(const Net* N, int k, int j) {
+    return N->orig != NULL ? N->orig[k] < N->orig[j] : k < j;
+}
+
+static inline void blend_init(Blend* B) { B->m = K_INF; B->a = B->r = B->g = B->b = 0.f; }
+
+/* Online normalised blend; foam_infer.cu:81-88. */
+static inline void blend_add(Blend* B, float m, float r, float g, float b) {
+    if (m < B->m) {
+        const float s = expf(-0.5f * (B->m - m));
+        B->a *= s; B->r *= s; B->g *= s; B->b *= s; B->m = m;
+    }
+    const float w = expf(-0.5f * (m - B->m));
+    B->a += w; B->r += w * r; B->g += w * g; B->b += w * b;
+}
+
+/* max(SH_k(d) + 1/2, 0) over all 48 coefficients in storage order; foam_infer.cu:121-149. */
+static void site_color(const Net* N, int k, const float b[16], float c[3]) {
+    c[0] = c[1] = c[2] = 0.5f;
+    if (N->sh_half) {
+        const uint16_t* s = (const uint16_t*)N->sh + 48 * (int64_t)k;
+        for (int i = 0; i < 48; ++i) c[i % 3] += b[i / 3] * half_to_float(s[i]);
+    } else {
+        const float* s = (const float*)N->sh + 48 * (int64_t)k;
+        for (int i = 0; i < 48; ++i) c[i % 3] += b[i / 3] * s[i];
+    }
+    c[0] = fmaxf(c[0], 0.f); c[1] = fmaxf(c[1], 0.f); c[2] = fmaxf(c[2], 0.f);
+}
+
+/* Per-ray direct-mapped colour cache, slot k mod 8; foam_infer.cu:151-168. With use_cache = 0 every lookup
+ * misses, which must give identical colours (only the SH-evaluation counter changes). */
+static void cached_color(const Net* N, const Opt* M, Slot* cache, int k, const float b[16], float c[3], int* n_sh) {
+    Slot* e = &cache[k & (K_CACHE - 1)];
+    if (M->use_cache && e->key == k) {
+        c[0] = e->rgb[0]; c[1] = e->rgb[1]; c[2] = e->rgb[2];
+        return;
+    }
+    site_color(N, k, b, c);
+    e->rgb[0] = c[0]; e->rgb[1] = c[1]; e->rgb[2] = c[2]; e->key = k;
+    ++*n_sh;
+}
+
+/* Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c); foam_infer.cu:176-194. */
+static int foam_walk_to(const Net* N, int c, float x0, float x1, float x2, int* steps) {
+    for (int it = 0; it < K_WALK_CAP; ++it) {
+        const float* pc = N->points + 4 * (int64_t)c;
+        float bd = (x0 - pc[0]) * (x0 - pc[0]) + (x1 - pc[1]) * (x1 - pc[1]) + (x2 - pc[2]) * (x2 - pc[2]);
+        int bk = c;
+        const int e0 = N->offsets[c], e1 = N->offsets[c + 1];
+        for (int e = e0 + 1; e < e1; ++e) {
+            const float* ed = N->edge + 4 * (int64_t)e;
+            const int k = N->nbr[e];
+            const float v0 = x0 - ed[0], v1 = x1 - ed[1], v2 = x2 - ed[2];
+            const float dk = v0 * v0 + v1 * v1 + v2 * v2;
+            if (dk < bd || (dk == bd && before(N, k, bk))) { bd = dk; bk = k; }
+        }
+        if (bk == c) break;
+        c = bk;
+        ++*steps;
+    }
+    return c;
+}
+
+/* One pass over the self-first neighbourhood of cell c for the sample at o + t d; foam_infer.cu:199-257. */
+static void eval_cell(const Net* N, const Opt* M, int c, float t, const float o[3], const float d[3],
+                      const float b[16], Slot* cache, int want_exit, float* sigma, float* mmin, Blend* B,
+                      float* t_exit, int* next, int* n_dens, int* n_sh) {
+    const int blend = M->color_mode != LAZY;
+    const float* pc = N->points + 4 * (int64_t)c;
+    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
+    const int e0 = N->offsets[c], e1 = N->offsets[c + 1];
+    *sigma = 0.f; *mmin = K_INF;
+    blend_init(B);
+    *t_exit = K_INF; *next = INT_MAX;
+    for (int e = e0; e < e1; ++e) {
+        const float* ed = N->edge + 4 * (int64_t)e;
+        const int k = N->nbr[e];
+        if (want_exit && e > e0) {
+            const float n0 = ed[0] - pc[0], n1 = ed[1] - pc[1], n2 = ed[2] - pc[2];
+            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+            if (dn > 0.f) {
+                const float m0 = 0.5f * (ed[0] + pc[0]) - o[0], m1 = 0.5f * (ed[1] + pc[1]) - o[1],
+                            m2 = 0.5f * (ed[2] + pc[2]) - o[2];
+                const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
+                if (tt < *t_exit || (tt == *t_exit && (*next == INT_MAX || before(N, k, *next)))) {
+                    *t_exit = tt; *next = k;
+                }
+            }
+        }
+        if (M->stage >= 1) {
+            const float v0 = x0 - ed[0], v1 = x1 - ed[1], v2 = x2 - ed[2];
+            const float r2 = v0 * v0 + v1 * v1 + v2 * v2;
+            float cut_r2, cut_lam;
+            cutoffs(ed[3], &cut_r2, &cut_lam);
+            const float* a = N->attr + 20 * (int64_t)k;
+            if (r2 <= cut_r2) {
+                *sigma += expf(a[6] - 0.5f * maha(a[0], a[1], a[2], a[3], a[4], a[5], v0, v1, v2));
+                ++*n_dens;
+            }
+            if (M->stage >= 2) {
+                const float lb = r2 * cut_lam;
+                if (blend ? lb <= B->m + M->color_cut : lb < *mmin) {
+                    const float m = maha(a[8], a[9], a[10], a[11], a[12], a[13], v0, v1, v2);
+                    if (blend) {
+                        if (m <= B->m + M->color_cut) {
+                            float c3[3];
+                            if (M->color_mode == BAKED) {
+                                c3[0] = a[16]; c3[1] = a[17]; c3[2] = a[18];
+                            } else {
+                                cached_color(N, M, cache, k, b, c3, n_sh);
+                            }
+                            blend_add(B, m, c3[0], c3[1], c3[2]);
+                        }
+                    } else {
+                        *mmin = fminf(*mmin, m);
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* Second (colour) pass of the lazy mode; foam_infer.cu:260-284. */
+static void color_lazy(const Net* N, const Opt* M, int c, float t, float mmin, const float o[3], const float d[3],
+                       const float b[16], Slot* cache, float C[3], int* n_sh) {
+    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
+    const int e0 = N->offsets[c], e1 = N->offsets[c + 1];
+    const float cut = mmin + M->color_cut;
+    float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
+    for (int e = e0; e < e1; ++e) {
+        const float* ed = N->edge + 4 * (int64_t)e;
+        const float v0 = x0 - ed[0], v1 = x1 - ed[1], v2 = x2 - ed[2];
+        float cut_r2, cut_lam;
+        cutoffs(ed[3], &cut_r2, &cut_lam);
+        if ((v0 * v0 + v1 * v1 + v2 * v2) * cut_lam > cut) continue;
+        const int k = N->nbr[e];
+        const float* a = N->attr + 20 * (int64_t)k;
+        const float m = maha(a[8], a[9], a[10], a[11], a[12], a[13], v0, v1, v2);
+        if (m > cut) continue;
+        const float w = expf(-0.5f * (m - mmin));
+        float c3[3];
+        cached_color(N, M, cache, k, b, c3, n_sh);
+        A += w; r += w * c3[0]; g += w * c3[1]; bl += w * c3[2];
+    }
+    const float inv = 1.f / A;
+    C[0] = r * inv; C[1] = g * inv; C[2] = bl * inv;
+}
+
+/* One ray of foam_infer_kernel (foam_infer.cu:286-361). trace (optional) receives the cell of every sample,
+ * in original numbering, up to trace_cap entries; the sample count is stats[0]. */
+static void foam_ray(const Net* N, const Opt* M, const float o[3], const float d[3], int start, float t_near,
+                     float t_far, int max_samples, float rgb[3], float* T_out, float* depth, int32_t stats[5],
+                     int32_t* trace, int trace_cap) {
+    const int blend = M->stage >= 2 && M->color_mode != LAZY;
+    Slot cache[K_CACHE];
+    for (int i = 0; i < K_CACHE; ++i) { cache[i].rgb[0] = cache[i].rgb[1] = cache[i].rgb[2] = 0.f; cache[i].key = -1; }
+    float b[16];
+    for (int i = 0; i < 16; ++i) b[i] = 0.f;
+    if (M->stage >= 2 && M->color_mode != BAKED) sh_basis(d[0], d[1], d[2], M->sh_deg, b);
+
+    int walk_steps = 0, n_dens = 0, n_sh = 0;
+    int c = foam_walk_to(N, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], &walk_steps);
+    float sP, mP, t_exit;
+    int next;
+    Blend BP, BQ;
+    eval_cell(N, M, c, t_near, o, d, b, cache, 1, &sP, &mP, &BP, &t_exit, &next, &n_dens, &n_sh);
+    if (trace != NULL && trace_cap > 0) trace[0] = N->orig != NULL ? N->orig[c] : c;
+    float tP = t_near, CP[3] = {0.f, 0.f, 0.f};
+    int hasP = 0, cP = c;
+    if (blend) {
+        const float inv = 1.f / BP.a;
+        CP[0] = BP.r * inv; CP[1] = BP.g * inv; CP[2] = BP.b * inv; hasP = 1;
+    }
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    int n_samples = 1, n_color = 0;
+    for (int it = 0; it < K_MAX_CELLS; ++it) {
+        const int last = next == INT_MAX || t_exit >= t_far || n_samples + 1 >= max_samples;
+        const float tQ = last ? t_far : fmaxf(t_exit, tP);
+        const int cQ = last ? c : next;
+        float sQ, mQ;
+        eval_cell(N, M, cQ, tQ, o, d, b, cache, !last, &sQ, &mQ, &BQ, &t_exit, &next, &n_dens, &n_sh);
+        if (trace != NULL && n_samples < trace_cap) trace[n_samples] = N->orig != NULL ? N->orig[cQ] : cQ;
+        ++n_samples;
+        const float delta = tQ - tP;
+        const float alpha = 1.f - expf(-0.5f * (sP + sQ) * delta);
+        const float w = T * alpha;
+        float CQ[3] = {0.f, 0.f, 0.f};
+        int hasQ = 0;
+        if (blend) {
+            const float inv = 1.f / BQ.a;
+            CQ[0] = BQ.r * inv; CQ[1] = BQ.g * inv; CQ[2] = BQ.b * inv; hasQ = 1;
+        }
+        if (M->stage >= 2 && w > M->w_thresh) {
+            if (!blend) {
+                if (!hasP) color_lazy(N, M, cP, tP, mP, o, d, b, cache, CP, &n_sh);
+                color_lazy(N, M, cQ, tQ, mQ, o, d, b, cache, CQ, &n_sh);
+                hasQ = 1;
+            }
+            for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (CP[a] + CQ[a]);
+            dep += w * 0.5f * (tP + tQ);
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        tP = tQ; sP = sQ; mP = mQ; hasP = hasQ; cP = cQ; c = cQ;
+        for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
+        if (last || T < M->t_thresh) break;
+    }
+    for (int a = 0; a < 3; ++a) rgb[a] = acc[a];
+    *T_out = T;
+    *depth = dep;
+    stats[0] = n_samples; stats[1] = n_color; stats[2] = walk_steps; stats[3] = n_dens; stats[4] = n_sh;
+}
+
+/* Renders the rays listed in `rays` (or all B rays when rays == NULL, n_sel = B) on n_threads OpenMP threads.
+ * Outputs are indexed by the position in the selection. Returns the wall time in seconds of the parallel loop. */
+double oracle_foam_infer(const float* points, const int32_t* offsets, const int32_t* nbr, const float* edge,
+                         const float* attr, const void* sh, int sh_half, int sh_deg, const float* o, const float* d,
+                         const int32_t* start, const float* near_t, const float* far_t, const int64_t* rays,
+                         int64_t n_sel, float t_thresh, float w_thresh, float color_cut, int color_mode, int stage,
+                         const int32_t* cap, const int32_t* orig, int use_cache, float* rgb, float* T, float* depth,
+                         int32_t* stats, int32_t* trace, int trace_cap, int n_threads) {
+    const Net N = {points, offsets, nbr, edge, attr, sh, orig, sh_half};
+    const Opt M = {t_thresh, w_thresh, color_cut, sh_deg, color_mode, stage, use_cache};
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+    const double t0 = omp_get_wtime();
+#pragma omp parallel for schedule(dynamic, 256)
+#endif
+    for (int64_t i = 0; i < n_sel; ++i) {
+        const int64_t r = rays != NULL ? rays[i] : i;
+        const int ms = cap != NULL ? cap[r] : INT_MAX;
+        foam_ray(&N, &M, o + 3 * r, d + 3 * r, start[r], near_t[r], far_t[r], ms, rgb + 3 * i, T + i, depth + i,
+                 stats + 5 * i, trace != NULL ? trace + (int64_t)trace_cap * i : NULL, trace_cap);
+    }
+#ifdef _OPENMP
+    return omp_get_wtime() - t0;
+#else
+    return 0.0;
+#endif
+}
+
+/* ==================================================================================== march_forward */
+
+typedef struct {
+    const float* points;   /* (N, 3) */
+    const int32_t* offsets; /* (N + 1) */
+    const int32_t* adj;    /* (M) */
+    const float* raw, *dA, *cA, *sh;
+    int sh_deg;
+} Field;
+
+static inline int neighbor(const Field* F, int i, int e0, int e) { return e == 0 ? i : F->adj[e0 + e - 1]; }
+
+/* Sample k of a ray: midpoints of dt steps to mid, then n_bg steps uniform in disparity; march.cu:143-153. */
+static void sample_at(float near, float mid, float far, int n_in, float dt, int n_bg, int k, float* t, float* delta) {
+    if (k < n_in) {
+        const float t0 = near + (float)k * dt, t1 = fminf(t0 + dt, mid);
+        *t = 0.5f * (t0 + t1);
+        *delta = t1 - t0;
+    } else {
+        const float i0 = 1.f / mid, i1 = 1.f / far;
+        const float u0 = (float)(k - n_in) / (float)n_bg, u1 = (float)(k - n_in + 1) / (float)n_bg;
+        *t = 1.f / (i0 + 0.5f * (u0 + u1) * (i1 - i0));
+        *delta = 1.f / (i0 + u1 * (i1 - i0)) - 1.f / (i0 + u0 * (i1 - i0));
+    }
+}
+
+void oracle_sample_at(float near, float mid, float far, int n_in, float dt, int n_bg, int k, float* t, float* delta) {
+    sample_at(near, mid, far, n_in, dt, n_bg, k, t, delta);
+}
+
+/* Lexicographic argmin of (|x - p|^2, index) over {cur} U adj(cur), repeated; march.cu:157-180. */
+static int march_walk_to(const Field* F, int cur, const float x[3], int* steps) {
+    for (int it = 0; it < K_WALK_CAP; ++it) {
+        const int e0 = F->offsets[cur], n = F->offsets[cur + 1] - e0 + 1;
+        float bd = K_INF;
+        int bk = INT_MAX;
+        for (int e = 0; e < n; ++e) {
+            const int k = neighbor(F, cur, e0, e);
+            const float* p = F->points + 3 * (int64_t)k;
+            const float v0 = x[0] - p[0], v1 = x[1] - p[1], v2 = x[2] - p[2];
+            const float dk = v0 * v0 + v1 * v1 + v2 * v2;
+            if (dk < bd || (dk == bd && k < bk)) { bd = dk; bk = k; }
+        }
+        if (bk == cur) break;
+        cur = bk;
+        ++*steps;
+    }
+    return cur;
+}
+
+static inline float conic_maha(const float* A, int k, const float v[3]) {
+    const float* a = A + 6 * (int64_t)k;
+    return a[0] * v[0] * v[0] + a[3] * v[1] * v[1] + a[5] * v[2] * v[2] +
+           2.f * (a[1] * v[0] * v[1] + a[2] * v[0] * v[2] + a[4] * v[1] * v[2]);
+}
+
+static void sh_eval(const float* sh, int k, const float b[16], int nb, float c[3]) {
+    const float* p = sh + 48 * (int64_t)k;
+    c[0] = c[1] = c[2] = 0.5f;
+    for (int j = 0; j < 16 && j < nb; ++j) {
+        c[0] += b[j] * p[3 * j];
+        c[1] += b[j] * p[3 * j + 1];
+        c[2] += b[j] * p[3 * j + 2];
+    }
+}
+
+/* Density at x over the neighbourhood of i (sequential sum); march.cu:182-192. */
+static float march_density(const Field* F, int i, const float x[3]) {
+    const int e0 = F->offsets[i], n = F->offsets[i + 1] - e0 + 1;
+    float s = 0.f;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)k;
+        const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+        s += expf(fminf(F->raw[k], 30.f) - 0.5f * conic_maha(F->dA, k, v));
+    }
+    return s;
+}
+
+/* Two-pass normalised colour blend; march.cu:195-219. */
+static void march_color(const Field* F, int i, const float x[3], const float b[16], float C[3]) {
+    const int e0 = F->offsets[i], n = F->offsets[i + 1] - e0 + 1;
+    const int nb = (F->sh_deg + 1) * (F->sh_deg + 1);
+    float mmin = K_INF;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)k;
+        const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+        mmin = fminf(mmin, conic_maha(F->cA, k, v));
+    }
+    float A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)k;
+        const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+        const float a = expf(-0.5f * (conic_maha(F->cA, k, v) - mmin));
+        float c[3];
+        sh_eval(F->sh, k, b, nb, c);
+        A += a; cr += a * fmaxf(c[0], 0.f); cg += a * fmaxf(c[1], 0.f); cb += a * fmaxf(c[2], 0.f);
+    }
+    const float inv_a = 1.f / A;
+    C[0] = cr * inv_a; C[1] = cg * inv_a; C[2] = cb * inv_a;
+}
+
+static void march_ray(const Field* F, float dt, int n_bg, float t_thresh, float w_thresh, const float o[3],
+                      const float d[3], int start, float near, float mid, float far, float rgb[3], float* T_out,
+                      float* depth, int32_t stats[3], int32_t* trace, int trace_cap) {
+    const int n_in = mid > near ? (int)ceilf((mid - near) / dt) : 0;
+    const int n_total = n_in + n_bg;
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F->sh_deg, b);
+    int cur = start, n_samples = 0, n_color = 0, walk_steps = 0;
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    for (int k = 0; k < n_total; ++k) {
+        float t, delta, x[3];
+        sample_at(near, mid, far, n_in, dt, n_bg, k, &t, &delta);
+        for (int a = 0; a < 3; ++a) x[a] = o[a] + t * d[a];
+        cur = march_walk_to(F, cur, x, &walk_steps);
+        if (trace != NULL && n_samples < trace_cap) trace[n_samples] = cur;
+        const float alpha = 1.f - expf(-march_density(F, cur, x) * delta);
+        const float w = T * alpha;
+        ++n_samples;
+        if (w > w_thresh) {
+            float C[3];
+            march_color(F, cur, x, b, C);
+            for (int a = 0; a < 3; ++a) acc[a] += w * C[a];
+            dep += w * t;
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        if (T < t_thresh) break;
+    }
+    for (int a = 0; a < 3; ++a) rgb[a] = acc[a];
+    *T_out = T;
+    *depth = dep;
+    stats[0] = n_samples; stats[1] = n_color; stats[2] = walk_steps;
+}
+
+double oracle_march_forward(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                            const float* dA, const float* cA, const float* sh, int sh_deg, const float* o,
+                            const float* d, const int32_t* start, const float* near_t, const float* mid_t,
+                            const float* far_t, const int64_t* rays, int64_t n_sel, float dt, int n_bg,
+                            float t_thresh, float w_thresh, float* rgb, float* T, float* depth, int32_t* stats,
+                            int32_t* trace, int trace_cap, int n_threads) {
+    const Field F = {points, offsets, adj, raw, dA, cA, sh, sh_deg};
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+    const double t0 = omp_get_wtime();
+#pragma omp parallel for schedule(dynamic, 64)
+#endif
+    for (int64_t i = 0; i < n_sel; ++i) {
+        const int64_t r = rays != NULL ? rays[i] : i;
+        march_ray(&F, dt, n_bg, t_thresh, w_thresh, o + 3 * r, d + 3 * r, start[r], near_t[r], mid_t[r], far_t[r],
+                  rgb + 3 * i, T + i, depth + i, stats + 3 * i,
+                  trace != NULL ? trace + (int64_t)trace_cap * i : NULL, trace_cap);
+    }
+#ifdef _OPENMP
+    return omp_get_wtime() - t0;
+#else
+    return 0.0;
+#endif
+}
+
+/* ============================================================================ vgf forward operators */
+
+/* Greedy walk of S sorted samples per ray, strict < (first found wins), starting at the previous site;
+ * vgf.cu:44-79. */
+void oracle_walk(const float* points, const int32_t* offsets, const int32_t* adj, const float* o, const float* d,
+                 const float* z, const int32_t* start, int64_t B, int S, int32_t* site, int32_t* steps, int n_threads) {
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#pragma omp parallel for schedule(dynamic, 64)
+#endif
+    for (int64_t r = 0; r < B; ++r) {
+        const float ox = o[3 * r], oy = o[3 * r + 1], oz = o[3 * r + 2];
+        const float dx = d[3 * r], dy = d[3 * r + 1], dz = d[3 * r + 2];
+        int cur = start[r], total = 0;
+        for (int s = 0; s < S; ++s) {
+            const float t = z[r * S + s];
+            const float x = ox + t * dx, y = oy + t * dy, w = oz + t * dz;
+            const float* pc = points + 3 * (int64_t)cur;
+            const float cx = x - pc[0], cy = y - pc[1], cz = w - pc[2];
+            float best_d = cx * cx + cy * cy + cz * cz;
+            for (int it = 0; it < K_WALK_CAP; ++it) {
+                int best = cur;
+                const int e1 = offsets[cur + 1];
+                for (int e = offsets[cur]; e < e1; ++e) {
+                    const int q = adj[e];
+                    const float* p = points + 3 * (int64_t)q;
+                    const float qx = x - p[0], qy = y - p[1], qz = w - p[2];
+                    const float dq = qx * qx + qy * qy + qz * qz;
+                    if (dq < best_d) { best_d = dq; best = q; }
+                }
+                if (best == cur) break;
+                cur = best;
+                ++total;
+            }
+            site[r * S + s] = cur;
+        }
+        if (steps != NULL) steps[r] = total;
+    }
+}
+
+/* Mahalanobis distance of x to Gaussian i from (log_scale, quat), with 1/s^2 scaled by inv_mult2;
+ * vgf.cu:98-119. */
+static float gauss_m(const float* points, const float* log_scale, const float* quat, int i, float x, float y, float z,
+                     float inv_mult2) {
+    const int64_t i3 = 3 * (int64_t)i;
+    const float v0 = x - points[i3], v1 = y - points[i3 + 1], v2 = z - points[i3 + 2];
+    const float* q = quat + 4 * (int64_t)i;
+    const float qnorm = fmaxf(sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]), 1e-12f);
+    const float w = q[0] / qnorm, a = q[1] / qnorm, b = q[2] / qnorm, c = q[3] / qnorm;
+    float R[9];
+    R[0] = 1.f - 2.f * (b * b + c * c); R[1] = 2.f * (a * b - w * c); R[2] = 2.f * (a * c + w * b);
+    R[3] = 2.f * (a * b + w * c); R[4] = 1.f - 2.f * (a * a + c * c); R[5] = 2.f * (b * c - w * a);
+    R[6] = 2.f * (a * c - w * b); R[7] = 2.f * (b * c + w * a); R[8] = 1.f - 2.f * (a * a + b * b);
+    float m = 0.f;
+    for (int k = 0; k < 3; ++k) {
+        const float yk = R[k] * v0 + R[3 + k] * v1 + R[6 + k] * v2;
+        const float s = expf(fminf(fmaxf(log_scale[i3 + k], -20.f), 20.f));
+        const float is2 = inv_mult2 / (s * s);
+        m += yk * yk * is2;
+    }
+    return m;
+}
+
+/* sigma(x) = sum over {i} U adj(i) of exp(min(raw_k, 30) - m_k / 2); vgf.cu:152-177. */
+void oracle_density(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                    const float* log_scale, const float* quat, const float* x, const int32_t* site, int64_t m,
+                    float scale_mult, float* sigma, int n_threads) {
+    const float inv_mult2 = (float)(1.0 / ((double)scale_mult * (double)scale_mult));
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t t = 0; t < m; ++t) {
+        const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
+        const int i = site[t];
+        float s = 0.f;
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            s += expf(fminf(raw[k], 30.f) - 0.5f * gauss_m(points, log_scale, quat, k, qx, qy, qz, inv_mult2));
+        }
+        sigma[t] = s;
+    }
+}
+
+/* Online-softmax blend of max(SH_k(d) + 1/2, 0) over {i} U adj(i); vgf.cu:230-282. */
+void oracle_color(const float* points, const int32_t* offsets, const int32_t* adj, const float* log_scale,
+                  const float* quat, const float* sh, int sh_deg, const float* x, const float* dirs,
+                  const int32_t* site, int64_t m, float* rgb, int n_threads) {
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t t = 0; t < m; ++t) {
+        const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
+        float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
+        const float inv = 1.f / sqrtf(fmaxf(dx * dx + dy * dy + dz * dz, 1e-20f));
+        dx *= inv; dy *= inv; dz *= inv;
+        float b[16];
+        sh_basis(dx, dy, dz, sh_deg, b);
+        const int nb = (sh_deg + 1) * (sh_deg + 1);
+        const int i = site[t];
+        float mmin = K_INF, A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            const float mk = gauss_m(points, log_scale, quat, k, qx, qy, qz, 1.f);
+            if (mk < mmin) {
+                const float f = mmin == K_INF ? 0.f : expf(-0.5f * (mmin - mk));
+                A *= f; cr *= f; cg *= f; cb *= f;
+                mmin = mk;
+            }
+            const float a = expf(-0.5f * (mk - mmin));
+            float c[3];
+            sh_eval(sh, k, b, nb, c);
+            A += a;
+            cr += a * fmaxf(c[0], 0.f);
+            cg += a * fmaxf(c[1], 0.f);
+            cb += a * fmaxf(c[2], 0.f);
+        }
+        rgb[3 * t] = cr / A;
+        rgb[3 * t + 1] = cg / A;
+        rgb[3 * t + 2] = cb / A;
+    }
+}
+
+/* A = R diag(1 / (s^2 + floor^2)) R^T as (xx, xy, xz, yy, yz, zz); vgf.cu:340-380. */
+void oracle_conic(const float* log_scale, const float* quat, int64_t n, float floor2, float* A) {
+    static const int ab[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
+    for (int64_t i = 0; i < n; ++i) {
+        const float* q = quat + 4 * i;
+        const float qnorm = fmaxf(sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]), 1e-12f);
+        const float w = q[0] / qnorm, a = q[1] / qnorm, b = q[2] / qnorm, c = q[3] / qnorm;
+        float R[9], iv[3];
+        R[0] = 1.f - 2.f * (b * b + c * c); R[1] = 2.f * (a * b - w * c); R[2] = 2.f * (a * c + w * b);
+        R[3] = 2.f * (a * b + w * c); R[4] = 1.f - 2.f * (a * a + c * c); R[5] = 2.f * (b * c - w * a);
+        R[6] = 2.f * (a * c - w * b); R[7] = 2.f * (b * c + w * a); R[8] = 1.f - 2.f * (a * a + b * b);
+        for (int k = 0; k < 3; ++k) {
+            const float s = expf(2.f * fminf(fmaxf(log_scale[3 * i + k], -20.f), 20.f));
+            iv[k] = 1.f / (s + floor2);
+        }
+        for (int e = 0; e < 6; ++e) {
+            const int x = ab[e][0], y = ab[e][1];
+            A[6 * i + e] = R[3 * x] * R[3 * y] * iv[0] + R[3 * x + 1] * R[3 * y + 1] * iv[1] +
+                           R[3 * x + 2] * R[3 * y + 2] * iv[2];
+        }
+    }
+}
+
+int oracle_omp_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

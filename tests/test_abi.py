@@ -1,0 +1,59 @@
+"""The C-ABI library: it loads without a GPU, exports every entry point include/vgr.h declares, and the Python
+binding declares each with the header's parameter count. No compute call is made here."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'vgr.h')
+
+
+def declared():
+	"""{name: parameter count} of every function declared in include/vgr.h."""
+	text = open(HEADER).read()
+	text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+	out = {}
+	for m in re.finditer(r'\b(?:int|const char\*)\s+(vgr_\w+)\s*\(([^)]*)\)\s*;', text):
+		params = m.group(2).strip()
+		out[m.group(1)] = 0 if params in ('', 'void') else params.count(',') + 1
+	return out
+
+
+def test_header_declares_the_entry_points():
+	names = declared()
+	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_march_forward', 'vgr_walk', 'vgr_density_forward',
+			  'vgr_color_forward', 'vgr_conic_forward', 'vgr_last_error', 'vgr_abi_version'):
+		assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+	from vgr import _lib
+	if not os.path.exists(_lib.LIB_PATH):
+		pytest.fail('libvgr.so is not built (run __graft_entry__.build())')
+	lib = ctypes.CDLL(_lib.LIB_PATH)
+	for name, nparams in declared().items():
+		assert hasattr(lib, name), f'{name} not exported'
+		assert len(_lib.SIGNATURES[name]) == nparams, f'{name}: binding has {len(_lib.SIGNATURES[name])} args'
+
+
+def test_library_reports_argument_errors_without_a_gpu():
+	"""Argument validation runs on the host before any HIP call."""
+	from vgr import _lib
+	lib = _lib.load()
+	assert lib.vgr_abi_version() == _lib.ABI_VERSION
+	rc = lib.vgr_conic_forward(None, None, -1, 0.0, None, None)
+	assert rc == 1 and b'n must be >= 0' in lib.vgr_last_error()
+	rc = lib.vgr_conic_forward(None, None, 0, 0.0, None, None)  # empty: nothing to launch
+	assert rc == 0
+	args = [None, 10, None, None, None, 10, None, None, 0, 3, None, None, None, None, None, 5, 1e-4, 1e-4, 1e30, 7, 2,
+			None, None, None, None, None, None, None]
+	assert lib.vgr_foam_infer(*args) == 1 and b'color_mode' in lib.vgr_last_error()
+	args[19], args[20] = 0, 9
+	assert lib.vgr_foam_infer(*args) == 1 and b'stage' in lib.vgr_last_error()
+	args[20] = 2
+	assert lib.vgr_foam_infer(*args) == 1 and b'null scene pointer' in lib.vgr_last_error()
+	with pytest.raises(RuntimeError, match='trace'):
+		_lib.call('vgr_foam_infer_traced', *args[:-1], None, 0, None)

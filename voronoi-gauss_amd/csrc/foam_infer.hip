@@ -1,0 +1,445 @@
+// Inference renderer at the ray / Voronoi-face interaction points, gfx950.
+//
+// Semantics follow csrc/foam_infer.cu:50-361 of the reference: a ray starts in the cell of x(near) (greedy
+// walk from `start`), then crosses cells through their exit faces (the nearest bisector plane ahead of the
+// ray); every crossing is a sample evaluated with the self-first neighbourhood of the cell it enters, and
+// consecutive samples are composited with the trapezoid rule until x(far), `cap` samples, or T < t_thresh.
+//
+// MI355X mapping: one ray per lane, rays ordered in 8x8 pixel tiles by the host so a wave64 is one tile and
+// its lanes walk mostly the same cells (the per-edge loads of a cell are then one broadcast line per wave);
+// workgroups are remapped so each XCD renders a contiguous band of tiles (L2 locality). The per-ray colour
+// cache (8 direct-mapped slots, keyed by site) lives in LDS, slot-major so lanes hit consecutive banks.
+#include "vgr_abi.h"
+#include "vgr_device.h"
+
+namespace vgr {
+namespace {
+
+constexpr int kBlock = 64;  // one wave64 per workgroup = one 8x8 ray tile
+constexpr int kCache = 8;
+constexpr int kLazy = VGR_COLOR_LAZY, kBaked = VGR_COLOR_BAKED, kFused = VGR_COLOR_FUSED;
+
+struct FoamScene {
+    const float4* __restrict__ points;  // (N) p, w unused
+    const int* __restrict__ offsets;    // (N + 1) self-first
+    const int* __restrict__ nbr;        // (E)
+    const float4* __restrict__ edge;    // (E) p_j, half2(r2_j, lam_j)
+    const float4* __restrict__ attr;    // (N, 5)
+    const float4* __restrict__ sh;      // (N, 12) fp32 or (N, 6) fp16
+    const int* __restrict__ orig;       // (N) or null
+    int n_sites;
+};
+
+struct FoamParams {
+    float t_thresh, w_thresh, color_cut;
+    int sh_deg;
+};
+
+struct FoamRays {
+    const float* __restrict__ o;
+    const float* __restrict__ d;
+    const int* __restrict__ start;
+    const float* __restrict__ t_near;
+    const float* __restrict__ t_far;
+    const int* __restrict__ cap;
+    int64_t n;
+};
+
+struct FoamOut {
+    float* __restrict__ rgb;
+    float* __restrict__ T;
+    float* __restrict__ depth;
+    int* __restrict__ stats;
+    int* __restrict__ trace;
+    int64_t trace_cap;
+};
+
+// Running normalised colour blend (fused / baked modes).
+struct Blend {
+    float m, a, r, g, b;
+};
+
+__device__ __forceinline__ void blend_init(Blend& B) { B.m = kInf, B.a = B.r = B.g = B.b = 0.f; }
+
+__device__ __forceinline__ void blend_add(Blend& B, float m, float r, float g, float b) {
+    if (m < B.m) {
+        const float s = fexp(-0.5f * (B.m - m));
+        B.a *= s, B.r *= s, B.g *= s, B.b *= s, B.m = m;
+    }
+    const float w = fexp(-0.5f * (m - B.m));
+    B.a += w, B.r += w * r, B.g += w * g, B.b += w * b;
+}
+
+// k precedes j in the tie-breaking order: the smaller original index.
+__device__ __forceinline__ bool before(const FoamScene& S, int k, int j) {
+    return S.orig != nullptr ? S.orig[k] < S.orig[j] : k < j;
+}
+
+// (r2, lam) half2 packed in the 4th component of an edge record.
+__device__ __forceinline__ float2 cutoffs(float w) {
+    const uint32_t u = __float_as_uint(w);
+    const _Float16 lo = __builtin_bit_cast(_Float16, static_cast<uint16_t>(u & 0xffffu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16));
+    return make_float2(static_cast<float>(lo), static_cast<float>(hi));
+}
+
+// max(SH_k(d) + 1/2, 0): coefficients accumulated in storage order over the first NV float4 of the site.
+template <bool HALF, int NV>
+__device__ __forceinline__ void site_color_n(const float4* __restrict__ sh, int k, const float (&b)[16],
+                                             float (&c)[3]) {
+    c[0] = c[1] = c[2] = 0.5f;
+    if (HALF) {
+        const float4* s = sh + 6 * static_cast<int64_t>(k);
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const float4 f = s[q];
+            const float fw[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 p = cutoffs(fw[u]);
+                const int i0 = 8 * q + 2 * u, i1 = i0 + 1;
+                c[i0 % 3] += b[i0 / 3] * p.x;
+                c[i1 % 3] += b[i1 / 3] * p.y;
+            }
+        }
+    } else {
+        const float4* s = sh + 12 * static_cast<int64_t>(k);
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const float4 f = s[q];
+            const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) c[(4 * q + u) % 3] += b[(4 * q + u) / 3] * fv[u];
+        }
+    }
+    c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
+}
+
+// Only the float4 holding coefficients of degree <= sh_deg are read (the others are multiplied by a zero
+// basis value, so skipping them leaves every finite result unchanged).
+template <bool HALF>
+__device__ __forceinline__ void site_color(const FoamScene& S, int deg, int k, const float (&b)[16], float (&c)[3]) {
+    if (HALF) {
+        switch (deg) {
+            case 0: site_color_n<true, sh_vec4_f16(0)>(S.sh, k, b, c); break;
+            case 1: site_color_n<true, sh_vec4_f16(1)>(S.sh, k, b, c); break;
+            case 2: site_color_n<true, sh_vec4_f16(2)>(S.sh, k, b, c); break;
+            default: site_color_n<true, sh_vec4_f16(3)>(S.sh, k, b, c); break;
+        }
+    } else {
+        switch (deg) {
+            case 0: site_color_n<false, sh_vec4_f32(0)>(S.sh, k, b, c); break;
+            case 1: site_color_n<false, sh_vec4_f32(1)>(S.sh, k, b, c); break;
+            case 2: site_color_n<false, sh_vec4_f32(2)>(S.sh, k, b, c); break;
+            default: site_color_n<false, sh_vec4_f32(3)>(S.sh, k, b, c); break;
+        }
+    }
+}
+
+// Per-ray colour cache in LDS: slot k mod 8 of this lane's column holds (r, g, b, k).
+template <bool HALF>
+__device__ __forceinline__ void cached_color(const FoamScene& S, int deg, float4* cache, int k, const float (&b)[16],
+                                             float (&c)[3], int& n_sh) {
+    float4& e = cache[(k & (kCache - 1)) * kBlock];
+    const float4 v = e;
+    if (__float_as_int(v.w) == k) {
+        c[0] = v.x, c[1] = v.y, c[2] = v.z;
+        return;
+    }
+    site_color<HALF>(S, deg, k, b, c);
+    e = make_float4(c[0], c[1], c[2], __int_as_float(k));
+    ++n_sh;
+}
+
+// Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated.
+__device__ int walk_to(const FoamScene& S, int c, float x0, float x1, float x2, int& steps) {
+    for (int it = 0; it < kWalkCap; ++it) {
+        const float4 pc = S.points[c];
+        float bd = (x0 - pc.x) * (x0 - pc.x) + (x1 - pc.y) * (x1 - pc.y) + (x2 - pc.z) * (x2 - pc.z);
+        int bk = c;
+        const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+        for (int e = e0 + 1; e < e1; ++e) {
+            const float4 ed = S.edge[e];
+            const int k = S.nbr[e];
+            const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
+            const float dk = v0 * v0 + v1 * v1 + v2 * v2;
+            if (dk < bd || (dk == bd && before(S, k, bk))) bd = dk, bk = k;
+        }
+        if (bk == c) break;
+        c = bk;
+        ++steps;
+    }
+    return c;
+}
+
+// Result of one pass over a cell's neighbourhood for one sample.
+struct CellEval {
+    float sigma, mmin, t_exit;
+    int next;
+    Blend B;
+};
+
+// One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
+// Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
+template <int STAGE, int COLOR, bool HALF>
+__device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
+                          const float (&d)[3], const float (&b)[16], float4* cache, bool want_exit, CellEval& R,
+                          int& n_dens, int& n_sh) {
+    constexpr bool BLEND = COLOR != kLazy;
+    const float4 pc = S.points[c];
+    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
+    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
+    blend_init(R.B);
+    for (int e = e0; e < e1; ++e) {
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+        if (want_exit && e > e0) {
+            const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
+            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+            if (dn > 0.f) {
+                const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
+                            m2 = 0.5f * (ed.z + pc.z) - o[2];
+                const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
+                if (tt < R.t_exit || (tt == R.t_exit && (R.next == INT_MAX || before(S, k, R.next))))
+                    R.t_exit = tt, R.next = k;
+            }
+        }
+        if (STAGE >= 1) {
+            const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
+            const float r2 = v0 * v0 + v1 * v1 + v2 * v2;
+            const float2 cut = cutoffs(ed.w);
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+            if (r2 <= cut.x) {
+                const float4 q0 = a[0], q1 = a[1];
+                R.sigma += fexp(q1.z - 0.5f * maha(q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, v0, v1, v2));
+                ++n_dens;
+            }
+            if (STAGE >= 2) {
+                const float lb = r2 * cut.y;
+                if (BLEND ? lb <= R.B.m + P.color_cut : lb < R.mmin) {
+                    const float4 q2 = a[2], q3 = a[3];
+                    const float m = maha(q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, v0, v1, v2);
+                    if (BLEND) {
+                        if (m <= R.B.m + P.color_cut) {
+                            float c3[3];
+                            if (COLOR == kBaked) {
+                                const float4 q4 = a[4];
+                                c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
+                            } else {
+                                cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
+                            }
+                            blend_add(R.B, m, c3[0], c3[1], c3[2]);
+                        }
+                    } else {
+                        R.mmin = fminf(R.mmin, m);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin.
+template <bool HALF>
+__device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
+                           const float (&d)[3], const float (&b)[16], float4* cache, float (&C)[3], int& n_sh) {
+    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
+    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    const float cut = mmin + P.color_cut;
+    float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
+    for (int e = e0; e < e1; ++e) {
+        const float4 ed = S.edge[e];
+        const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
+        if ((v0 * v0 + v1 * v1 + v2 * v2) * cutoffs(ed.w).y > cut) continue;
+        const int k = S.nbr[e];
+        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+        const float4 q2 = a[2], q3 = a[3];
+        const float m = maha(q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, v0, v1, v2);
+        if (m > cut) continue;
+        const float w = fexp(-0.5f * (m - mmin));
+        float c3[3];
+        cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
+        A += w, r += w * c3[0], g += w * c3[1], bl += w * c3[2];
+    }
+    const float inv = 1.f / A;
+    C[0] = r * inv, C[1] = g * inv, C[2] = bl * inv;
+}
+
+template <bool TRACE>
+__device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O, int64_t r, int s, int c) {
+    if (TRACE && s < O.trace_cap) O.trace[r * O.trace_cap + s] = S.orig != nullptr ? S.orig[c] : c;
+}
+
+template <int STAGE, int COLOR, bool HALF, bool TRACE>
+__global__ void __launch_bounds__(kBlock)
+    foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
+    constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
+    constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
+    __shared__ float4 cache_lds[kSH ? kCache * kBlock : 1];
+    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
+    if (r >= R.n) return;
+    const int start = R.start[r];
+    if (start < 0 || start >= S.n_sites) {  // not traced: empty foreground
+        O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+        O.T[r] = 1.f, O.depth[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) O.stats[5 * r + i] = 0;
+        return;
+    }
+    float4* cache = cache_lds + (kSH ? threadIdx.x : 0);
+    if (kSH) {
+#pragma unroll
+        for (int i = 0; i < kCache; ++i) cache[i * kBlock] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+    }
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float t_near = R.t_near[r], t_far = R.t_far[r];
+    const int max_samples = R.cap != nullptr ? R.cap[r] : INT_MAX;
+    float b[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) b[i] = 0.f;
+    if (kSH) sh_basis(d[0], d[1], d[2], P.sh_deg, b);
+
+    int walk_steps = 0, n_dens = 0, n_sh = 0;
+    int c = walk_to(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
+    CellEval E;
+    eval_cell<STAGE, COLOR, HALF>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    trace_cell<TRACE>(S, O, r, 0, c);
+    float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
+    bool hasP = false;
+    int cP = c;
+    if (BLEND) {
+        const float inv = 1.f / E.B.a;
+        CP[0] = E.B.r * inv, CP[1] = E.B.g * inv, CP[2] = E.B.b * inv, hasP = true;
+    }
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    int n_samples = 1, n_color = 0;
+    for (int it = 0; it < kMaxCells; ++it) {
+        const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
+        const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
+        const int cQ = last ? c : E.next;
+        eval_cell<STAGE, COLOR, HALF>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        trace_cell<TRACE>(S, O, r, n_samples, cQ);
+        ++n_samples;
+        const float sQ = E.sigma, mQ = E.mmin;
+        const float delta = tQ - tP;
+        const float alpha = 1.f - fexp(-0.5f * (sP + sQ) * delta);
+        const float w = T * alpha;
+        float CQ[3] = {0.f, 0.f, 0.f};
+        bool hasQ = false;
+        if (BLEND) {
+            const float inv = 1.f / E.B.a;
+            CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv, hasQ = true;
+        }
+        if (STAGE >= 2 && w > P.w_thresh) {
+            if (!BLEND) {
+                if (!hasP) color_lazy<HALF>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
+                color_lazy<HALF>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                hasQ = true;
+            }
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (CP[a] + CQ[a]);
+            dep += w * 0.5f * (tP + tQ);
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        tP = tQ, sP = sQ, mP = mQ, hasP = hasQ, cP = cQ, c = cQ;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
+        if (last || T < P.t_thresh) break;
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
+    O.T[r] = T;
+    O.depth[r] = dep;
+    int* st = O.stats + 5 * r;
+    st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
+}
+
+template <int STAGE, int COLOR, bool HALF, bool TRACE>
+int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
+    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
+                       stream, S, P, R, O);
+    return launch_status("foam_infer_kernel");
+}
+
+template <bool TRACE>
+int dispatch(int stage, int color_mode, bool half, const FoamScene& S, const FoamParams& P, const FoamRays& R,
+             const FoamOut& O, hipStream_t stream) {
+    if (stage == 0) return launch<0, kLazy, false, TRACE>(S, P, R, O, stream);
+    if (stage == 1) return launch<1, kLazy, false, TRACE>(S, P, R, O, stream);
+    if (color_mode == kBaked) return launch<2, kBaked, false, TRACE>(S, P, R, O, stream);
+    if (color_mode == kLazy)
+        return half ? launch<2, kLazy, true, TRACE>(S, P, R, O, stream)
+                    : launch<2, kLazy, false, TRACE>(S, P, R, O, stream);
+    return half ? launch<2, kFused, true, TRACE>(S, P, R, O, stream)
+                : launch<2, kFused, false, TRACE>(S, P, R, O, stream);
+}
+
+int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr, const float* edge,
+               int64_t n_edges, const float* attr, const void* sh, int32_t sh_half, int64_t sh_deg, const float* o,
+               const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
+               double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
+               const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
+               int32_t* trace, int64_t trace_cap, void* stream) {
+    VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
+    VGR_REQUIRE(color_mode >= kLazy && color_mode <= kFused,
+                "color_mode must be 0 (lazy), 1 (baked) or 2 (fused)");
+    VGR_REQUIRE(stage >= 0 && stage <= 2, "stage must be 0, 1 or 2");
+    VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
+    if (n_rays == 0) return VGR_OK;
+    VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_infer: n_sites must be in [1, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_infer: n_edges must be in [N, 2^31) (got %lld)",
+                static_cast<long long>(n_edges));
+    VGR_REQUIRE(points && offsets && nbr && edge && attr, "foam_infer: null scene pointer");
+    VGR_REQUIRE(o && d && start && near_t && far_t, "foam_infer: null ray pointer");
+    VGR_REQUIRE(rgb && T && depth && stats, "foam_infer: null output pointer");
+    const bool needs_sh = stage == 2 && color_mode != kBaked;
+    VGR_REQUIRE(!needs_sh || sh != nullptr, "foam_infer: sh is required unless colors are baked");
+    const FoamScene S{reinterpret_cast<const float4*>(points),
+                      offsets,
+                      nbr,
+                      reinterpret_cast<const float4*>(edge),
+                      reinterpret_cast<const float4*>(attr),
+                      needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
+                      orig,
+                      static_cast<int>(n_sites)};
+    const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
+                       static_cast<int>(sh_deg)};
+    const FoamRays R{o, d, start, near_t, far_t, cap, n_rays};
+    const FoamOut O{rgb, T, depth, stats, trace, trace_cap};
+    const hipStream_t s = as_stream(stream);
+    if (trace != nullptr) return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, s);
+    return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, s);
+}
+
+}  // namespace
+}  // namespace vgr
+
+extern "C" int vgr_foam_infer(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                              const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
+                              int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                              const float* near_t, const float* far_t, int64_t n_rays, double t_thresh,
+                              double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
+                              const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth,
+                              int32_t* stats, void* stream) {
+    return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
+                           near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
+                           T, depth, stats, nullptr, 0, stream);
+}
+
+extern "C" int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* offsets,
+                                     const int32_t* nbr, const float* edge, int64_t n_edges, const float* attr,
+                                     const void* sh, int32_t sh_half, int64_t sh_deg, const float* o, const float* d,
+                                     const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
+                                     double t_thresh, double w_thresh, double color_cut, int64_t color_mode,
+                                     int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
+                                     float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                                     void* stream) {
+    VGR_REQUIRE(trace != nullptr && trace_cap > 0, "foam_infer_traced: trace must be non-null with trace_cap > 0");
+    return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
+                           near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
+                           T, depth, stats, trace, trace_cap, stream);
+}

@@ -1,0 +1,300 @@
+"""Operator boundary of the forward/inference path: the reference's ext.py API (ext.py:11-216) backed by the
+hand-written gfx950 kernels of libvgr.so instead of JIT-built CUDA extensions.
+
+Same names, argument meaning and error behaviour as the reference:
+  extension().walk / density_forward / color_forward / conic_forward       (csrc/vgf.cu:438-546)
+  march_extension().march_forward                                          (csrc/march.cu:383-403)
+  foam_infer_extension().foam_infer                                        (csrc/foam_infer.cu:376-435)
+  Graph, density, color, conic, conic_reference, march                     (ext.py:46-182)
+Inputs are checked like the reference's TORCH_CHECKs (CUDA, contiguous, dtype, shapes) and a violation raises
+RuntimeError; outputs are allocated here with torch on the input's device and the kernels run asynchronously on
+torch's current stream. Training (the backward kernels and the autograd replay) is not part of this build: the
+autograd wrappers evaluate the forward pass and raise if a gradient is requested."""
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_of
+
+
+def _check(x, name, dtype):
+	if not isinstance(x, torch.Tensor) or not x.is_cuda:
+		raise RuntimeError(f'{name} must be a CUDA tensor')
+	if not x.is_contiguous():
+		raise RuntimeError(f'{name} must be contiguous')
+	if x.dtype != dtype:
+		raise RuntimeError(f'{name} has the wrong dtype')
+
+
+def _require(cond, msg):
+	if not cond:
+		raise RuntimeError(msg)
+
+
+# ============================================================================ vgf.cu forward operators
+
+class _FieldExtension:
+	"""Forward operators of csrc/vgf.cu (walk, density_forward, color_forward, conic_forward)."""
+
+	@staticmethod
+	def walk(points, offsets, adj, o, d, z, start):
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (adj, 'adj', torch.int32), (o, 'o', torch.float32), (d, 'd', torch.float32),
+						 (z, 'z', torch.float32), (start, 'start', torch.int32)):
+			_check(t, n, dt)
+		B, S = z.size(0), z.size(1)
+		site = torch.empty(B, S, dtype=torch.int32, device=z.device)
+		steps = torch.empty(B, dtype=torch.int32, device=z.device)
+		if B == 0:
+			return [site, steps]
+		with torch.cuda.device(z.device):
+			call('vgr_walk', ptr(points), points.size(0), ptr(offsets), ptr(adj), adj.numel(), ptr(o), ptr(d),
+				 ptr(z), ptr(start), B, S, ptr(site), ptr(steps), stream_of(z.device))
+		return [site, steps]
+
+	@staticmethod
+	def density_forward(points, offsets, adj, raw, log_scale, quat, x, site, scale_mult):
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
+						 (quat, 'quat', torch.float32), (raw, 'raw', torch.float32), (x, 'x', torch.float32),
+						 (site, 'site', torch.int32)):
+			_check(t, n, dt)
+		m = x.size(0)
+		sigma = torch.empty(m, dtype=torch.float32, device=x.device)
+		if m == 0:
+			return sigma
+		with torch.cuda.device(x.device):
+			call('vgr_density_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+				 ptr(raw), ptr(log_scale), ptr(quat), ptr(x), ptr(site), m, float(scale_mult), ptr(sigma),
+				 stream_of(x.device))
+		return sigma
+
+	@staticmethod
+	def color_forward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site):
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
+						 (quat, 'quat', torch.float32), (sh, 'sh', torch.float32), (x, 'x', torch.float32),
+						 (dirs, 'dirs', torch.float32), (site, 'site', torch.int32)):
+			_check(t, n, dt)
+		_require(sh.dim() == 3 and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+		m = x.size(0)
+		rgb = torch.empty(m, 3, dtype=torch.float32, device=x.device)
+		if m == 0:
+			return rgb
+		with torch.cuda.device(x.device):
+			call('vgr_color_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+				 ptr(log_scale), ptr(quat), ptr(sh), int(sh_deg), ptr(x), ptr(dirs), ptr(site), m, ptr(rgb),
+				 stream_of(x.device))
+		return rgb
+
+	@staticmethod
+	def conic_forward(log_scale, quat, floor):
+		_check(log_scale, 'log_scale', torch.float32)
+		_check(quat, 'quat', torch.float32)
+		n = quat.size(0)
+		A = torch.empty(n, 6, dtype=torch.float32, device=quat.device)
+		if n == 0:
+			return A
+		with torch.cuda.device(quat.device):
+			call('vgr_conic_forward', ptr(log_scale), ptr(quat), n, float(floor), ptr(A), stream_of(quat.device))
+		return A
+
+
+# ============================================================================ march.cu forward
+
+class _MarchExtension:
+	@staticmethod
+	def march_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
+					  t_thresh, w_thresh, trace_cap=0):
+		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0)."""
+		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
+						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
+						  (d, 'd', torch.float32), (start, 'start', torch.int32), (near, 'near', torch.float32),
+						  (mid, 'mid', torch.float32), (far, 'far', torch.float32)):
+			_check(t, n, dtp)
+		_require(sh.dim() == 3 and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+		_require(dA.size(1) == 6 and cA.size(1) == 6, 'conics must be (N, 6)')
+		B = o.size(0)
+		dev = o.device
+		rgb = torch.empty(B, 3, dtype=torch.float32, device=dev)
+		T = torch.empty(B, dtype=torch.float32, device=dev)
+		depth = torch.empty(B, dtype=torch.float32, device=dev)
+		stats = torch.empty(B, 3, dtype=torch.int32, device=dev)
+		trace = torch.full((B, trace_cap), -1, dtype=torch.int32, device=dev) if trace_cap > 0 else None
+		out = [rgb, T, depth, stats] + ([trace] if trace is not None else [])
+		if B == 0:
+			return out
+		with torch.cuda.device(dev):
+			call('vgr_march_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+				 ptr(raw), ptr(dA), ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid),
+				 ptr(far), B, float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(depth),
+				 ptr(stats), ptr(trace), int(trace_cap), stream_of(dev))
+		return out
+
+
+# ============================================================================ foam_infer.cu
+
+class _FoamInferExtension:
+	@staticmethod
+	def foam_infer(points, offsets, nbr, edge, attr, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
+				   color_cut, color_mode, stage, cap, orig, trace_cap=0):
+		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 5) int32] (+ trace (B, trace_cap) int32, the cell of
+		every sample in original numbering, -1 past the last sample, when trace_cap > 0)."""
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32), (attr, 'attr', torch.float32),
+						 (o, 'o', torch.float32), (d, 'd', torch.float32), (start, 'start', torch.int32),
+						 (near, 'near', torch.float32), (far, 'far', torch.float32), (cap, 'cap', torch.int32),
+						 (orig, 'orig', torch.int32)):
+			_check(t, n, dt)
+		_require(isinstance(sh, torch.Tensor) and sh.is_cuda and sh.is_contiguous(),
+				 'sh must be a contiguous CUDA tensor')
+		half = sh.dtype == torch.float16
+		_require(half or sh.dtype == torch.float32, 'sh must be float32 or float16')
+		n = points.size(0)
+		_require(points.dim() == 2 and points.size(1) == 4, 'points must be (N, 4)')
+		_require(offsets.numel() == n + 1, 'offsets must be (N + 1)')
+		_require(edge.dim() == 2 and edge.size(1) == 4 and edge.size(0) == nbr.numel(), 'edge must be (E, 4)')
+		_require(attr.dim() == 2 and attr.size(1) == 20 and attr.size(0) == n, 'attr must be (N, 20)')
+		_require(0 <= color_mode <= 2, 'color_mode must be 0 (lazy), 1 (baked) or 2 (fused)')
+		baked = color_mode == 1
+		_require(baked or (sh.dim() == 3 and sh.size(0) == n and sh.size(1) == 16 and sh.size(2) == 3),
+				 'sh must be (N, 16, 3)')
+		_require(0 <= stage <= 2, 'stage must be 0, 1 or 2')
+		B = o.size(0)
+		dev = o.device
+		rgb = torch.empty(B, 3, dtype=torch.float32, device=dev)
+		T = torch.empty(B, dtype=torch.float32, device=dev)
+		depth = torch.empty(B, dtype=torch.float32, device=dev)
+		stats = torch.empty(B, 5, dtype=torch.int32, device=dev)
+		trace = torch.full((B, trace_cap), -1, dtype=torch.int32, device=dev) if trace_cap > 0 else None
+		out = [rgb, T, depth, stats] + ([trace] if trace is not None else [])
+		if B == 0:
+			return out
+		cp = cap if cap.numel() == B else None
+		og = orig if orig.numel() == n else None
+		args = [ptr(points), n, ptr(offsets), ptr(nbr), ptr(edge), nbr.numel(), ptr(attr),
+				None if baked else ptr(sh), int(half), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B,
+				float(t_thresh), float(w_thresh), float(color_cut), int(color_mode), int(stage), ptr(cp), ptr(og),
+				ptr(rgb), ptr(T), ptr(depth), ptr(stats)]
+		with torch.cuda.device(dev):
+			if trace is None:
+				call('vgr_foam_infer', *args, stream_of(dev))
+			else:
+				call('vgr_foam_infer_traced', *args, ptr(trace), int(trace_cap), stream_of(dev))
+		return out
+
+
+_FIELD, _MARCH, _FOAM_INFER = _FieldExtension(), _MarchExtension(), _FoamInferExtension()
+
+
+def extension():
+	"""vgf.cu forward operators (reference: ext.py:30-31)."""
+	_lib.load()
+	return _FIELD
+
+
+def march_extension():
+	"""march.cu forward (reference: ext.py:34-35)."""
+	_lib.load()
+	return _MARCH
+
+
+def foam_infer_extension():
+	"""foam_infer.cu (reference: ext.py:42-43)."""
+	_lib.load()
+	return _FOAM_INFER
+
+
+def foam_extension():
+	"""The training foam kernel (csrc/foam.cu, forward with records + backward) is not part of this build."""
+	raise NotImplementedError('the training renderer (foam.cu) is out of scope: use foam_infer_extension()')
+
+
+class Graph:
+	"""Fixed sites and their Delaunay adjacency (CSR, int32) on the GPU (ext.py:46-58)."""
+
+	def __init__(self, points, offsets, adj):
+		self.points = points.float().contiguous()
+		self.offsets = offsets.int().contiguous()
+		self.adj = adj.int().contiguous()
+
+	def walk(self, o, d, z, start):
+		"""Nearest site of every sample o + z d; z (B, S) sorted along each ray, start (B,) a site near o."""
+		site, steps = extension().walk(self.points, self.offsets, self.adj, o.float().contiguous(),
+									   d.float().contiguous(), z.float().contiguous(), start.int().contiguous())
+		return site, steps
+
+
+class _ForwardOnly(torch.autograd.Function):
+	"""Wraps a forward result so that parameters requiring gradients keep a graph edge whose backward raises:
+	the training kernels are out of scope."""
+
+	@staticmethod
+	def forward(ctx, out, *params):
+		return out.clone()
+
+	@staticmethod
+	def backward(ctx, *grads):
+		raise RuntimeError('backward of the voronoi-gauss field is out of scope of this build (forward/inference only)')
+
+
+def _forward_only(out, params):
+	if torch.is_grad_enabled() and any(isinstance(p, torch.Tensor) and p.requires_grad for p in params):
+		return _ForwardOnly.apply(out, *params)
+	return out
+
+
+def density(graph, raw, log_scale, quat, x, site, scale_mult=1.0):
+	"""sigma(x) = sum over the Voronoi neighborhood of site of exp(raw_k) G_k(x); scale_mult widens the
+	Gaussians (proposal passes). Reference: ext.py:78-87."""
+	x = x.detach().float().contiguous()
+	site = site.int().contiguous()
+	params = [p.contiguous() for p in (raw, log_scale, quat)]
+	out = extension().density_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params], x, site,
+									  float(scale_mult))
+	return out if scale_mult != 1.0 else _forward_only(out, params)
+
+
+def color(graph, log_scale, quat, sh, x, dirs, site, sh_deg=3):
+	"""C(x, d) = sum_k H_k(x) c_k(d) / sum_k H_k(x) over the Voronoi neighborhood of site; sh (N, 16, 3).
+	Reference: ext.py:108-117."""
+	x = x.detach().float().contiguous()
+	dirs = dirs.detach().float().contiguous()
+	site = site.int().contiguous()
+	params = [p.contiguous() for p in (log_scale, quat, sh)]
+	out = extension().color_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
+									int(sh_deg), x, dirs, site)
+	return _forward_only(out, params)
+
+
+def conic(log_scale, quat, floor=0.0):
+	"""(N, 6) inverse covariances (xx, xy, xz, yy, yz, zz) of R diag(s^2 + floor^2) R^T (ext.py:134-136)."""
+	params = [log_scale.contiguous(), quat.contiguous()]
+	out = extension().conic_forward(params[0].detach(), params[1].detach(), float(floor))
+	return _forward_only(out, params)
+
+
+def conic_reference(log_scale, quat, floor=0.0):
+	"""PyTorch version of conic (for tests), ext.py:139-149."""
+	q = quat / quat.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+	w, x, y, z = q.unbind(-1)
+	R = torch.stack([
+		1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+		2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+		2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1).view(-1, 3, 3)
+	inv_var = 1.0 / (torch.exp(2 * log_scale.clamp(-20, 20)) + floor * floor)
+	A = (R * inv_var[:, None, :]) @ R.transpose(1, 2).contiguous()
+	return torch.stack([A[:, 0, 0], A[:, 0, 1], A[:, 0, 2], A[:, 1, 1], A[:, 1, 2], A[:, 2, 2]], -1).contiguous()
+
+
+def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg, t_thresh=1e-4, w_thresh=1e-4):
+	"""Uniform-step fused rendering -> foreground rgb (B, 3) (without background), final transmittance (B,),
+	depth (B,), per-ray stats (B, 3) int: samples marched, samples with color, walk steps (ext.py:172-182)."""
+	rays = tuple(t.float().contiguous() for t in (o, d)) + (start.int().contiguous(),) + \
+		tuple(t.float().contiguous() for t in (near, mid, far))
+	params = [p.contiguous() for p in (raw, dA, cA, sh)]
+	rgb, T, depth, stats = march_extension().march_forward(graph.points, graph.offsets, graph.adj,
+														   *[p.detach() for p in params], int(sh_deg), *rays,
+														   float(dt), int(n_bg), float(t_thresh), float(w_thresh))
+	return _forward_only(rgb, params), _forward_only(T, params), depth, stats
