@@ -32,14 +32,18 @@ def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e
 	return res
 
 
-def compare(g, r, exact_trace=True, stats_frac=1.0, tol=TOL):
-	"""GPU outputs g against oracle outputs r."""
+def compare(g, r, exact_trace=True, stats_frac=1.0, tol=TOL, w_thresh=1e-4, t_max=4.0):
+	"""GPU outputs g against oracle outputs r. rgb and T: within `tol` on every ray. Per-ray statistics equal on
+	at least stats_frac of the rays; the others are rays where a threshold test (w > w_thresh or T < t_thresh) saw
+	a value within a few ulps of the threshold, since exp differs by ulps between the CPU and the GPU. On those
+	rays a segment of weight ~w_thresh at t <= t_max is in or out, so depth may move by w_thresh * t_max."""
 	assert np.isfinite(g['rgb']).all() and np.isfinite(g['T']).all()
 	np.testing.assert_allclose(g['rgb'], r['rgb'], atol=tol, rtol=0)
 	np.testing.assert_allclose(g['T'], r['T'], atol=tol, rtol=0)
-	np.testing.assert_allclose(g['depth'], r['depth'], atol=tol * max(1.0, float(np.abs(r['depth']).max())), rtol=0)
 	same = (g['stats'] == r['stats']).all(1)
 	assert same.mean() >= stats_frac, f'stats equal on {same.mean():.4f} of rays'
+	np.testing.assert_allclose(g['depth'][same], r['depth'][same], atol=tol, rtol=tol)
+	np.testing.assert_allclose(g['depth'][~same], r['depth'][~same], atol=tol + w_thresh * t_max, rtol=tol)
 	if g['trace'] is not None:
 		if exact_trace:
 			np.testing.assert_array_equal(g['trace'], r['trace'])
@@ -78,7 +82,7 @@ def test_small_field_stages_thresholds_off(gpu, small, stage):
 def test_small_field_modes(gpu, small, color_mode, sh_half, reorder):
 	f, (o, d, start, near, _, far) = small
 	pk = f.pack(sh_half=sh_half, reorder=reorder)
-	st = pk['inv'][start] if reorder else start
+	st = pk['inv'][start].astype(np.int32) if reorder else start
 	g = gpu_foam(gpu, pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
 	r = oracle.foam_infer(pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
 	compare(g, r, exact_trace=False, stats_frac=0.98)
@@ -121,7 +125,7 @@ def test_benchmark_scenes_vs_oracle(gpu, config, scale, img):
 	model, pk = scene_pack(sc, reorder=config % 2 == 0)
 	o, d, start, _ = sc.camera_rays(tile=8)
 	near, _, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
-	st = pk['inv'][start] if pk['inv'] is not None else start
+	st = pk['inv'][start].astype(np.int32) if pk['inv'] is not None else start
 	if len(o) > 60000:  # the oracle checks a deterministic subset; the GPU renders the same subset
 		sel = np.arange(0, len(o), len(o) // 60000 + 1)
 		o, d, st, near, far = o[sel], d[sel], st[sel], near[sel], far[sel]
@@ -158,7 +162,7 @@ def test_render_rays_foam_infer_api(gpu, small):
 		pack = render.pack_foam(model, reorder=reorder)
 		out = render.render_rays_foam_infer(model, pack, T(o), T(d), T(start), far_radius=2.0, trace_cap=512)
 		pk = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in pack.items()}
-		st = pk['inv'][start] if reorder else start
+		st = pk['inv'][start].astype(np.int32) if reorder else start
 		r = oracle.foam_infer(pk, 3, o, d, st, near, far, trace_cap=512)
 		np.testing.assert_allclose(out['rgb'].cpu().numpy(), r['rgb'] + r['T'][:, None] * 0.5, atol=TOL)
 		np.testing.assert_allclose(out['acc'].cpu().numpy(), 1 - r['T'], atol=TOL)
