@@ -16,6 +16,14 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-4  # absolute, fp32 rgb / T / depth (north-star parity bar)
 
 
+def ref_foam(*args, **kw):
+	"""The oracle with its per-ray colour cache off: the HIP kernel caches SH coefficient blocks per wave instead
+	of colours per ray and evaluates the SH polynomial at every colour lookup, so its SH-evaluation counter
+	(stats[:, 4]) equals the oracle's count without a colour cache; colours are identical either way."""
+	kw.setdefault('use_cache', False)
+	return oracle.foam_infer(*args, **kw)
+
+
 def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, color_cut=math.inf,
 			 color_mode=0, stage=2, cap=None, trace_cap=0):
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)  # noqa: E731
@@ -72,7 +80,7 @@ def test_small_field_stages_thresholds_off(gpu, small, stage):
 	f, (o, d, start, near, _, far) = small
 	pk = f.pack()
 	g = gpu_foam(gpu, pk, 3, o, d, start, near, far, 0.0, -1.0, stage=stage, trace_cap=512)
-	r = oracle.foam_infer(pk, 3, o, d, start, near, far, 0.0, -1.0, stage=stage, trace_cap=512)
+	r = ref_foam(pk, 3, o, d, start, near, far, 0.0, -1.0, stage=stage, trace_cap=512)
 	compare(g, r)
 
 
@@ -84,7 +92,7 @@ def test_small_field_modes(gpu, small, color_mode, sh_half, reorder):
 	pk = f.pack(sh_half=sh_half, reorder=reorder)
 	st = pk['inv'][start].astype(np.int32) if reorder else start
 	g = gpu_foam(gpu, pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
-	r = oracle.foam_infer(pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
+	r = ref_foam(pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
 	compare(g, r, exact_trace=False, stats_frac=0.98)
 
 
@@ -99,11 +107,11 @@ def test_small_field_baked_eps_and_cap(gpu, small):
 	cut = 2 * math.log(1 / 1e-3)
 	for mode in (1, 2, 0):
 		g = gpu_foam(gpu, pk, 3, o, d, start, near, far, color_cut=cut, color_mode=mode, trace_cap=512)
-		r = oracle.foam_infer(pk, 3, o, d, start, near, far, color_cut=cut, color_mode=mode, trace_cap=512)
+		r = ref_foam(pk, 3, o, d, start, near, far, color_cut=cut, color_mode=mode, trace_cap=512)
 		compare(g, r, exact_trace=False, stats_frac=0.98)
 	cap = np.maximum(2, r['stats'][:, 0] // 2).astype(np.int32)
 	g = gpu_foam(gpu, pk, 3, o, d, start, near, far, stage=0, cap=cap, trace_cap=512)
-	r = oracle.foam_infer(pk, 3, o, d, start, near, far, stage=0, cap=cap, trace_cap=512)
+	r = ref_foam(pk, 3, o, d, start, near, far, stage=0, cap=cap, trace_cap=512)
 	compare(g, r)
 	np.testing.assert_array_equal(g['stats'][:, 0], cap)
 
@@ -130,7 +138,7 @@ def test_benchmark_scenes_vs_oracle(gpu, config, scale, img):
 		sel = np.arange(0, len(o), len(o) // 60000 + 1)
 		o, d, st, near, far = o[sel], d[sel], st[sel], near[sel], far[sel]
 	g = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, trace_cap=256)
-	r = oracle.foam_infer(pk, sc.sh_deg, o, d, st, near, far, trace_cap=256)
+	r = ref_foam(pk, sc.sh_deg, o, d, st, near, far, trace_cap=256)
 	compare(g, r, exact_trace=False, stats_frac=0.99)
 	assert psnr(g['rgb'], r['rgb']) >= 60.0
 
@@ -142,10 +150,10 @@ def test_random_ray_batch_config5(gpu):
 	o, d, start, _ = sc.camera_rays()
 	near, _, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
 	g = gpu_foam(gpu, pk, 3, o, d, start, near, far, trace_cap=1024)
-	r = oracle.foam_infer(pk, 3, o, d, start, near, far, trace_cap=1024)
+	r = ref_foam(pk, 3, o, d, start, near, far, trace_cap=1024)
 	compare(g, r, exact_trace=False, stats_frac=0.99)
 	g0 = gpu_foam(gpu, pk, 3, o, d, start, near, far, stage=0, trace_cap=1024)
-	r0 = oracle.foam_infer(pk, 3, o, d, start, near, far, stage=0, trace_cap=1024)
+	r0 = ref_foam(pk, 3, o, d, start, near, far, stage=0, trace_cap=1024)
 	compare(g0, r0)
 
 
@@ -163,7 +171,7 @@ def test_render_rays_foam_infer_api(gpu, small):
 		out = render.render_rays_foam_infer(model, pack, T(o), T(d), T(start), far_radius=2.0, trace_cap=512)
 		pk = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in pack.items()}
 		st = pk['inv'][start].astype(np.int32) if reorder else start
-		r = oracle.foam_infer(pk, 3, o, d, st, near, far, trace_cap=512)
+		r = ref_foam(pk, 3, o, d, st, near, far, trace_cap=512)
 		np.testing.assert_allclose(out['rgb'].cpu().numpy(), r['rgb'] + r['T'][:, None] * 0.5, atol=TOL)
 		np.testing.assert_allclose(out['acc'].cpu().numpy(), 1 - r['T'], atol=TOL)
 
@@ -187,5 +195,5 @@ def test_errors_and_empty(gpu, small):
 	bad[:4] = [-1, f.n, 2 ** 30, -7]
 	g = gpu_foam(gpu, pk, 3, o, d, bad, near, far)
 	assert (g['T'][:4] == 1).all() and (g['rgb'][:4] == 0).all() and (g['stats'][:4] == 0).all()
-	r = oracle.foam_infer(pk, 3, o[4:], d[4:], start[4:], near[4:], far[4:])
+	r = ref_foam(pk, 3, o[4:], d[4:], start[4:], near[4:], far[4:])
 	np.testing.assert_allclose(g['rgb'][4:], r['rgb'], atol=TOL)

@@ -54,21 +54,23 @@ struct FoamOut {
     int64_t trace_cap;
 };
 
+// Tuning knobs (compile-time): VGR_CONTRACT lets the density / colour arithmetic contract into FMA (the
+// traversal arithmetic never does); VGR_PIPE is the software-pipelining depth of the neighbourhood loops
+// (0: none, 1: edge record of e + 1 in flight while e is computed, 2: edge records two ahead and the site
+// records of e + 1 in flight).
+#ifndef VGR_CONTRACT
+#define VGR_CONTRACT 1
+#endif
+#ifndef VGR_PIPE
+#define VGR_PIPE 2
+#endif
+
 // Running normalised colour blend (fused / baked modes).
 struct Blend {
     float m, a, r, g, b;
 };
 
 __device__ __forceinline__ void blend_init(Blend& B) { B.m = kInf, B.a = B.r = B.g = B.b = 0.f; }
-
-__device__ __forceinline__ void blend_add(Blend& B, float m, float r, float g, float b) {
-    if (m < B.m) {
-        const float s = fexp(-0.5f * (B.m - m));
-        B.a *= s, B.r *= s, B.g *= s, B.b *= s, B.m = m;
-    }
-    const float w = fexp(-0.5f * (m - B.m));
-    B.a += w, B.r += w * r, B.g += w * g, B.b += w * b;
-}
 
 // k precedes j in the tie-breaking order: the smaller original index.
 __device__ __forceinline__ bool before(const FoamScene& S, int k, int j) {
@@ -83,37 +85,81 @@ __device__ __forceinline__ float2 cutoffs(float w) {
     return make_float2(static_cast<float>(lo), static_cast<float>(hi));
 }
 
-// max(SH_k(d) + 1/2, 0): coefficients accumulated in storage order over the first NV float4 of the site.
+// ------------------------------------------------------------------ field arithmetic (may contract to FMA)
+#if VGR_CONTRACT
+#pragma clang fp contract(fast)
+#endif
+
+__device__ __forceinline__ void blend_add(Blend& B, float m, float r, float g, float b) {
+    if (m < B.m) {
+        const float s = fexp(-0.5f * (B.m - m));
+        B.a *= s, B.r *= s, B.g *= s, B.b *= s, B.m = m;
+    }
+    const float w = fexp(-0.5f * (m - B.m));
+    B.a += w, B.r += w * r, B.g += w * g, B.b += w * b;
+}
+
+__device__ __forceinline__ float maha_f(const float4& p, const float4& q, float vx, float vy, float vz) {
+    return p.x * vx * vx + p.w * vy * vy + q.y * vz * vz + 2.f * (p.y * vx * vy + p.z * vx * vz + q.x * vy * vz);
+}
+
+// Sample point o + t d, used by the field terms only (the traversal never reads it).
+__device__ __forceinline__ void sample_point(const float (&o)[3], const float (&d)[3], float t, float (&x)[3]) {
+    x[0] = o[0] + t * d[0], x[1] = o[1] + t * d[1], x[2] = o[2] + t * d[2];
+}
+
+__device__ __forceinline__ void offset_of(const float (&x)[3], const float4& p, float& v0, float& v1, float& v2,
+                                          float& r2) {
+    v0 = x[0] - p.x, v1 = x[1] - p.y, v2 = x[2] - p.z;
+    r2 = v0 * v0 + v1 * v1 + v2 * v2;
+}
+
+// rho_k G_k(x) from the density record (q0 = xx xy xz yy, q1 = yz zz min(raw, 30) 0).
+__device__ __forceinline__ float density_term(const float4& q0, const float4& q1, float v0, float v1, float v2) {
+    return fexp(q1.z - 0.5f * maha_f(q0, q1, v0, v1, v2));
+}
+
+__device__ __forceinline__ float weight_of(float m, float mmin) { return fexp(-0.5f * (m - mmin)); }
+
+__device__ __forceinline__ void accumulate(float& A, float& r, float& g, float& bl, float w, const float (&c)[3]) {
+    A += w, r += w * c[0], g += w * c[1], bl += w * c[2];
+}
+
+// max(SH_k(d) + 1/2, 0) from the first NV float4 of a site's coefficients, accumulated in storage order.
 template <bool HALF, int NV>
-__device__ __forceinline__ void site_color_n(const float4* __restrict__ sh, int k, const float (&b)[16],
-                                             float (&c)[3]) {
+__device__ __forceinline__ void sh_color_from(const float4 (&f)[NV], const float (&b)[16], float (&c)[3]) {
     c[0] = c[1] = c[2] = 0.5f;
-    if (HALF) {
-        const float4* s = sh + 6 * static_cast<int64_t>(k);
 #pragma unroll
-        for (int q = 0; q < NV; ++q) {
-            const float4 f = s[q];
-            const float fw[4] = {f.x, f.y, f.z, f.w};
+    for (int q = 0; q < NV; ++q) {
+        const float fv[4] = {f[q].x, f[q].y, f[q].z, f[q].w};
+        if (HALF) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const float2 p = cutoffs(fw[u]);
+                const float2 p = cutoffs(fv[u]);
                 const int i0 = 8 * q + 2 * u, i1 = i0 + 1;
                 c[i0 % 3] += b[i0 / 3] * p.x;
                 c[i1 % 3] += b[i1 / 3] * p.y;
             }
-        }
-    } else {
-        const float4* s = sh + 12 * static_cast<int64_t>(k);
-#pragma unroll
-        for (int q = 0; q < NV; ++q) {
-            const float4 f = s[q];
-            const float fv[4] = {f.x, f.y, f.z, f.w};
+        } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) c[(4 * q + u) % 3] += b[(4 * q + u) / 3] * fv[u];
         }
     }
     c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
 }
+
+template <bool HALF, int NV>
+__device__ __forceinline__ void site_color_n(const float4* __restrict__ sh, int k, const float (&b)[16],
+                                             float (&c)[3]) {
+    const float4* s = sh + (HALF ? 6 : 12) * static_cast<int64_t>(k);
+    float4 f[NV];
+#pragma unroll
+    for (int q = 0; q < NV; ++q) f[q] = s[q];
+    sh_color_from<HALF, NV>(f, b, c);
+}
+
+#pragma clang fp contract(off)
+// ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
 // Only the float4 holding coefficients of degree <= sh_deg are read (the others are multiplied by a zero
 // basis value, so skipping them leaves every finite result unchanged).
@@ -136,11 +182,97 @@ __device__ __forceinline__ void site_color(const FoamScene& S, int deg, int k, c
     }
 }
 
-// Per-ray colour cache in LDS: slot k mod 8 of this lane's column holds (r, g, b, k).
+// Colour of site k for this ray, through one of two LDS caches (VGR_SHCACHE):
+//  0  per-lane cache of site colours (r, g, b, k), 8 direct-mapped slots per lane (k mod 8);
+//  1  wave-shared cache of SH coefficient blocks, kSlots direct-mapped slots (k mod kSlots): the 64 rays of a
+//     tile read mostly the same sites, so a block is fetched from memory once per wave and every other lane
+//     reads it from LDS; the colour itself is evaluated per lane (it depends on the ray direction).
+// Both give the colour max(SH_k(d) + 1/2, 0) bit for bit; n_sh counts the SH evaluations performed.
+#ifndef VGR_SHCACHE
+#define VGR_SHCACHE 1
+#endif
+constexpr int kSlots = 64;
+
+struct ColorCache {
+    float4* col;          // lane cache: this lane's column, slots kBlock apart
+    float4* data;         // wave cache: [12][kSlots] float4 coefficient blocks
+    volatile int* tag;    // wave cache: site held by each slot (-1: empty)
+    volatile int* claim;  // wave cache: lane elected to fill each slot
+};
+
+// LDS footprint per block of the colour cache, in float4 units (the tag and claim arrays follow the data).
+constexpr int cache_vec4(bool sh) { return !sh ? 1 : VGR_SHCACHE ? 12 * kSlots + 2 * kSlots / 4 : kCache * kBlock; }
+
+__device__ __forceinline__ ColorCache make_cache(float4* lds) {
+    ColorCache C;
+    C.col = lds + threadIdx.x;
+    C.data = lds;
+    C.tag = reinterpret_cast<volatile int*>(lds + 12 * kSlots);
+    C.claim = C.tag + kSlots;
+#if VGR_SHCACHE
+    for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
+#else
+#pragma unroll
+    for (int i = 0; i < kCache; ++i) C.col[i * kBlock] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+#endif
+    __syncthreads();
+    return C;
+}
+
+template <bool HALF, int NV>
+__device__ __forceinline__ void wave_color_n(ColorCache& C, const float4* __restrict__ sh, int k, const float (&b)[16],
+                                             float (&c)[3]) {
+    const int slot = k & (kSlots - 1);
+    const float4* src = sh + (HALF ? 6 : 12) * static_cast<int64_t>(k);
+    float4 f[NV];
+    bool have = false;
+    if (C.tag[slot] != k) {  // miss: one lane per slot fetches its block and publishes it
+        const int lane = static_cast<int>(threadIdx.x);
+        C.claim[slot] = lane;
+        if (C.claim[slot] == lane) {
+#pragma unroll
+            for (int q = 0; q < NV; ++q) f[q] = src[q];
+#pragma unroll
+            for (int q = 0; q < NV; ++q) C.data[q * kSlots + slot] = f[q];
+            C.tag[slot] = k;
+            have = true;
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the LDS reads below after the publication above
+    if (!have) {
+        if (C.tag[slot] == k) {
+#pragma unroll
+            for (int q = 0; q < NV; ++q) f[q] = C.data[q * kSlots + slot];
+        } else {  // the slot went to another site this round: read from memory
+#pragma unroll
+            for (int q = 0; q < NV; ++q) f[q] = src[q];
+        }
+    }
+    sh_color_from<HALF, NV>(f, b, c);
+}
+
 template <bool HALF>
-__device__ __forceinline__ void cached_color(const FoamScene& S, int deg, float4* cache, int k, const float (&b)[16],
+__device__ __forceinline__ void cached_color(const FoamScene& S, int deg, ColorCache& C, int k, const float (&b)[16],
                                              float (&c)[3], int& n_sh) {
-    float4& e = cache[(k & (kCache - 1)) * kBlock];
+#if VGR_SHCACHE
+    ++n_sh;
+    if (HALF) {
+        switch (deg) {
+            case 0: wave_color_n<true, sh_vec4_f16(0)>(C, S.sh, k, b, c); break;
+            case 1: wave_color_n<true, sh_vec4_f16(1)>(C, S.sh, k, b, c); break;
+            case 2: wave_color_n<true, sh_vec4_f16(2)>(C, S.sh, k, b, c); break;
+            default: wave_color_n<true, sh_vec4_f16(3)>(C, S.sh, k, b, c); break;
+        }
+    } else {
+        switch (deg) {
+            case 0: wave_color_n<false, sh_vec4_f32(0)>(C, S.sh, k, b, c); break;
+            case 1: wave_color_n<false, sh_vec4_f32(1)>(C, S.sh, k, b, c); break;
+            case 2: wave_color_n<false, sh_vec4_f32(2)>(C, S.sh, k, b, c); break;
+            default: wave_color_n<false, sh_vec4_f32(3)>(C, S.sh, k, b, c); break;
+        }
+    }
+#else
+    float4& e = C.col[(k & (kCache - 1)) * kBlock];
     const float4 v = e;
     if (__float_as_int(v.w) == k) {
         c[0] = v.x, c[1] = v.y, c[2] = v.z;
@@ -149,6 +281,7 @@ __device__ __forceinline__ void cached_color(const FoamScene& S, int deg, float4
     site_color<HALF>(S, deg, k, b, c);
     e = make_float4(c[0], c[1], c[2], __int_as_float(k));
     ++n_sh;
+#endif
 }
 
 // Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated.
@@ -179,88 +312,158 @@ struct CellEval {
     Blend B;
 };
 
-// One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
-// Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
+// Exit-face candidate of edge (c -> k): bisector-plane parameter ahead of the ray, reference arithmetic.
+__device__ __forceinline__ void exit_candidate(const FoamScene& S, const float4& pc, const float4& ed, int k,
+                                               const float (&o)[3], const float (&d)[3], CellEval& R) {
+    const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
+    const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+    if (dn > 0.f) {
+        const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
+                    m2 = 0.5f * (ed.z + pc.z) - o[2];
+        const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
+        if (tt < R.t_exit || (tt == R.t_exit && (R.next == INT_MAX || before(S, k, R.next)))) R.t_exit = tt, R.next = k;
+    }
+}
+
+// Field terms of neighbour k (edge record ed, site records q0..q3) for the sample x.
 template <int STAGE, int COLOR, bool HALF>
-__device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
-                          const float (&d)[3], const float (&b)[16], float4* cache, bool want_exit, CellEval& R,
-                          int& n_dens, int& n_sh) {
+__device__ __forceinline__ void field_terms(const FoamScene& S, const FoamParams& P, const float (&x)[3],
+                                            const float4& ed, int k, const float4& q0, const float4& q1,
+                                            const float4& q2, const float4& q3, const float (&b)[16], ColorCache& cache,
+                                            CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = COLOR != kLazy;
-    const float4 pc = S.points[c];
-    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
-    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
-    R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
-    blend_init(R.B);
-    for (int e = e0; e < e1; ++e) {
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
-        if (want_exit && e > e0) {
-            const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
-            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
-            if (dn > 0.f) {
-                const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
-                            m2 = 0.5f * (ed.z + pc.z) - o[2];
-                const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
-                if (tt < R.t_exit || (tt == R.t_exit && (R.next == INT_MAX || before(S, k, R.next))))
-                    R.t_exit = tt, R.next = k;
-            }
-        }
-        if (STAGE >= 1) {
-            const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
-            const float r2 = v0 * v0 + v1 * v1 + v2 * v2;
-            const float2 cut = cutoffs(ed.w);
-            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-            if (r2 <= cut.x) {
-                const float4 q0 = a[0], q1 = a[1];
-                R.sigma += fexp(q1.z - 0.5f * maha(q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, v0, v1, v2));
-                ++n_dens;
-            }
-            if (STAGE >= 2) {
-                const float lb = r2 * cut.y;
-                if (BLEND ? lb <= R.B.m + P.color_cut : lb < R.mmin) {
-                    const float4 q2 = a[2], q3 = a[3];
-                    const float m = maha(q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, v0, v1, v2);
-                    if (BLEND) {
-                        if (m <= R.B.m + P.color_cut) {
-                            float c3[3];
-                            if (COLOR == kBaked) {
-                                const float4 q4 = a[4];
-                                c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
-                            } else {
-                                cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
-                            }
-                            blend_add(R.B, m, c3[0], c3[1], c3[2]);
-                        }
+    float v0, v1, v2, r2;
+    offset_of(x, ed, v0, v1, v2, r2);
+    const float2 cut = cutoffs(ed.w);
+    if (r2 <= cut.x) {
+        R.sigma += density_term(q0, q1, v0, v1, v2);
+        ++n_dens;
+    }
+    if (STAGE >= 2) {
+        const float lb = r2 * cut.y;
+        if (BLEND ? lb <= R.B.m + P.color_cut : lb < R.mmin) {
+            const float m = maha_f(q2, q3, v0, v1, v2);
+            if (BLEND) {
+                if (m <= R.B.m + P.color_cut) {
+                    float c3[3];
+                    if (COLOR == kBaked) {
+                        const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
+                        c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
                     } else {
-                        R.mmin = fminf(R.mmin, m);
+                        cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
                     }
+                    blend_add(R.B, m, c3[0], c3[1], c3[2]);
                 }
+            } else {
+                R.mmin = fminf(R.mmin, m);
             }
         }
     }
 }
 
+// One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
+// Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
+// The loop is software-pipelined (VGR_PIPE): the edge records and site records of the next edges are loaded
+// while the current one is evaluated (indices clamped to the cell, so every load stays in bounds).
+template <int STAGE, int COLOR, bool HALF>
+__device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
+                          const float (&d)[3], const float (&b)[16], ColorCache& cache, bool want_exit, CellEval& R,
+                          int& n_dens, int& n_sh) {
+    const float4 pc = S.points[c];
+    float x[3];
+    sample_point(o, d, t, x);
+    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    const int last = e1 - 1;
+    R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
+    blend_init(R.B);
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#if VGR_PIPE == 0
+    for (int e = e0; e < e1; ++e) {
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+        if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
+        if (STAGE >= 1) {
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+            const float4 q0 = a[0], q1 = a[1];
+            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
+            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
+        }
+    }
+#else
+    float4 ed = S.edge[e0];
+    int k = S.nbr[e0];
+#if VGR_PIPE >= 2
+    float4 ed1 = S.edge[min(e0 + 1, last)];
+    int k1 = S.nbr[min(e0 + 1, last)];
+    float4 q0 = zero4, q1 = zero4, q2 = zero4, q3 = zero4;
+    if (STAGE >= 1) {
+        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+        q0 = a[0], q1 = a[1];
+        if (STAGE >= 2) q2 = a[2], q3 = a[3];
+    }
+#endif
+    for (int e = e0; e < e1; ++e) {
+#if VGR_PIPE >= 2
+        // in flight while edge e is evaluated: site records of e + 1, edge records of e + 2
+        const int e2 = min(e + 2, last);
+        const float4 ed2 = S.edge[e2];
+        const int k2 = S.nbr[e2];
+        float4 n0 = zero4, n1 = zero4, n2 = zero4, n3 = zero4;
+        if (STAGE >= 1) {
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
+            n0 = a[0], n1 = a[1];
+            if (STAGE >= 2) n2 = a[2], n3 = a[3];
+        }
+        if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
+        if (STAGE >= 1) field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
+        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
+        q0 = n0, q1 = n1, q2 = n2, q3 = n3;
+#else
+        const int e1n = min(e + 1, last);
+        const float4 edn = S.edge[e1n];
+        const int kn = S.nbr[e1n];
+        if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
+        if (STAGE >= 1) {
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+            const float4 q0 = a[0], q1 = a[1];
+            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
+            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
+        }
+        ed = edn, k = kn;
+#endif
+    }
+#endif
+}
+
 // Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin.
 template <bool HALF>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
-                           const float (&d)[3], const float (&b)[16], float4* cache, float (&C)[3], int& n_sh) {
-    const float x0 = o[0] + t * d[0], x1 = o[1] + t * d[1], x2 = o[2] + t * d[2];
+                           const float (&d)[3], const float (&b)[16], ColorCache& cache, float (&C)[3], int& n_sh) {
+    float x[3];
+    sample_point(o, d, t, x);
     const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    const int last = e1 - 1;
     const float cut = mmin + P.color_cut;
     float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
+    float4 ed = S.edge[e0];
+    int k = S.nbr[e0];
     for (int e = e0; e < e1; ++e) {
-        const float4 ed = S.edge[e];
-        const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
-        if ((v0 * v0 + v1 * v1 + v2 * v2) * cutoffs(ed.w).y > cut) continue;
-        const int k = S.nbr[e];
+        const int en = min(e + 1, last);
+        const float4 edn = S.edge[en];
+        const int kn = S.nbr[en];
         const float4* a = S.attr + 5 * static_cast<int64_t>(k);
         const float4 q2 = a[2], q3 = a[3];
-        const float m = maha(q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, v0, v1, v2);
-        if (m > cut) continue;
-        const float w = fexp(-0.5f * (m - mmin));
-        float c3[3];
-        cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
-        A += w, r += w * c3[0], g += w * c3[1], bl += w * c3[2];
+        float v0, v1, v2, r2;
+        offset_of(x, ed, v0, v1, v2, r2);
+        if (r2 * cutoffs(ed.w).y <= cut) {
+            const float m = maha_f(q2, q3, v0, v1, v2);
+            if (m <= cut) {
+                float c3[3];
+                cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
+                accumulate(A, r, g, bl, weight_of(m, mmin), c3);
+            }
+        }
+        ed = edn, k = kn;
     }
     const float inv = 1.f / A;
     C[0] = r * inv, C[1] = g * inv, C[2] = bl * inv;
@@ -276,7 +479,9 @@ __global__ void __launch_bounds__(kBlock)
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    __shared__ float4 cache_lds[kSH ? kCache * kBlock : 1];
+    __shared__ float4 cache_lds[cache_vec4(kSH)];
+    ColorCache cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache(cache_lds);
     const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
     if (r >= R.n) return;
     const int start = R.start[r];
@@ -286,11 +491,6 @@ __global__ void __launch_bounds__(kBlock)
 #pragma unroll
         for (int i = 0; i < 5; ++i) O.stats[5 * r + i] = 0;
         return;
-    }
-    float4* cache = cache_lds + (kSH ? threadIdx.x : 0);
-    if (kSH) {
-#pragma unroll
-        for (int i = 0; i < kCache; ++i) cache[i * kBlock] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
     }
     const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
@@ -357,10 +557,121 @@ __global__ void __launch_bounds__(kBlock)
     st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
 }
 
+#ifndef VGR_FLAT
+#define VGR_FLAT 0
+#endif
+
+// Flat variant for the single-pass modes (stages 0 and 1, fused and baked colours): every loop iteration
+// evaluates exactly one edge of the lane's current sample, whatever its cell, and a lane that completes a
+// sample composites it and starts the next one in the same iteration. Lanes whose cells have fewer edges
+// move on instead of idling while the wave finishes longer cells (the per-sample kernel runs every cell for
+// the longest neighbourhood in the wave). Same samples, same order of terms, same results.
+template <int STAGE, int COLOR, bool HALF, bool TRACE>
+__global__ void __launch_bounds__(kBlock)
+    foam_flat_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
+    constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
+    constexpr bool BLEND = STAGE >= 2;
+    __shared__ float4 cache_lds[cache_vec4(kSH)];
+    ColorCache cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache(cache_lds);
+    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
+    if (r >= R.n) return;
+    const int start = R.start[r];
+    if (start < 0 || start >= S.n_sites) {
+        O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+        O.T[r] = 1.f, O.depth[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) O.stats[5 * r + i] = 0;
+        return;
+    }
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float t_near = R.t_near[r], t_far = R.t_far[r];
+    const int max_samples = R.cap != nullptr ? R.cap[r] : INT_MAX;
+    float b[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) b[i] = 0.f;
+    if (kSH) sh_basis(d[0], d[1], d[2], P.sh_deg, b);
+
+    int walk_steps = 0, n_dens = 0, n_sh = 0;
+    int c = walk_to(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
+    // current sample: parameter t in cell c, edges [e, e_end), first edge e_self (the cell itself)
+    float t = t_near;
+    bool want_exit = true, is_last = false, have_P = false;
+    float4 pc = S.points[c];
+    int e = S.offsets[c], e_end = S.offsets[c + 1], e_self = e;
+    float x[3];
+    sample_point(o, d, t, x);
+    CellEval E;
+    E.sigma = 0.f, E.mmin = kInf, E.t_exit = kInf, E.next = INT_MAX;
+    blend_init(E.B);
+    float tP = 0.f, sP = 0.f, CP[3] = {0.f, 0.f, 0.f};
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    int n_samples = 0, n_color = 0, iters = 0;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (;;) {
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+        if (want_exit && e != e_self) exit_candidate(S, pc, ed, k, o, d, E);
+        if (STAGE >= 1) {
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+            const float4 q0 = a[0], q1 = a[1];
+            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
+            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, E, n_dens, n_sh);
+        }
+        if (++e < e_end) continue;
+        // the sample is complete
+        trace_cell<TRACE>(S, O, r, n_samples, c);
+        ++n_samples;
+        float CQ[3] = {0.f, 0.f, 0.f};
+        if (BLEND) {
+            const float inv = 1.f / E.B.a;
+            CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv;
+        }
+        if (have_P) {
+            const float delta = t - tP;
+            const float alpha = 1.f - fexp(-0.5f * (sP + E.sigma) * delta);
+            const float w = T * alpha;
+            if (STAGE >= 2 && w > P.w_thresh) {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (CP[a] + CQ[a]);
+                dep += w * 0.5f * (tP + t);
+                ++n_color;
+            }
+            T *= 1.f - alpha;
+            if (is_last || T < P.t_thresh || ++iters >= kMaxCells) break;
+        }
+        have_P = true, tP = t, sP = E.sigma;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
+        // next sample: the exit crossing, or x(far) in the same cell
+        is_last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
+        t = is_last ? t_far : fmaxf(E.t_exit, tP);
+        c = is_last ? c : E.next;
+        want_exit = !is_last;
+        pc = S.points[c];
+        e = S.offsets[c], e_end = S.offsets[c + 1], e_self = e;
+        sample_point(o, d, t, x);
+        E.sigma = 0.f, E.mmin = kInf, E.t_exit = kInf, E.next = INT_MAX;
+        blend_init(E.B);
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
+    O.T[r] = T;
+    O.depth[r] = dep;
+    int* st = O.stats + 5 * r;
+    st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
+}
+
 template <int STAGE, int COLOR, bool HALF, bool TRACE>
 int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
-    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
-                       stream, S, P, R, O);
+    constexpr bool kFlat = VGR_FLAT && (STAGE < 2 || COLOR != kLazy);  // single-pass modes
+    if (kFlat)
+        hipLaunchKernelGGL((foam_flat_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
+                           stream, S, P, R, O);
+    else
+        hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock),
+                           0, stream, S, P, R, O);
     return launch_status("foam_infer_kernel");
 }
 
