@@ -21,11 +21,24 @@ sys.path.insert(0, os.path.join(ROOT, 'voronoi-gauss_amd'))
 
 METRIC = 'Mrays/s and FPS @1080p (2M sites) on 1 MI355X; achieved HBM GB/s vs peak'
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'foam_infer_config3_traffic.json')
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'foam_infer_config3_pmc.md')
 
 
 def log(*a):
 	print('[bench]', *a, file=sys.stderr, flush=True)
+
+
+def measured_traffic(workload):
+	"""DRAM bytes per launch of this workload from the committed rocprofv3 PMC summary (a line
+	'traffic_bytes_per_launch: <bytes> workload: <key>'), or None when no summary matches."""
+	import re
+	if not os.path.exists(TRAFFIC_FILE):
+		return None
+	for line in open(TRAFFIC_FILE):
+		m = re.match(r'\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)\s+workload:\s*(\S+)', line)
+		if m and m.group(2) == workload:
+			return float(m.group(1))
+	return None
 
 
 def algorithmic_bytes(stats, sh_bytes):
@@ -46,7 +59,8 @@ def main():
 	ap.add_argument('--warmup', type=int, default=3)
 	ap.add_argument('--config', type=int, default=3)
 	ap.add_argument('--scale', type=float, default=1.0, help='site-count scale (1 = the BASELINE config)')
-	ap.add_argument('--colors', default='exact', choices=['exact', 'fused'])
+	ap.add_argument('--colors', default='fused', choices=['exact', 'fused'],
+				help='exact colour modes (eps_color = 0): lazy second pass or fused online blend')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
@@ -108,11 +122,7 @@ def main():
 	abytes = algorithmic_bytes(stats.cpu(), sh_bytes)
 	achieved = abytes / (ms * 1e-3) / 1e9
 	st = stats.double()
-	traffic = None
-	if os.path.exists(TRAFFIC_FILE):
-		rec = json.load(open(TRAFFIC_FILE))
-		if rec.get('workload') == f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}':
-			traffic = rec.get('bytes_per_launch')
+	traffic = measured_traffic(f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}')
 
 	cpu = None
 	if args.cpu_seconds > 0:
@@ -146,6 +156,7 @@ def main():
 			'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 			'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic,
 			'algorithmic_bytes_per_launch': abytes,
+			'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1),
 		},
 		'cpu_baseline': cpu,
 	}

@@ -7,8 +7,8 @@
 //
 // MI355X mapping: one ray per lane, rays ordered in 8x8 pixel tiles by the host so a wave64 is one tile and
 // its lanes walk mostly the same cells (the per-edge loads of a cell are then one broadcast line per wave);
-// workgroups are remapped so each XCD renders a contiguous band of tiles (L2 locality). The per-ray colour
-// cache (8 direct-mapped slots, keyed by site) lives in LDS, slot-major so lanes hit consecutive banks.
+// workgroups are remapped so each XCD renders a contiguous band of tiles (L2 locality). SH coefficient blocks
+// are cached per wave in LDS (the tile's rays read mostly the same sites); colours are evaluated per lane.
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -16,7 +16,6 @@ namespace vgr {
 namespace {
 
 constexpr int kBlock = 64;  // one wave64 per workgroup = one 8x8 ray tile
-constexpr int kCache = 8;
 constexpr int kLazy = VGR_COLOR_LAZY, kBaked = VGR_COLOR_BAKED, kFused = VGR_COLOR_FUSED;
 
 struct FoamScene {
@@ -148,73 +147,33 @@ __device__ __forceinline__ void sh_color_from(const float4 (&f)[NV], const float
     c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
 }
 
-template <bool HALF, int NV>
-__device__ __forceinline__ void site_color_n(const float4* __restrict__ sh, int k, const float (&b)[16],
-                                             float (&c)[3]) {
-    const float4* s = sh + (HALF ? 6 : 12) * static_cast<int64_t>(k);
-    float4 f[NV];
-#pragma unroll
-    for (int q = 0; q < NV; ++q) f[q] = s[q];
-    sh_color_from<HALF, NV>(f, b, c);
-}
-
 #pragma clang fp contract(off)
 // ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
-// Only the float4 holding coefficients of degree <= sh_deg are read (the others are multiplied by a zero
-// basis value, so skipping them leaves every finite result unchanged).
-template <bool HALF>
-__device__ __forceinline__ void site_color(const FoamScene& S, int deg, int k, const float (&b)[16], float (&c)[3]) {
-    if (HALF) {
-        switch (deg) {
-            case 0: site_color_n<true, sh_vec4_f16(0)>(S.sh, k, b, c); break;
-            case 1: site_color_n<true, sh_vec4_f16(1)>(S.sh, k, b, c); break;
-            case 2: site_color_n<true, sh_vec4_f16(2)>(S.sh, k, b, c); break;
-            default: site_color_n<true, sh_vec4_f16(3)>(S.sh, k, b, c); break;
-        }
-    } else {
-        switch (deg) {
-            case 0: site_color_n<false, sh_vec4_f32(0)>(S.sh, k, b, c); break;
-            case 1: site_color_n<false, sh_vec4_f32(1)>(S.sh, k, b, c); break;
-            case 2: site_color_n<false, sh_vec4_f32(2)>(S.sh, k, b, c); break;
-            default: site_color_n<false, sh_vec4_f32(3)>(S.sh, k, b, c); break;
-        }
-    }
-}
-
-// Colour of site k for this ray, through one of two LDS caches (VGR_SHCACHE):
-//  0  per-lane cache of site colours (r, g, b, k), 8 direct-mapped slots per lane (k mod 8);
-//  1  wave-shared cache of SH coefficient blocks, kSlots direct-mapped slots (k mod kSlots): the 64 rays of a
-//     tile read mostly the same sites, so a block is fetched from memory once per wave and every other lane
-//     reads it from LDS; the colour itself is evaluated per lane (it depends on the ray direction).
-// Both give the colour max(SH_k(d) + 1/2, 0) bit for bit; n_sh counts the SH evaluations performed.
-#ifndef VGR_SHCACHE
-#define VGR_SHCACHE 1
-#endif
+// Colour of site k for this ray through the wave-shared LDS cache of SH coefficient blocks: kSlots direct-mapped
+// slots (site k mod kSlots), stored [12][kSlots] float4 so that lanes reading different slots hit different
+// banks. The 64 rays of a tile read mostly the same sites, so a block is fetched from memory once per wave and
+// the other lanes read it from LDS (about 85 % of lookups on the config-3 scene); the colour itself,
+// max(SH_k(d) + 1/2, 0), is evaluated per lane since it depends on the ray direction. On a miss one lane per slot
+// is elected (claim write, read back) to fetch the block and publish it; a lane whose slot went to another site
+// in the same round reads memory. n_sh counts the SH evaluations, i.e. every colour lookup.
 constexpr int kSlots = 64;
 
 struct ColorCache {
-    float4* col;          // lane cache: this lane's column, slots kBlock apart
-    float4* data;         // wave cache: [12][kSlots] float4 coefficient blocks
-    volatile int* tag;    // wave cache: site held by each slot (-1: empty)
-    volatile int* claim;  // wave cache: lane elected to fill each slot
+    float4* data;         // [12][kSlots] coefficient blocks
+    volatile int* tag;    // site held by each slot (-1: empty)
+    volatile int* claim;  // lane elected to fill each slot
 };
 
-// LDS footprint per block of the colour cache, in float4 units (the tag and claim arrays follow the data).
-constexpr int cache_vec4(bool sh) { return !sh ? 1 : VGR_SHCACHE ? 12 * kSlots + 2 * kSlots / 4 : kCache * kBlock; }
+// LDS footprint per block of the colour cache, in float4 units (tag and claim arrays follow the blocks).
+constexpr int cache_vec4(bool sh) { return sh ? 12 * kSlots + 2 * kSlots / 4 : 1; }
 
 __device__ __forceinline__ ColorCache make_cache(float4* lds) {
     ColorCache C;
-    C.col = lds + threadIdx.x;
     C.data = lds;
     C.tag = reinterpret_cast<volatile int*>(lds + 12 * kSlots);
     C.claim = C.tag + kSlots;
-#if VGR_SHCACHE
     for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
-#else
-#pragma unroll
-    for (int i = 0; i < kCache; ++i) C.col[i * kBlock] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
-#endif
     __syncthreads();
     return C;
 }
@@ -251,10 +210,11 @@ __device__ __forceinline__ void wave_color_n(ColorCache& C, const float4* __rest
     sh_color_from<HALF, NV>(f, b, c);
 }
 
+// Only the float4 holding the coefficients of degree <= sh_deg are read: the others are multiplied by a zero basis
+// value, so skipping them leaves every finite colour unchanged.
 template <bool HALF>
 __device__ __forceinline__ void cached_color(const FoamScene& S, int deg, ColorCache& C, int k, const float (&b)[16],
                                              float (&c)[3], int& n_sh) {
-#if VGR_SHCACHE
     ++n_sh;
     if (HALF) {
         switch (deg) {
@@ -271,17 +231,6 @@ __device__ __forceinline__ void cached_color(const FoamScene& S, int deg, ColorC
             default: wave_color_n<false, sh_vec4_f32(3)>(C, S.sh, k, b, c); break;
         }
     }
-#else
-    float4& e = C.col[(k & (kCache - 1)) * kBlock];
-    const float4 v = e;
-    if (__float_as_int(v.w) == k) {
-        c[0] = v.x, c[1] = v.y, c[2] = v.z;
-        return;
-    }
-    site_color<HALF>(S, deg, k, b, c);
-    e = make_float4(c[0], c[1], c[2], __int_as_float(k));
-    ++n_sh;
-#endif
 }
 
 // Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated.
@@ -557,121 +506,10 @@ __global__ void __launch_bounds__(kBlock)
     st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
 }
 
-#ifndef VGR_FLAT
-#define VGR_FLAT 0
-#endif
-
-// Flat variant for the single-pass modes (stages 0 and 1, fused and baked colours): every loop iteration
-// evaluates exactly one edge of the lane's current sample, whatever its cell, and a lane that completes a
-// sample composites it and starts the next one in the same iteration. Lanes whose cells have fewer edges
-// move on instead of idling while the wave finishes longer cells (the per-sample kernel runs every cell for
-// the longest neighbourhood in the wave). Same samples, same order of terms, same results.
-template <int STAGE, int COLOR, bool HALF, bool TRACE>
-__global__ void __launch_bounds__(kBlock)
-    foam_flat_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
-    constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
-    constexpr bool BLEND = STAGE >= 2;
-    __shared__ float4 cache_lds[cache_vec4(kSH)];
-    ColorCache cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache(cache_lds);
-    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
-    if (r >= R.n) return;
-    const int start = R.start[r];
-    if (start < 0 || start >= S.n_sites) {
-        O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
-        O.T[r] = 1.f, O.depth[r] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) O.stats[5 * r + i] = 0;
-        return;
-    }
-    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
-    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
-    const float t_near = R.t_near[r], t_far = R.t_far[r];
-    const int max_samples = R.cap != nullptr ? R.cap[r] : INT_MAX;
-    float b[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) b[i] = 0.f;
-    if (kSH) sh_basis(d[0], d[1], d[2], P.sh_deg, b);
-
-    int walk_steps = 0, n_dens = 0, n_sh = 0;
-    int c = walk_to(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
-    // current sample: parameter t in cell c, edges [e, e_end), first edge e_self (the cell itself)
-    float t = t_near;
-    bool want_exit = true, is_last = false, have_P = false;
-    float4 pc = S.points[c];
-    int e = S.offsets[c], e_end = S.offsets[c + 1], e_self = e;
-    float x[3];
-    sample_point(o, d, t, x);
-    CellEval E;
-    E.sigma = 0.f, E.mmin = kInf, E.t_exit = kInf, E.next = INT_MAX;
-    blend_init(E.B);
-    float tP = 0.f, sP = 0.f, CP[3] = {0.f, 0.f, 0.f};
-    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
-    int n_samples = 0, n_color = 0, iters = 0;
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (;;) {
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
-        if (want_exit && e != e_self) exit_candidate(S, pc, ed, k, o, d, E);
-        if (STAGE >= 1) {
-            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-            const float4 q0 = a[0], q1 = a[1];
-            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
-            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, E, n_dens, n_sh);
-        }
-        if (++e < e_end) continue;
-        // the sample is complete
-        trace_cell<TRACE>(S, O, r, n_samples, c);
-        ++n_samples;
-        float CQ[3] = {0.f, 0.f, 0.f};
-        if (BLEND) {
-            const float inv = 1.f / E.B.a;
-            CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv;
-        }
-        if (have_P) {
-            const float delta = t - tP;
-            const float alpha = 1.f - fexp(-0.5f * (sP + E.sigma) * delta);
-            const float w = T * alpha;
-            if (STAGE >= 2 && w > P.w_thresh) {
-#pragma unroll
-                for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (CP[a] + CQ[a]);
-                dep += w * 0.5f * (tP + t);
-                ++n_color;
-            }
-            T *= 1.f - alpha;
-            if (is_last || T < P.t_thresh || ++iters >= kMaxCells) break;
-        }
-        have_P = true, tP = t, sP = E.sigma;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
-        // next sample: the exit crossing, or x(far) in the same cell
-        is_last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
-        t = is_last ? t_far : fmaxf(E.t_exit, tP);
-        c = is_last ? c : E.next;
-        want_exit = !is_last;
-        pc = S.points[c];
-        e = S.offsets[c], e_end = S.offsets[c + 1], e_self = e;
-        sample_point(o, d, t, x);
-        E.sigma = 0.f, E.mmin = kInf, E.t_exit = kInf, E.next = INT_MAX;
-        blend_init(E.B);
-    }
-#pragma unroll
-    for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
-    O.T[r] = T;
-    O.depth[r] = dep;
-    int* st = O.stats + 5 * r;
-    st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
-}
-
 template <int STAGE, int COLOR, bool HALF, bool TRACE>
 int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
-    constexpr bool kFlat = VGR_FLAT && (STAGE < 2 || COLOR != kLazy);  // single-pass modes
-    if (kFlat)
-        hipLaunchKernelGGL((foam_flat_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
-                           stream, S, P, R, O);
-    else
-        hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock),
-                           0, stream, S, P, R, O);
+    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
+                       stream, S, P, R, O);
     return launch_status("foam_infer_kernel");
 }
 
