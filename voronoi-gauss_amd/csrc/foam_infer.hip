@@ -159,10 +159,14 @@ __device__ __forceinline__ void sh_color_from(const float4 (&f)[NV], const float
 // in the same round reads memory. n_sh counts the SH evaluations, i.e. every colour lookup.
 constexpr int kSlots = 64;
 
+// Volatile ints typed as LDS: the election and tag accesses stay ds_read / ds_write. Through a generic pointer
+// they would be flat accesses, after each of which the wave waits for all of its outstanding global loads.
+typedef __attribute__((address_space(3))) volatile int lds_int;
+
 struct ColorCache {
-    float4* data;         // [12][kSlots] coefficient blocks
-    volatile int* tag;    // site held by each slot (-1: empty)
-    volatile int* claim;  // lane elected to fill each slot
+    float4* data;    // [12][kSlots] coefficient blocks
+    lds_int* tag;    // site held by each slot (-1: empty)
+    lds_int* claim;  // lane elected to fill each slot
 };
 
 // LDS footprint per block of the colour cache, in float4 units (tag and claim arrays follow the blocks).
@@ -171,7 +175,7 @@ constexpr int cache_vec4(bool sh) { return sh ? 12 * kSlots + 2 * kSlots / 4 : 1
 __device__ __forceinline__ ColorCache make_cache(float4* lds) {
     ColorCache C;
     C.data = lds;
-    C.tag = reinterpret_cast<volatile int*>(lds + 12 * kSlots);
+    C.tag = (lds_int*)(lds + 12 * kSlots);
     C.claim = C.tag + kSlots;
     for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
     __syncthreads();
