@@ -53,15 +53,10 @@ struct FoamOut {
     int64_t trace_cap;
 };
 
-// Tuning knobs (compile-time): VGR_CONTRACT lets the density / colour arithmetic contract into FMA (the
-// traversal arithmetic never does); VGR_PIPE is the software-pipelining depth of the neighbourhood loops
-// (0: none, 1: edge record of e + 1 in flight while e is computed, 2: edge records two ahead and the site
-// records of e + 1 in flight).
+// Tuning knob (compile-time): VGR_CONTRACT lets the density / colour arithmetic contract into FMA (the traversal
+// arithmetic never does).
 #ifndef VGR_CONTRACT
 #define VGR_CONTRACT 1
-#endif
-#ifndef VGR_PIPE
-#define VGR_PIPE 2
 #endif
 
 // Running normalised colour blend (fused / baked modes).
@@ -124,13 +119,16 @@ __device__ __forceinline__ void accumulate(float& A, float& r, float& g, float& 
     A += w, r += w * c[0], g += w * c[1], bl += w * c[2];
 }
 
-// max(SH_k(d) + 1/2, 0) from the first NV float4 of a site's coefficients, accumulated in storage order.
-template <bool HALF, int NV>
-__device__ __forceinline__ void sh_color_from(const float4 (&f)[NV], const float (&b)[16], float (&c)[3]) {
-    c[0] = c[1] = c[2] = 0.5f;
+// Adds blocks q0 .. q0 + 3 (those below nv) of a site's SH coefficients (fp32, or fp16 pairs) to c: the colour
+// SH_k(d) accumulates over the coefficients in storage order, coefficient i of channel i mod 3 times basis i / 3.
+template <bool HALF>
+__device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int nv, const float (&b)[16],
+                                              float (&c)[3]) {
 #pragma unroll
-    for (int q = 0; q < NV; ++q) {
-        const float fv[4] = {f[q].x, f[q].y, f[q].z, f[q].w};
+    for (int uq = 0; uq < 4; ++uq) {
+        const int q = q0 + uq;
+        if (q >= nv) break;
+        const float fv[4] = {f[uq].x, f[uq].y, f[uq].z, f[uq].w};
         if (HALF) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -144,20 +142,24 @@ __device__ __forceinline__ void sh_color_from(const float4 (&f)[NV], const float
             for (int u = 0; u < 4; ++u) c[(4 * q + u) % 3] += b[(4 * q + u) / 3] * fv[u];
         }
     }
-    c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
 }
 
 #pragma clang fp contract(off)
 // ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
-// Colour of site k for this ray through the wave-shared LDS cache of SH coefficient blocks: kSlots direct-mapped
-// slots (site k mod kSlots), stored [12][kSlots] float4 so that lanes reading different slots hit different
-// banks. The 64 rays of a tile read mostly the same sites, so a block is fetched from memory once per wave and
-// the other lanes read it from LDS (about 85 % of lookups on the config-3 scene); the colour itself,
-// max(SH_k(d) + 1/2, 0), is evaluated per lane since it depends on the ray direction. On a miss one lane per slot
-// is elected (claim write, read back) to fetch the block and publish it; a lane whose slot went to another site
-// in the same round reads memory. n_sh counts the SH evaluations, i.e. every colour lookup.
-constexpr int kSlots = 64;
+// Colour blocks of site k for this ray come through the wave-shared LDS cache of SH coefficient blocks: kSlots
+// direct-mapped slots (site k mod kSlots), stored [12][kSlots] float4 so that lanes reading different slots hit
+// different banks. The 64 rays of a tile read overlapping sets of sites (45 % of the lookups find their block in
+// LDS on the config-3 scene); the colour itself, max(SH_k(d) + 1/2, 0), is evaluated per lane since it depends on
+// the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup. 48 slots keep the cache at 9.8 KB
+// per wave, so that 16 waves (4 per SIMD) fit in a CU's 160 KB of LDS: the kernel is latency-bound, and a fourth
+// wave per SIMD gains more than the larger cache a 64-slot layout (3 waves) would give.
+#ifndef VGR_SLOTS
+#define VGR_SLOTS 48
+#endif
+constexpr int kSlots = VGR_SLOTS;
+
+__device__ __forceinline__ int slot_of(int k) { return static_cast<int>(static_cast<uint32_t>(k) % kSlots); }
 
 // Volatile ints typed as LDS: the election and tag accesses stay ds_read / ds_write. Through a generic pointer
 // they would be flat accesses, after each of which the wave waits for all of its outstanding global loads.
@@ -166,75 +168,101 @@ typedef __attribute__((address_space(3))) volatile int lds_int;
 struct ColorCache {
     float4* data;    // [12][kSlots] coefficient blocks
     lds_int* tag;    // site held by each slot (-1: empty)
-    lds_int* claim;  // lane elected to fill each slot
+    lds_int* claim;  // election word of each slot
+    lds_int* req;    // sites being fetched in the current fill
 };
 
-// LDS footprint per block of the colour cache, in float4 units (tag and claim arrays follow the blocks).
-constexpr int cache_vec4(bool sh) { return sh ? 12 * kSlots + 2 * kSlots / 4 : 1; }
+// LDS footprint per block of the colour cache, in float4 units (tag, claim and request arrays follow the blocks).
+constexpr int cache_vec4(bool sh) { return sh ? 12 * kSlots + (3 * kSlots + 3) / 4 : 1; }
 
 __device__ __forceinline__ ColorCache make_cache(float4* lds) {
     ColorCache C;
     C.data = lds;
     C.tag = (lds_int*)(lds + 12 * kSlots);
     C.claim = C.tag + kSlots;
-    for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
+    C.req = C.claim + kSlots;
+    for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1, C.req[i] = 0;
     __syncthreads();
     return C;
 }
 
-template <bool HALF, int NV>
-__device__ __forceinline__ void wave_color_n(ColorCache& C, const float4* __restrict__ sh, int k, const float (&b)[16],
-                                             float (&c)[3]) {
-    const int slot = k & (kSlots - 1);
-    const float4* src = sh + (HALF ? 6 : 12) * static_cast<int64_t>(k);
-    float4 f[NV];
-    bool have = false;
-    if (C.tag[slot] != k) {  // miss: one lane per slot fetches its block and publishes it
-        const int lane = static_cast<int>(threadIdx.x);
-        C.claim[slot] = lane;
-        if (C.claim[slot] == lane) {
-#pragma unroll
-            for (int q = 0; q < NV; ++q) f[q] = src[q];
-#pragma unroll
-            for (int q = 0; q < NV; ++q) C.data[q * kSlots + slot] = f[q];
-            C.tag[slot] = k;
-            have = true;
-        }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the LDS reads below after the publication above
-    if (!have) {
-        if (C.tag[slot] == k) {
-#pragma unroll
-            for (int q = 0; q < NV; ++q) f[q] = C.data[q * kSlots + slot];
-        } else {  // the slot went to another site this round: read from memory
-#pragma unroll
-            for (int q = 0; q < NV; ++q) f[q] = src[q];
-        }
-    }
-    sh_color_from<HALF, NV>(f, b, c);
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
 }
 
-// Only the float4 holding the coefficients of degree <= sh_deg are read: the others are multiplied by a zero basis
-// value, so skipping them leaves every finite colour unchanged.
-template <bool HALF>
-__device__ __forceinline__ void cached_color(const FoamScene& S, int deg, ColorCache& C, int k, const float (&b)[16],
-                                             float (&c)[3], int& n_sh) {
-    ++n_sh;
-    if (HALF) {
-        switch (deg) {
-            case 0: wave_color_n<true, sh_vec4_f16(0)>(C, S.sh, k, b, c); break;
-            case 1: wave_color_n<true, sh_vec4_f16(1)>(C, S.sh, k, b, c); break;
-            case 2: wave_color_n<true, sh_vec4_f16(2)>(C, S.sh, k, b, c); break;
-            default: wave_color_n<true, sh_vec4_f16(3)>(C, S.sh, k, b, c); break;
+// max(SH_k(d) + 1/2, 0) for every active lane (the lanes that need a colour now; control flow is uniform across
+// them), site k's coefficient block read through the wave cache.
+//
+// The texture path and LDS charge a wave-wide load the same cycles however few of its lanes are active, so the
+// fetch keeps load instructions per round low, and it keeps registers low (a block is read and multiplied four
+// float4 at a time) so that four waves fit on each SIMD. Each pass: lanes whose site is cached pin their slot; the
+// missing sites get one elected lane per unpinned slot and are fetched by all active lanes together (one float4 per
+// lane per load, about five blocks per instruction); then every lane whose block is now in LDS reads it and
+// evaluates its colour. Lanes whose slot was pinned by, or went to, another site wait for the next pass; every pass
+// serves at least one slot, so the loop ends (usually after one pass, two in about a third of the rounds).
+template <bool HALF, int NV>
+__device__ __forceinline__ void cached_colour(ColorCache& C, const float4* __restrict__ sh, int k, const float (&b)[16],
+                                              float (&c)[3]) {
+    const int lane = static_cast<int>(threadIdx.x);
+    const int slot = slot_of(k);
+    const uint64_t active = __ballot(1);
+    const int n_active = __popcll(active), rank = lanes_below(active);
+    bool pending = true;
+    for (;;) {
+        // The phases are separated by wave barriers: the lanes of a phase act on what every lane did in the phase
+        // before. The barrier is convergent, so the compiler cannot fold two one-sided stores into an if/else and
+        // run the claim read-back (on one side) before the pin (on the other), as it may for independent threads.
+        const bool hit = pending && C.tag[slot] == k;
+        const bool miss = pending && !hit;
+        if (miss) C.claim[slot] = lane;
+        __builtin_amdgcn_wave_barrier();
+        if (hit) C.claim[slot] = -1;  // pin, after the claims
+        __builtin_amdgcn_wave_barrier();
+        const bool win = miss && C.claim[slot] == lane;
+        const uint64_t wins = __ballot(win);
+        if (wins != 0) {
+            if (win) C.req[lanes_below(wins)] = k;
+            __builtin_amdgcn_wave_barrier();
+            const int total = NV * __popcll(wins);
+            for (int base = 0; base < total; base += n_active) {
+                const int j = base + rank;
+                if (j < total) {
+                    const int r = j / NV, q = j - r * NV;
+                    const int kr = C.req[r];
+                    C.data[q * kSlots + slot_of(kr)] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // publish the tags after the blocks
+            if (win) C.tag[slot] = k;
+            __builtin_amdgcn_wave_barrier();
         }
-    } else {
-        switch (deg) {
-            case 0: wave_color_n<false, sh_vec4_f32(0)>(C, S.sh, k, b, c); break;
-            case 1: wave_color_n<false, sh_vec4_f32(1)>(C, S.sh, k, b, c); break;
-            case 2: wave_color_n<false, sh_vec4_f32(2)>(C, S.sh, k, b, c); break;
-            default: wave_color_n<false, sh_vec4_f32(3)>(C, S.sh, k, b, c); break;
+        const bool served = hit || (miss && C.tag[slot] == k);
+        if (served) {
+            c[0] = c[1] = c[2] = 0.5f;
+#pragma unroll
+            for (int q0 = 0; q0 < NV; q0 += 4) {
+                float4 f[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (q0 + u < NV) f[u] = C.data[(q0 + u) * kSlots + slot];
+                sh_accumulate<HALF>(f, q0, NV, b, c);
+                __builtin_amdgcn_sched_barrier(0);  // one chunk of the block in registers at a time
+            }
+            c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
         }
+        pending = pending && !served;
+        __builtin_amdgcn_wave_barrier();
+        if (__ballot(pending) == 0) break;
     }
+}
+
+// Number of float4 a colour fetch reads: the blocks holding coefficients of degree <= DEG (the others multiply a
+// zero basis value, so leaving them out changes no finite colour).
+template <bool HALF, int DEG>
+constexpr int sh_vec4() {
+    return HALF ? sh_vec4_f16(DEG) : sh_vec4_f32(DEG);
 }
 
 // Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated.
@@ -278,50 +306,30 @@ __device__ __forceinline__ void exit_candidate(const FoamScene& S, const float4&
     }
 }
 
-// Field terms of neighbour k (edge record ed, site records q0..q3) for the sample x.
-template <int STAGE, int COLOR, bool HALF>
-__device__ __forceinline__ void field_terms(const FoamScene& S, const FoamParams& P, const float (&x)[3],
-                                            const float4& ed, int k, const float4& q0, const float4& q1,
-                                            const float4& q2, const float4& q3, const float (&b)[16], ColorCache& cache,
-                                            CellEval& R, int& n_dens, int& n_sh) {
-    constexpr bool BLEND = COLOR != kLazy;
-    float v0, v1, v2, r2;
-    offset_of(x, ed, v0, v1, v2, r2);
-    const float2 cut = cutoffs(ed.w);
-    if (r2 <= cut.x) {
-        R.sigma += density_term(q0, q1, v0, v1, v2);
-        ++n_dens;
-    }
-    if (STAGE >= 2) {
-        const float lb = r2 * cut.y;
-        if (BLEND ? lb <= R.B.m + P.color_cut : lb < R.mmin) {
-            const float m = maha_f(q2, q3, v0, v1, v2);
-            if (BLEND) {
-                if (m <= R.B.m + P.color_cut) {
-                    float c3[3];
-                    if (COLOR == kBaked) {
-                        const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
-                        c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
-                    } else {
-                        cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
-                    }
-                    blend_add(R.B, m, c3[0], c3[1], c3[2]);
-                }
-            } else {
-                R.mmin = fminf(R.mmin, m);
-            }
-        }
-    }
+// Site records of neighbour k read by a pass: density (q0, q1) from stage 1, colour conic (q2, q3) from stage 2.
+struct SiteRec {
+    float4 q0, q1, q2, q3;
+};
+
+template <int STAGE>
+__device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    SiteRec r{zero4, zero4, zero4, zero4};
+    const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+    if (STAGE >= 1) r.q0 = a[0], r.q1 = a[1];
+    if (STAGE >= 2) r.q2 = a[2], r.q3 = a[3];
+    return r;
 }
 
 // One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
 // Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
-// The loop is software-pipelined (VGR_PIPE): the edge records and site records of the next edges are loaded
-// while the current one is evaluated (indices clamped to the cell, so every load stays in bounds).
-template <int STAGE, int COLOR, bool HALF>
+// The loop is software-pipelined: the edge record of e + 2 and the site records of e + 1 are loaded while edge e is
+// evaluated (indices clamped to the cell, so every load stays in bounds).
+template <int STAGE, int COLOR, bool HALF, int DEG>
 __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
                           const float (&d)[3], const float (&b)[16], ColorCache& cache, bool want_exit, CellEval& R,
                           int& n_dens, int& n_sh) {
+    constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
     const float4 pc = S.points[c];
     float x[3];
     sample_point(o, d, t, x);
@@ -329,67 +337,53 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
     const int last = e1 - 1;
     R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
     blend_init(R.B);
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#if VGR_PIPE == 0
+    float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
+    int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+    SiteRec q = site_rec<STAGE>(S, k);
     for (int e = e0; e < e1; ++e) {
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
-        if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
-        if (STAGE >= 1) {
-            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-            const float4 q0 = a[0], q1 = a[1];
-            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
-            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
-        }
-    }
-#else
-    float4 ed = S.edge[e0];
-    int k = S.nbr[e0];
-#if VGR_PIPE >= 2
-    float4 ed1 = S.edge[min(e0 + 1, last)];
-    int k1 = S.nbr[min(e0 + 1, last)];
-    float4 q0 = zero4, q1 = zero4, q2 = zero4, q3 = zero4;
-    if (STAGE >= 1) {
-        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-        q0 = a[0], q1 = a[1];
-        if (STAGE >= 2) q2 = a[2], q3 = a[3];
-    }
-#endif
-    for (int e = e0; e < e1; ++e) {
-#if VGR_PIPE >= 2
-        // in flight while edge e is evaluated: site records of e + 1, edge records of e + 2
         const int e2 = min(e + 2, last);
         const float4 ed2 = S.edge[e2];
         const int k2 = S.nbr[e2];
-        float4 n0 = zero4, n1 = zero4, n2 = zero4, n3 = zero4;
-        if (STAGE >= 1) {
-            const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
-            n0 = a[0], n1 = a[1];
-            if (STAGE >= 2) n2 = a[2], n3 = a[3];
-        }
-        if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
-        if (STAGE >= 1) field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
-        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
-        q0 = n0, q1 = n1, q2 = n2, q3 = n3;
-#else
-        const int e1n = min(e + 1, last);
-        const float4 edn = S.edge[e1n];
-        const int kn = S.nbr[e1n];
+        const SiteRec qn = site_rec<STAGE>(S, k1);
         if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
         if (STAGE >= 1) {
-            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-            const float4 q0 = a[0], q1 = a[1];
-            const float4 q2 = STAGE >= 2 ? a[2] : zero4, q3 = STAGE >= 2 ? a[3] : zero4;
-            field_terms<STAGE, COLOR, HALF>(S, P, x, ed, k, q0, q1, q2, q3, b, cache, R, n_dens, n_sh);
+            float v0, v1, v2, r2;
+            offset_of(x, ed, v0, v1, v2, r2);
+            const float2 cut = cutoffs(ed.w);
+            if (r2 <= cut.x) {
+                R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
+                ++n_dens;
+            }
+            if (STAGE >= 2) {
+                const float lb = r2 * cut.y;
+                if (BLEND) {
+                    const float lim = R.B.m + P.color_cut;
+                    if (lb <= lim) {
+                        const float m = maha_f(q.q2, q.q3, v0, v1, v2);
+                        if (m <= lim) {
+                            float c3[3];
+                            if (COLOR == kBaked) {
+                                const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
+                                c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
+                            } else {
+                                ++n_sh;
+                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                            }
+                            blend_add(R.B, m, c3[0], c3[1], c3[2]);
+                        }
+                    }
+                } else if (lb < R.mmin) {
+                    R.mmin = fminf(R.mmin, maha_f(q.q2, q.q3, v0, v1, v2));
+                }
+            }
         }
-        ed = edn, k = kn;
-#endif
+        ed = ed1, k = k1, ed1 = ed2, k1 = k2, q = qn;
     }
-#endif
 }
 
-// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin.
-template <bool HALF>
+// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin; pipelined like
+// eval_cell.
+template <bool HALF, int DEG>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
                            const float (&d)[3], const float (&b)[16], ColorCache& cache, float (&C)[3], int& n_sh) {
     float x[3];
@@ -398,25 +392,27 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
     const int last = e1 - 1;
     const float cut = mmin + P.color_cut;
     float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
-    float4 ed = S.edge[e0];
-    int k = S.nbr[e0];
+    float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
+    int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+    float4 q2 = S.attr[5 * static_cast<int64_t>(k) + 2], q3 = S.attr[5 * static_cast<int64_t>(k) + 3];
     for (int e = e0; e < e1; ++e) {
-        const int en = min(e + 1, last);
-        const float4 edn = S.edge[en];
-        const int kn = S.nbr[en];
-        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-        const float4 q2 = a[2], q3 = a[3];
+        const int e2 = min(e + 2, last);
+        const float4 ed2 = S.edge[e2];
+        const int k2 = S.nbr[e2];
+        const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
+        const float4 n2 = a[2], n3 = a[3];
         float v0, v1, v2, r2;
         offset_of(x, ed, v0, v1, v2, r2);
         if (r2 * cutoffs(ed.w).y <= cut) {
             const float m = maha_f(q2, q3, v0, v1, v2);
             if (m <= cut) {
                 float c3[3];
-                cached_color<HALF>(S, P.sh_deg, cache, k, b, c3, n_sh);
+                ++n_sh;
+                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
                 accumulate(A, r, g, bl, weight_of(m, mmin), c3);
             }
         }
-        ed = edn, k = kn;
+        ed = ed1, k = k1, ed1 = ed2, k1 = k2, q2 = n2, q3 = n3;
     }
     const float inv = 1.f / A;
     C[0] = r * inv, C[1] = g * inv, C[2] = bl * inv;
@@ -427,8 +423,13 @@ __device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O,
     if (TRACE && s < O.trace_cap) O.trace[r * O.trace_cap + s] = S.orig != nullptr ? S.orig[c] : c;
 }
 
-template <int STAGE, int COLOR, bool HALF, bool TRACE>
-__global__ void __launch_bounds__(kBlock)
+// Waves per SIMD the register allocation is bounded for (VGR_WAVES; 0 leaves it to the compiler).
+#ifndef VGR_WAVES
+#define VGR_WAVES 4
+#endif
+
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
+__global__ void __launch_bounds__(kBlock, VGR_WAVES)
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
@@ -452,12 +453,12 @@ __global__ void __launch_bounds__(kBlock)
     float b[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) b[i] = 0.f;
-    if (kSH) sh_basis(d[0], d[1], d[2], P.sh_deg, b);
+    if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
     int c = walk_to(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
     CellEval E;
-    eval_cell<STAGE, COLOR, HALF>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    eval_cell<STAGE, COLOR, HALF, DEG>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
     trace_cell<TRACE>(S, O, r, 0, c);
     float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
     bool hasP = false;
@@ -472,7 +473,7 @@ __global__ void __launch_bounds__(kBlock)
         const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
         const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
         const int cQ = last ? c : E.next;
-        eval_cell<STAGE, COLOR, HALF>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        eval_cell<STAGE, COLOR, HALF, DEG>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
         trace_cell<TRACE>(S, O, r, n_samples, cQ);
         ++n_samples;
         const float sQ = E.sigma, mQ = E.mmin;
@@ -487,8 +488,8 @@ __global__ void __launch_bounds__(kBlock)
         }
         if (STAGE >= 2 && w > P.w_thresh) {
             if (!BLEND) {
-                if (!hasP) color_lazy<HALF>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
-                color_lazy<HALF>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                if (!hasP) color_lazy<HALF, DEG>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
+                color_lazy<HALF, DEG>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
                 hasQ = true;
             }
 #pragma unroll
@@ -510,24 +511,35 @@ __global__ void __launch_bounds__(kBlock)
     st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
 }
 
-template <int STAGE, int COLOR, bool HALF, bool TRACE>
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
 int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
-    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock), 0,
-                       stream, S, P, R, O);
+    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, DEG, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock),
+                       0, stream, S, P, R, O);
     return launch_status("foam_infer_kernel");
+}
+
+// Kernels with SH colours are specialised on the SH degree (block size and basis known at compile time).
+template <int COLOR, bool HALF, bool TRACE>
+int launch_sh(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
+    switch (P.sh_deg) {
+        case 0: return launch<2, COLOR, HALF, 0, TRACE>(S, P, R, O, stream);
+        case 1: return launch<2, COLOR, HALF, 1, TRACE>(S, P, R, O, stream);
+        case 2: return launch<2, COLOR, HALF, 2, TRACE>(S, P, R, O, stream);
+        default: return launch<2, COLOR, HALF, 3, TRACE>(S, P, R, O, stream);
+    }
 }
 
 template <bool TRACE>
 int dispatch(int stage, int color_mode, bool half, const FoamScene& S, const FoamParams& P, const FoamRays& R,
              const FoamOut& O, hipStream_t stream) {
-    if (stage == 0) return launch<0, kLazy, false, TRACE>(S, P, R, O, stream);
-    if (stage == 1) return launch<1, kLazy, false, TRACE>(S, P, R, O, stream);
-    if (color_mode == kBaked) return launch<2, kBaked, false, TRACE>(S, P, R, O, stream);
+    if (stage == 0) return launch<0, kLazy, false, 0, TRACE>(S, P, R, O, stream);
+    if (stage == 1) return launch<1, kLazy, false, 0, TRACE>(S, P, R, O, stream);
+    if (color_mode == kBaked) return launch<2, kBaked, false, 0, TRACE>(S, P, R, O, stream);
     if (color_mode == kLazy)
-        return half ? launch<2, kLazy, true, TRACE>(S, P, R, O, stream)
-                    : launch<2, kLazy, false, TRACE>(S, P, R, O, stream);
-    return half ? launch<2, kFused, true, TRACE>(S, P, R, O, stream)
-                : launch<2, kFused, false, TRACE>(S, P, R, O, stream);
+        return half ? launch_sh<kLazy, true, TRACE>(S, P, R, O, stream)
+                    : launch_sh<kLazy, false, TRACE>(S, P, R, O, stream);
+    return half ? launch_sh<kFused, true, TRACE>(S, P, R, O, stream)
+                : launch_sh<kFused, false, TRACE>(S, P, R, O, stream);
 }
 
 int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr, const float* edge,
