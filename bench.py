@@ -41,15 +41,44 @@ def measured_traffic(workload):
 	return None
 
 
-def algorithmic_bytes(stats, sh_bytes):
+def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray):
 	"""Cache-oblivious bytes of one launch from the per-ray counters (B, 5) = samples, coloured segments, walk
 	steps, density terms, SH evaluations:
 	  56 per ray (o, d, near, far, start in; rgb, T, depth out)
 	  + 24 per sample (cell position 16 + offsets 8)
 	  + 84 per neighbourhood edge = density term (edge record 16 + nbr 4 + density record 32 + colour-conic record 32)
-	  + sh_bytes per SH evaluation (distinct-site colour reads of the ray)."""
+	  + sh_bytes per distinct site whose colour the ray blends (u_sh_per_ray, measured on traced rays)."""
 	s = stats.double()
-	return float(56 * len(s) + 24 * s[:, 0].sum() + 84 * s[:, 3].sum() + sh_bytes * s[:, 4].sum())
+	return float(56 * len(s) + 24 * s[:, 0].sum() + 84 * s[:, 3].sum() + sh_bytes * u_sh_per_ray * len(s))
+
+
+def distinct_blended_sites(fi, pack, args_of, n_rays, sh_deg, tiles=256):
+	"""Mean number of distinct sites whose colour a ray blends, over `tiles` 8x8 ray tiles spread evenly over the
+	launch: the rays are traced again (same kernel, outside the timed region) and, exact colours blending every
+	neighbour of every visited cell, the distinct neighbours of each ray's cells are counted."""
+	import torch
+	dev = pack['points'].device
+	n_tiles = n_rays // 64
+	pick = torch.linspace(0, n_tiles - 1, min(tiles, n_tiles), device=dev).long()
+	rays = (pick[:, None] * 64 + torch.arange(64, device=dev)).reshape(-1)
+	cap = 4096
+	out = fi.foam_infer(*args_of(rays), trace_cap=cap)
+	stats, trace = out[3], out[4]
+	n = stats[:, 0].long().clamp(max=cap)
+	valid = torch.arange(cap, device=dev)[None, :] < n[:, None]
+	ray_id = torch.arange(len(rays), device=dev)[:, None].expand(-1, cap)[valid]
+	cells = trace[valid].long()
+	if pack['inv'] is not None:
+		cells = pack['inv'][cells]
+	start = pack['offsets'][cells].long()
+	count = (pack['offsets'][cells + 1] - pack['offsets'][cells]).long()
+	total = int(count.sum())
+	first = torch.repeat_interleave(torch.cumsum(count, 0) - count, count)
+	edge = torch.repeat_interleave(start, count) + torch.arange(total, device=dev) - first
+	sites = pack['nbr'][edge].long()
+	keys = torch.unique(torch.repeat_interleave(ray_id, count) * len(pack['points']) + sites)
+	u = torch.bincount(keys // len(pack['points']), minlength=len(rays)).double()
+	return float(u.mean()), len(rays)
 
 
 def main():
@@ -119,7 +148,12 @@ def main():
 	log(f'{args.steps} steps: mean {ms:.3f} ms, median {np.median(launch_ms):.3f} ms, wall {wall * 1e3 / args.steps:.3f} '
 		f'ms/step')
 	sh_bytes = 12 * (sc.sh_deg + 1) ** 2
-	abytes = algorithmic_bytes(stats.cpu(), sh_bytes)
+	args_of = lambda sel: (pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'],  # noqa
+						   sc.sh_deg, o[sel], d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, math.inf, mode, 2,
+						   empty, pack['orig'])
+	u_sh, u_rays = distinct_blended_sites(fi, pack, args_of, B, sc.sh_deg)
+	log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
+	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
 	achieved = abytes / (ms * 1e-3) / 1e9
 	st = stats.double()
 	traffic = measured_traffic(f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}')
@@ -150,6 +184,7 @@ def main():
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
 			'density_terms_per_ray': round(float(st[:, 3].mean()), 1),
 			'sh_evals_per_ray': round(float(st[:, 4].mean()), 1),
+			'distinct_blended_sites_per_ray': round(u_sh, 1), 'distinct_sites_traced_rays': u_rays,
 			'mean_T': round(float(T.double().mean()), 4),
 		},
 		'roofline': {
