@@ -120,6 +120,28 @@ int vgr_color_forward(const float* points, int64_t n_sites, const int32_t* offse
  */
 int vgr_conic_forward(const float* log_scale, const float* quat, int64_t n, double floor, float* A, void* stream);
 
+/*
+ * Uniform grid over the sites for exact nearest-site queries: the start-cell locator. No kernel of the reference
+ * corresponds; it replaces the host-side cKDTree query of nearest_sites() (sites.py:38-39), which finds the start
+ * site per camera centre (bench_infer.py:60, eval_scene.py:69, bench_fps.py:156) and per ray origin of a ray batch.
+ * Grid: res[0] x res[1] x res[2] cells of edge cell[a] from lo (host arrays of 3); cell (x, y, z) has index
+ * (z res[1] + y) res[0] + x, G = res[0] res[1] res[2] <= 4096^2.
+ *   points f32 (N, stride), xyz first; cell_start i32 (G + 1) and cell_sites i32 (N): the sites of cell g are
+ *   cell_sites[cell_start[g] .. cell_start[g + 1]), in no particular order; work i32 (vgr_grid_work_size(N, G)).
+ */
+int64_t vgr_grid_work_size(int64_t n_sites, int64_t n_cells);
+int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+                   const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work, void* stream);
+
+/*
+ * Nearest site of every query point: the lexicographic argmin of (float64 squared distance, site index), as
+ * cKDTree (float64) answers it up to exact distance ties.
+ *   queries f32 (m, 3) -> site i32 (m); the grid arguments as built by vgr_grid_build
+ */
+int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+                     const int32_t* res, const int32_t* cell_start, const int32_t* cell_sites, const float* queries,
+                     int64_t n_queries, int32_t* site, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

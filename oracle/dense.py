@@ -6,6 +6,7 @@ Independent restatements, in numpy float64, of the reference's own test oracles;
   march_samples / march_dense   test_march.py:14-22 and :59-79 (exact nearest site, NeRF compositing)
   density_dense / color_dense   test_grad.py:21-48, :92-104 (quaternion Mahalanobis, softmax blend)
   sh_basis              test_grad.py:21-32
+  nearest_brute         sites.py:38-39 (cKDTree nearest site), by exhaustive float64 search
 Every neighbourhood is the explicit set {c} U adj(c); nearest sites come from cKDTree, not from a walk.
 """
 
@@ -176,4 +177,19 @@ def color_dense(pts, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site):
 		a = np.exp(lw - lw.max())
 		a /= a.sum()
 		out[i] = a @ np.maximum(np.einsum('j,njc->nc', B[i], sh[nb]) + 0.5, 0)
+	return out
+
+
+def nearest_brute(points, queries):
+	"""Nearest site of every query point by exhaustive search: the lexicographic argmin of (float64 squared
+	distance (dx^2 + dy^2) + dz^2, site index). Restates nearest_sites (sites.py:38-39, scipy cKDTree in float64)
+	up to exact distance ties, which cKDTree leaves unspecified."""
+	p = np.asarray(points, np.float64)[:, :3]
+	q = np.asarray(queries, np.float64)
+	out = np.empty(len(q), np.int32)
+	chunk = max(1, int(2e7 // max(len(p), 1)))
+	for s in range(0, len(q), chunk):
+		v = q[s:s + chunk, None, :] - p[None]
+		d2 = (v[..., 0] * v[..., 0] + v[..., 1] * v[..., 1]) + v[..., 2] * v[..., 2]
+		out[s:s + chunk] = d2.argmin(1)  # first index among equal minima
 	return out

@@ -16,7 +16,7 @@ def declared():
 	text = open(HEADER).read()
 	text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
 	out = {}
-	for m in re.finditer(r'\b(?:int|const char\*)\s+(vgr_\w+)\s*\(([^)]*)\)\s*;', text):
+	for m in re.finditer(r'\b(?:int|int64_t|const char\*)\s+(vgr_\w+)\s*\(([^)]*)\)\s*;', text):
 		params = m.group(2).strip()
 		out[m.group(1)] = 0 if params in ('', 'void') else params.count(',') + 1
 	return out
@@ -25,7 +25,8 @@ def declared():
 def test_header_declares_the_entry_points():
 	names = declared()
 	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_march_forward', 'vgr_walk', 'vgr_density_forward',
-			  'vgr_color_forward', 'vgr_conic_forward', 'vgr_last_error', 'vgr_abi_version'):
+			  'vgr_color_forward', 'vgr_conic_forward', 'vgr_grid_work_size', 'vgr_grid_build', 'vgr_grid_nearest',
+			  'vgr_last_error', 'vgr_abi_version'):
 		assert n in names
 
 
@@ -57,3 +58,11 @@ def test_library_reports_argument_errors_without_a_gpu():
 	assert lib.vgr_foam_infer(*args) == 1 and b'null scene pointer' in lib.vgr_last_error()
 	with pytest.raises(RuntimeError, match='trace'):
 		_lib.call('vgr_foam_infer_traced', *args[:-1], None, 0, None)
+	# grid: geometry is validated before any launch; the work size is a closed form
+	f3, i3 = (ctypes.c_float * 3), (ctypes.c_int32 * 3)
+	assert lib.vgr_grid_work_size(100, 5000) == 100 + 5000 + 2 + 1
+	rc = lib.vgr_grid_nearest(None, 1, 3, f3(0, 0, 0), f3(1, 1, 1), i3(0, 1, 1), None, None, None, 5, None, None)
+	assert rc == 1 and b'res[0]' in lib.vgr_last_error()
+	rc = lib.vgr_grid_build(None, 1, 3, f3(0, 0, 0), f3(1, 1, -1), i3(1, 1, 1), None, None, None, None)
+	assert rc == 1 and b'cell edge 2' in lib.vgr_last_error()
+	assert lib.vgr_grid_nearest(None, 1, 3, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, None, 0, None, None) == 0

@@ -295,3 +295,24 @@ def test_sh_basis_known_values_and_orthonormality(oracle_lib):
 	B = np.stack([oracle.sh_basis(v, 3) for v in dirs[::4]]).astype(np.float64)
 	G = 4 * np.pi * B.T @ B / len(B)
 	np.testing.assert_allclose(G, np.eye(16), atol=2e-3)
+
+
+def test_nearest_brute_matches_ckdtree_and_closed_forms():
+	"""nearest_brute (the start-cell oracle) against scipy's cKDTree (the reference's nearest_sites, sites.py:38-39)
+	on uniform and clustered sites, queries inside and outside the cloud; closed forms on a lattice."""
+	from scipy.spatial import cKDTree
+	rng = np.random.default_rng(7)
+	uni = rng.uniform(-1, 1, (4000, 3)).astype(np.float32)
+	clu = (rng.normal(0, 0.05, (4000, 3)) + rng.uniform(-1, 1, (40, 3))[rng.integers(0, 40, 4000)]).astype(np.float32)
+	for pts in (uni, clu):
+		q = np.concatenate([rng.uniform(-1.2, 1.2, (3000, 3)), rng.normal(0, 4, (200, 3))]).astype(np.float32)
+		got = dense.nearest_brute(pts, q)
+		ref = cKDTree(pts.astype(np.float64)).query(q.astype(np.float64))[1]
+		np.testing.assert_array_equal(got, ref)
+	# lattice: the nearest site of a point in an open Voronoi cell of a unit lattice is its rounding
+	g = np.stack(np.meshgrid(*[np.arange(5.0)] * 3, indexing='ij'), -1).reshape(-1, 3).astype(np.float32)
+	q = rng.uniform(-0.4, 4.4, (500, 3)).astype(np.float32)
+	expect = (np.clip(np.rint(q), 0, 4) @ np.array([25, 5, 1])).astype(np.int32)
+	np.testing.assert_array_equal(dense.nearest_brute(g, q), expect)
+	# equidistant: ties go to the smaller index
+	assert dense.nearest_brute(np.array([[1, 0, 0], [-1, 0, 0]], np.float32), np.zeros((1, 3), np.float32))[0] == 0

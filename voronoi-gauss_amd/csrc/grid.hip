@@ -1,0 +1,279 @@
+// Uniform grid over the sites and exact nearest-site queries, gfx950: the start-cell locator of the traversals.
+//
+// The reference locates start cells on the host with scipy's cKDTree (sites.py:38-39, called per camera centre
+// in bench_infer.py:60 and eval_scene.py:69, and per ray origin for ray batches). Here the sites are binned into a
+// uniform grid by a counting sort on the GPU (histogram, exclusive scan, scatter), and each query scans Chebyshev
+// rings of grid cells around its own cell until no unscanned cell can hold a closer site. Distances are computed in
+// float64, as cKDTree computes them, and ties go to the smaller site index, so the answer is cKDTree's except
+// where two sites are at exactly the same float64 distance.
+#include "vgr_abi.h"
+#include "vgr_device.h"
+
+namespace vgr {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kScanThreads = 1024;                   // threads of a scan block
+constexpr int kScanItems = 4;                        // counts per scan thread
+constexpr int kScanTile = kScanThreads * kScanItems;  // counts per scan block
+constexpr int64_t kMaxCells = int64_t(kScanTile) * kScanTile;
+
+struct Geom {
+    float lo[3];    // grid origin
+    float cell[3];  // cell edge per axis
+    int res[3];     // cells per axis
+};
+
+__device__ __forceinline__ int axis_cell(float x, float lo, float cell, int res) {
+    const int c = static_cast<int>(floorf((x - lo) / cell));
+    return min(max(c, 0), res - 1);
+}
+
+__device__ __forceinline__ const float* site_ptr(const float* pts, int stride, int64_t i) { return pts + stride * i; }
+
+// Cell of every site, and the number of sites per cell.
+__global__ void __launch_bounds__(kBlock) grid_count(const float* __restrict__ pts, int stride, int64_t n, Geom g,
+                                                     int* __restrict__ cell_of, int* __restrict__ count) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const float* p = site_ptr(pts, stride, i);
+    const int cx = axis_cell(p[0], g.lo[0], g.cell[0], g.res[0]);
+    const int cy = axis_cell(p[1], g.lo[1], g.cell[1], g.res[1]);
+    const int cz = axis_cell(p[2], g.lo[2], g.cell[2], g.res[2]);
+    const int c = (cz * g.res[1] + cy) * g.res[0] + cx;
+    cell_of[i] = c;
+    atomicAdd(count + c, 1);
+}
+
+// Exclusive scan of one tile of kScanTile counts within the tile; the tile total goes to tile_sum.
+__global__ void __launch_bounds__(kScanThreads) scan_tiles(const int* __restrict__ count, int64_t n_cells,
+                                                           int* __restrict__ start, int* __restrict__ tile_sum) {
+    __shared__ int part[kScanThreads];
+    const int64_t base = int64_t(blockIdx.x) * kScanTile + int64_t(threadIdx.x) * kScanItems;
+    int v[kScanItems], sum = 0;
+#pragma unroll
+    for (int u = 0; u < kScanItems; ++u) {
+        v[u] = base + u < n_cells ? count[base + u] : 0;
+        sum += v[u];
+    }
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive scan of the thread sums
+        const int add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+        __syncthreads();
+        part[threadIdx.x] += add;
+        __syncthreads();
+    }
+    int run = part[threadIdx.x] - sum;
+#pragma unroll
+    for (int u = 0; u < kScanItems; ++u) {
+        if (base + u < n_cells) start[base + u] = run;
+        run += v[u];
+    }
+    if (threadIdx.x == kScanThreads - 1) tile_sum[blockIdx.x] = part[threadIdx.x];
+}
+
+// Exclusive scan of the tile totals (at most kScanTile of them) in place, by one block; the grand total goes to
+// tile_sum[n_tiles].
+__global__ void __launch_bounds__(kScanThreads) scan_tile_sums(int* __restrict__ tile_sum, int n_tiles) {
+    __shared__ int part[kScanThreads];
+    const int base = threadIdx.x * kScanItems;
+    int v[kScanItems], sum = 0;
+#pragma unroll
+    for (int u = 0; u < kScanItems; ++u) {
+        v[u] = base + u < n_tiles ? tile_sum[base + u] : 0;
+        sum += v[u];
+    }
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+        const int add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+        __syncthreads();
+        part[threadIdx.x] += add;
+        __syncthreads();
+    }
+    int run = part[threadIdx.x] - sum;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kScanItems; ++u) {
+        if (base + u < n_tiles) tile_sum[base + u] = run;
+        run += v[u];
+    }
+    if (threadIdx.x == kScanThreads - 1) tile_sum[n_tiles] = part[threadIdx.x];
+}
+
+// Adds the tile offsets: start becomes the global exclusive scan (start[n_cells] = total), and the count array is
+// overwritten with it, as the fill cursor.
+__global__ void __launch_bounds__(kBlock) scan_add(int* __restrict__ start, int* __restrict__ cursor, int64_t n_cells,
+                                                   const int* __restrict__ tile_sum, int n_tiles) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i < n_cells) {
+        const int s = start[i] + tile_sum[i / kScanTile];
+        start[i] = s;
+        cursor[i] = s;
+    } else if (i == n_cells) {
+        start[i] = tile_sum[n_tiles];
+    }
+}
+
+// Scatter: every site takes the next slot of its cell (the order within a cell is arbitrary; queries do not
+// depend on it).
+__global__ void __launch_bounds__(kBlock) grid_fill(int64_t n, const int* __restrict__ cell_of,
+                                                    int* __restrict__ cursor, int* __restrict__ cell_sites) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n) return;
+    cell_sites[atomicAdd(cursor + cell_of[i], 1)] = static_cast<int>(i);
+}
+
+// Nearest site of each query: lexicographic argmin of (float64 squared distance, site index).
+//
+// Rings r = 0, 1, ... of cells at Chebyshev distance r from the query's (clamped) cell are scanned. Every unscanned
+// site lies beyond a face of the scanned block that is not on the grid boundary, so after ring r no unscanned site
+// is closer than the distance lb from the query to the nearest such face; the scan stops once the best distance is
+// below lb (shrunk by a margin covering the float32 rounding of cell assignment), or when the block covers the
+// grid.
+__global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__ pts, int stride, Geom g,
+                                                       const int* __restrict__ cell_start,
+                                                       const int* __restrict__ cell_sites,
+                                                       const float* __restrict__ q, int64_t m, double margin,
+                                                       int* __restrict__ out) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= m) return;
+    const double qx = q[3 * i], qy = q[3 * i + 1], qz = q[3 * i + 2];
+    const int c[3] = {axis_cell(static_cast<float>(qx), g.lo[0], g.cell[0], g.res[0]),
+                      axis_cell(static_cast<float>(qy), g.lo[1], g.cell[1], g.res[1]),
+                      axis_cell(static_cast<float>(qz), g.lo[2], g.cell[2], g.res[2])};
+    const double qa[3] = {qx, qy, qz};
+    double best = 1e300;
+    int best_k = INT_MAX;
+    const auto visit = [&](int x, int y, int z) {
+        const int cell = (z * g.res[1] + y) * g.res[0] + x;
+        for (int s = cell_start[cell], e = cell_start[cell + 1]; s < e; ++s) {
+            const int k = cell_sites[s];
+            const float* p = site_ptr(pts, stride, k);
+            const double dx = qx - p[0], dy = qy - p[1], dz = qz - p[2];
+            const double d2 = dx * dx + dy * dy + dz * dz;
+            if (d2 < best || (d2 == best && k < best_k)) best = d2, best_k = k;
+        }
+    };
+    const int r_max = max(max(g.res[0], g.res[1]), g.res[2]);
+    for (int r = 0; r <= r_max; ++r) {
+        // the cells at Chebyshev distance exactly r, clipped to the grid: whole rows where z or y is on the shell,
+        // the two end cells of the other rows
+        const int z0 = max(c[2] - r, 0), z1 = min(c[2] + r, g.res[2] - 1);
+        const int y0 = max(c[1] - r, 0), y1 = min(c[1] + r, g.res[1] - 1);
+        const int x0 = max(c[0] - r, 0), x1 = min(c[0] + r, g.res[0] - 1);
+        for (int z = z0; z <= z1; ++z) {
+            for (int y = y0; y <= y1; ++y) {
+                if (z == c[2] - r || z == c[2] + r || y == c[1] - r || y == c[1] + r) {
+                    for (int x = x0; x <= x1; ++x) visit(x, y, z);
+                } else {
+                    if (c[0] - r >= 0) visit(c[0] - r, y, z);
+                    if (r > 0 && c[0] + r < g.res[0]) visit(c[0] + r, y, z);
+                }
+            }
+        }
+        double lb = 1e300;
+        bool open = false;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            if (c[a] - r > 0) lb = fmin(lb, qa[a] - (double(g.lo[a]) + double(c[a] - r) * g.cell[a])), open = true;
+            if (c[a] + r < g.res[a] - 1)
+                lb = fmin(lb, double(g.lo[a]) + double(c[a] + r + 1) * g.cell[a] - qa[a]), open = true;
+        }
+        if (!open) break;  // the scanned block covers the grid
+        lb -= margin;
+        if (lb > 0.0 && best < lb * lb) break;
+    }
+    out[i] = best_k;
+}
+
+Geom make_geom(const float* lo, const float* cell, const int32_t* res) {
+    Geom g{};
+    for (int a = 0; a < 3; ++a) g.lo[a] = lo[a], g.cell[a] = cell[a], g.res[a] = res[a];
+    return g;
+}
+
+int check_geom(const float* lo, const float* cell, const int32_t* res, int64_t* n_cells) {
+    VGR_REQUIRE(lo && cell && res, "grid: null geometry pointer");
+    int64_t g = 1;
+    for (int a = 0; a < 3; ++a) {
+        VGR_REQUIRE(res[a] >= 1 && res[a] <= 65536, "grid: res[%d] must be in [1, 65536] (got %d)", a, res[a]);
+        VGR_REQUIRE(cell[a] > 0.f, "grid: cell edge %d must be > 0", a);
+        g *= res[a];
+    }
+    VGR_REQUIRE(g <= kMaxCells, "grid: at most %lld cells (got %lld)", static_cast<long long>(kMaxCells),
+                static_cast<long long>(g));
+    *n_cells = g;
+    return VGR_OK;
+}
+
+}  // namespace
+}  // namespace vgr
+
+extern "C" int64_t vgr_grid_work_size(int64_t n_sites, int64_t n_cells) {
+    const int64_t tiles = (n_cells + vgr::kScanTile - 1) / vgr::kScanTile;
+    return n_sites + n_cells + tiles + 1;
+}
+
+extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+                              const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work,
+                              void* stream) {
+    using namespace vgr;
+    int64_t n_cells = 0;
+    if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
+    VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "grid_build: n_sites must be in [0, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    VGR_REQUIRE(stride >= 3, "grid_build: stride must be >= 3 floats (got %d)", stride);
+    VGR_REQUIRE(cell_start && work && (n_sites == 0 || (points && cell_sites)), "grid_build: null pointer");
+    const hipStream_t s = as_stream(stream);
+    const Geom g = make_geom(lo, cell, res);
+    int* cell_of = work;
+    int* count = work + n_sites;
+    int* tile_sum = count + n_cells;
+    const int n_tiles = static_cast<int>((n_cells + kScanTile - 1) / kScanTile);
+    if (hipMemsetAsync(count, 0, sizeof(int) * n_cells, s) != hipSuccess) return launch_status("grid_build memset");
+    if (n_sites > 0) {
+        hipLaunchKernelGGL(grid_count, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, s, points, int(stride),
+                           n_sites, g, cell_of, count);
+        if (int rc = launch_status("grid_count")) return rc;
+    }
+    hipLaunchKernelGGL(scan_tiles, dim3(n_tiles), dim3(kScanThreads), 0, s, count, n_cells, cell_start, tile_sum);
+    if (int rc = launch_status("scan_tiles")) return rc;
+    hipLaunchKernelGGL(scan_tile_sums, dim3(1), dim3(kScanThreads), 0, s, tile_sum, n_tiles);
+    if (int rc = launch_status("scan_tile_sums")) return rc;
+    hipLaunchKernelGGL(scan_add, dim3(grid_for(n_cells + 1, kBlock)), dim3(kBlock), 0, s, cell_start, count, n_cells,
+                       tile_sum, n_tiles);
+    if (int rc = launch_status("scan_add")) return rc;
+    if (n_sites > 0) {
+        hipLaunchKernelGGL(grid_fill, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, s, n_sites, cell_of, count,
+                           cell_sites);
+        return launch_status("grid_fill");
+    }
+    return VGR_OK;
+}
+
+extern "C" int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t stride, const float* lo,
+                                const float* cell, const int32_t* res, const int32_t* cell_start,
+                                const int32_t* cell_sites, const float* queries, int64_t n_queries, int32_t* site,
+                                void* stream) {
+    using namespace vgr;
+    int64_t n_cells = 0;
+    if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
+    VGR_REQUIRE(n_queries >= 0, "grid_nearest: n_queries must be >= 0");
+    if (n_queries == 0) return VGR_OK;
+    VGR_REQUIRE(n_sites >= 1 && n_sites <= INT_MAX, "grid_nearest: n_sites must be in [1, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    VGR_REQUIRE(stride >= 3, "grid_nearest: stride must be >= 3 floats (got %d)", stride);
+    VGR_REQUIRE(points && cell_start && cell_sites && queries && site, "grid_nearest: null pointer");
+    // float32 cell assignment can put a site one rounding step across a cell face: shrink the stopping bound by
+    // a few float32 ulps of the grid's extent
+    double extent = 0.0;
+    for (int a = 0; a < 3; ++a)
+        extent = fmax(extent, fabs(double(lo[a])) + double(cell[a]) * res[a]);
+    const double margin = extent * 1e-6;
+    const Geom g = make_geom(lo, cell, res);
+    hipLaunchKernelGGL(grid_nearest, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream), points,
+                       int(stride), g, cell_start, cell_sites, queries, n_queries, margin, site);
+    return launch_status("grid_nearest");
+}

@@ -26,11 +26,14 @@ SIGNATURES = {
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
+	'vgr_grid_work_size': [_I64, _I64],
+	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
+	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
 	'vgr_abi_version': [],
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _lib = None
 
 
@@ -46,6 +49,7 @@ def load():
 			fn.argtypes = argtypes
 			fn.restype = ctypes.c_int
 		lib.vgr_last_error.restype = ctypes.c_char_p
+		lib.vgr_grid_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

@@ -1,7 +1,8 @@
 """Site graph of the field: Delaunay (Voronoi-neighbour) adjacency as int32 CSR, and nearest-site queries.
 
 Mirrors sites.py:24-45 of the reference (delaunay_graph, nearest_sites, neighbor_spacing); both use scipy's
-Qhull Delaunay and cKDTree, so the scene a caller builds here is the scene the reference would build."""
+Qhull Delaunay and cKDTree, so the scene a caller builds here is the scene the reference would build. On CUDA
+tensors nearest_sites runs on the GPU instead (vgr.grid)."""
 
 import numpy as np
 from scipy.spatial import Delaunay, cKDTree
@@ -23,7 +24,12 @@ def delaunay_graph(points):
 
 
 def nearest_sites(points, queries):
-	"""Index of the nearest site of every query point (sites.py:38-39)."""
+	"""Index of the nearest site of every query point (sites.py:38-39). numpy arrays: scipy's cKDTree, as the
+	reference does; CUDA tensors: the GPU grid of vgr.grid.SiteGrid (the same answers up to exact distance ties,
+	which go to the smaller index), returned as an int32 CUDA tensor."""
+	if getattr(points, 'is_cuda', False):
+		from .grid import SiteGrid
+		return SiteGrid(points.contiguous()).nearest(queries.contiguous())
 	return cKDTree(points).query(queries)[1].astype(np.int32)
 
 
