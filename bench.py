@@ -7,6 +7,10 @@ resident in HBM. Prints one JSON line: Mrays/s (value), ms per step, FPS at 1080
 on the launch stream) and the CPU oracle timed on the host on a bounded, deterministic subset of the same rays.
 
   python bench.py [--steps K] [--warmup W] [--colors exact|fused] [--no-reorder] [--cpu-seconds S]
+
+Other rows of the path, each as one JSON line of the same form (not the headline):
+  --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
+  --workload locate   start-cell location on config 5 (nearest site of 16,777,216 ray origins among 4M sites)
 """
 
 import argparse
@@ -84,8 +88,8 @@ def distinct_blended_sites(fi, pack, args_of, n_rays, sh_deg, tiles=256):
 def main():
 	ap = argparse.ArgumentParser()
 	ap.add_argument('--gpus', type=int, default=1)
-	ap.add_argument('--steps', type=int, default=20)
-	ap.add_argument('--warmup', type=int, default=3)
+	ap.add_argument('--steps', type=int, default=None, help='timed steps (default 20; march: 3)')
+	ap.add_argument('--warmup', type=int, default=None, help='untimed steps (default 3; march: 1)')
 	ap.add_argument('--config', type=int, default=3)
 	ap.add_argument('--scale', type=float, default=1.0, help='site-count scale (1 = the BASELINE config)')
 	ap.add_argument('--colors', default='fused', choices=['exact', 'fused'],
@@ -94,13 +98,26 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
+	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate'],
+					help='foam: the headline (foam_infer, config 3); march / locate: the other rows, on config 5')
 	args = ap.parse_args()
+	if args.steps is None:
+		args.steps = 3 if args.workload == 'march' else 20
+	if args.warmup is None:
+		args.warmup = 1 if args.workload == 'march' else 3
 	if args.gpus != 1:
 		print(f'bench.py renders on one GPU only (got --gpus {args.gpus}): rays are independent, so N GPUs would '
 			  f'each render 1/N of the cameras with a replicated scene; multi-GPU runs are not part of this build.',
 			  file=sys.stderr)
 		sys.exit(2)
+	if args.workload == 'march':
+		return bench_march(args)
+	if args.workload == 'locate':
+		return bench_locate(args)
+	bench_foam(args)
 
+
+def bench_foam(args):
 	import numpy as np
 	import torch
 
@@ -222,6 +239,170 @@ def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu
 			'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), exact colours, C/OpenMP '
 					  f'thread per ray',
 			'parity_max_abs_rgb': err, 'parity_max_abs_T': errT}
+
+
+def time_steps(call, steps, warmup, stream):
+	"""Runs `call` warmup times, then times `steps` calls with HIP events on `stream` -> (per-call ms list, last
+	output, wall ms per step)."""
+	import torch
+	out = None
+	for _ in range(warmup):
+		out = call()
+	torch.cuda.synchronize()
+	ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+	torch.cuda.synchronize()
+	wall0 = time.perf_counter()
+	for a, b in ev:
+		a.record(stream)
+		out = call()
+		b.record(stream)
+	torch.cuda.synchronize()
+	wall = (time.perf_counter() - wall0) * 1e3 / steps
+	return [a.elapsed_time(b) for a, b in ev], out, wall
+
+
+def emit(metric, value, unit, args, ms, config, roofline, cpu, dtype='f32'):
+	res = {'metric': metric, 'value': round(value, 3), 'unit': unit, 'n_gpus': 1, 'steps': args.steps,
+		   'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': True, 'scaling': 'weak',
+		   'vs_baseline': None, 'dtype': dtype, 'data': 'synthetic', 'config': config, 'roofline': roofline,
+		   'cpu_baseline': cpu}
+	print(json.dumps(res), flush=True)
+
+
+def bench_locate(args):
+	"""Start-cell location for config 5: the nearest of 4,000,000 sites for each of the 16,777,216 ray origins
+	(vgr_grid_nearest over a grid built once, outside the timed region). CPU baseline: the reference's own
+	nearest_sites (scipy cKDTree, sites.py:38-39, single-threaded as called there) on a bounded sample."""
+	import numpy as np
+	import torch
+
+	from vgr import grid, scenes
+	dev = torch.device('cuda:0')
+	pts_np = scenes.site_points(5, args.scale)
+	o_np, _ = scenes.ray_batch(5)
+	pts, q = torch.from_numpy(pts_np).to(dev), torch.from_numpy(o_np).to(dev)
+	N, B = len(pts), len(q)
+	log(f'config 5 sites {N}, ray origins {B}')
+	stream = torch.cuda.current_stream(dev)
+	build_ms, g, _ = time_steps(lambda: grid.SiteGrid(pts), 3, 1, stream)
+	n_cells = g.res[0] * g.res[1] * g.res[2]
+	launch_ms, out, wall = time_steps(lambda: g.nearest(q), args.steps, args.warmup, stream)
+	ms = float(np.mean(launch_ms))
+	log(f'grid {g.res} ({n_cells} cells) built in {np.mean(build_ms):.3f} ms; {args.steps} queries launches: '
+		f'mean {ms:.3f} ms, wall {wall:.3f} ms/step')
+	# compulsory bytes of one launch: query in (12 B), site out (4 B); the grid and points read once
+	abytes = 16.0 * B + 16.0 * N + 4.0 * N + 4.0 * (n_cells + 1)
+	achieved = abytes / (ms * 1e-3) / 1e9
+	cpu = None
+	if args.cpu_seconds > 0:
+		from scipy.spatial import cKDTree
+		t0 = time.perf_counter()
+		tree = cKDTree(pts_np)
+		t_build = time.perf_counter() - t0
+		probe = o_np[:20000]
+		t0 = time.perf_counter()
+		tree.query(probe)
+		rate = len(probe) / (time.perf_counter() - t0)
+		k = max(1, int(B / (rate * args.cpu_seconds)))
+		sel = np.arange(0, B, k)
+		t0 = time.perf_counter()
+		ref = tree.query(o_np[sel])[1]
+		t = time.perf_counter() - t0
+		mism = int((out.cpu().numpy()[sel] != ref).sum())
+		log(f'cpu cKDTree: build {t_build:.2f} s, {len(sel)} queries (every {k}th) in {t:.2f} s; '
+			f'{mism} mismatches against the GPU')
+		cpu = {'value': round(len(sel) / t / 1e6, 4), 'unit': 'Mqueries/s', 'cores': 1, 'kind': 'reference',
+			   'sample': f'every {k}th of the {B} ray origins ({len(sel)} queries), scipy cKDTree.query as in the '
+						 f'reference nearest_sites (sites.py:38-39), single-threaded; tree build {t_build:.2f} s '
+						 f'not included', 'parity_mismatches': mism}
+	emit('Mqueries/s nearest-site start location (config 5: 4M sites, 16.7M ray origins) on 1 MI355X', B / ms / 1e3,
+		 'Mqueries/s', args, ms,
+		 {'workload': f'config 5 start cells: nearest of {N} sites (seeded uniform draw) for each of {B} ray '
+					  f'origins', 'sites': N, 'queries': B, 'grid_res': g.res, 'grid_build_ms': round(float(np.mean(build_ms)), 3)},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+
+
+def bench_march(args):
+	"""march_forward on config 5: 4,000,000 uniform sites of low density (no early termination), 16,777,216
+	incoherent rays from inside [-0.9, 0.9]^3, start sites from the GPU grid, dt = 1/512 inside the unit ball and 64
+	disparity steps beyond (render.py:109-124 defaults). CPU baseline: the C/OpenMP oracle on a bounded sample."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, grid, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	t0 = time.time()
+	sc = scenes.make_scene(5, scale=args.scale, log=log)
+	log(f'scene config 5: {sc.n_sites} sites ({time.time() - t0:.0f} s)')
+	model = VoronoiGaussField.from_scene(sc, dev)
+	o_np, d_np = sc.ray_batch
+	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
+	start = grid.SiteGrid(model.graph.points).nearest(o)
+	dt, n_bg = 1 / 512, 64
+	near, mid, far = render.ray_bounds(o, d, 0.02, sc.far_radius)
+	floor = 0.5 * dt
+	dA = ext.conic(model.d_log_scale, model.d_quat, floor)
+	cA = ext.conic(model.c_log_scale, model.c_quat, floor)
+	sh = model.sh().contiguous()
+	B = len(o)
+	me = ext.march_extension()
+	args_of = lambda sel=slice(None): (model.graph.points, model.graph.offsets, model.graph.adj, model.raw, dA, cA, sh,  # noqa
+									   sc.sh_deg, o[sel], d[sel], start[sel], near[sel], mid[sel], far[sel], dt, n_bg,
+									   1e-4, 1e-4)
+	stream = torch.cuda.current_stream(dev)
+	launch_ms, out, wall = time_steps(lambda: me.march_forward(*args_of()), args.steps, args.warmup, stream)
+	ms = float(np.mean(launch_ms))
+	rgb, T, depth, stats = out
+	st = stats.double()
+	log(f'{args.steps} steps: mean {ms:.3f} ms, wall {wall:.3f} ms/step; samples/ray {st[:, 0].mean():.1f}, '
+		f'coloured {st[:, 1].mean():.1f}, walk steps {st[:, 2].mean():.1f}')
+	E = 1.0 + len(sc.adj) / sc.n_sites  # mean self-inclusive neighbourhood
+	SHB = 12 * (sc.sh_deg + 1) ** 2
+	# per sample: walk steps (8 + 16 E) each, density (8 + E (16 + 28)), colour when active E (24 + SHB); rays 56 B
+	abytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) + st[:, 1].sum() * E * (24 + SHB))
+	achieved = abytes / (ms * 1e-3) / 1e9
+	cpu = None
+	if args.cpu_seconds > 0:
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		host = [x.cpu().numpy() for x in (model.graph.points, model.graph.offsets, model.graph.adj, model.raw, dA, cA,
+										  sh)]
+		rays = [x.cpu().numpy() for x in (o, d, start, near, mid, far)]
+		probe = np.arange(0, B, max(1, B // 2000), dtype=np.int64)
+		r = oracle.march_forward(*host, sc.sh_deg, *rays, dt, n_bg, rays=probe)
+		rate = len(probe) / max(r['seconds'], 1e-6)
+		k = max(1, int(B / (rate * args.cpu_seconds)))
+		sel = np.arange(0, B, k, dtype=np.int64)
+		r = oracle.march_forward(*host, sc.sh_deg, *rays, dt, n_bg, rays=sel)
+		err = float(np.abs(r['rgb'] - rgb.cpu().numpy()[sel]).max())
+		errT = float(np.abs(r['T'] - T.cpu().numpy()[sel]).max())
+		# the same rays with the thresholds off (t_thresh = 0, w_thresh = -1): every sample coloured, no early stop,
+		# so no decision can flip on the few-ulp difference between the device exp and the host's
+		sub = sel[:: max(1, len(sel) // 20000)]
+		gs = me.march_forward(*args_of(torch.from_numpy(sub).to(dev))[:-2], 0.0, -1.0)
+		rs = oracle.march_forward(*host, sc.sh_deg, *rays, dt, n_bg, t_thresh=0.0, w_thresh=-1.0, rays=sub)
+		err_off = float(np.abs(rs['rgb'] - gs[0].cpu().numpy()).max())
+		errT_off = float(np.abs(rs['T'] - gs[1].cpu().numpy()).max())
+		log(f'cpu oracle: {len(sel)} rays (every {k}th) in {r["seconds"]:.2f} s on {oracle.max_threads()} threads; '
+			f'max |rgb - gpu| {err:.2e}, max |T - gpu| {errT:.2e}; thresholds off ({len(sub)} rays): '
+			f'{err_off:.2e}, {errT_off:.2e}')
+		cpu = {'value': round(len(sel) / r['seconds'] / 1e6, 5), 'unit': 'Mrays/s', 'cores': oracle.max_threads(),
+			   'kind': 'port', 'sample': f'every {k}th ray of the same {B}-ray batch ({len(sel)} rays), C/OpenMP '
+										 f'thread per ray', 'parity_max_abs_rgb': err, 'parity_max_abs_T': errT,
+			   'parity_thresholds_off_max_abs_rgb': err_off, 'parity_thresholds_off_max_abs_T': errT_off,
+			   'parity_note': 'with w_thresh = 1e-4 many config-5 samples have weight within ulps of the threshold, so '
+							  'device and host exp (the reference uses __expf, march.cu:241) colour slightly different '
+							  'sample sets; the thresholds-off figures compare the arithmetic'}
+	emit('Mrays/s march_forward (config 5: 4M sites, 16.7M incoherent rays) on 1 MI355X', B / ms / 1e3, 'Mrays/s',
+		 args, ms,
+		 {'workload': f'config 5 march: {sc.n_sites} sites, {B} rays, dt 1/512 inside the unit ball + {n_bg} '
+					  f'disparity steps, starts from the GPU grid', 'sites': sc.n_sites, 'rays': B,
+		  'samples_per_ray': round(float(st[:, 0].mean()), 2), 'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
+		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4)},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
 
 
 if __name__ == '__main__':

@@ -225,6 +225,8 @@ def load_geometry(config, n_sites=None, cache_dir=DEFAULT_CACHE, log=print):
 	p, cls = _geometry(config, n, rng)
 	p32 = p.astype(np.float32)
 	t0 = time.time()
+	if log:
+		log(f'[scene] config {config}: Delaunay of {n} sites (Qhull) ...')
 	pts, idx, offsets, adj = delaunay_graph(p32.astype(np.float64))
 	if log:
 		log(f'[scene] config {config}: Delaunay of {n} sites in {time.time() - t0:.1f} s, mean degree '
@@ -271,8 +273,22 @@ def make_scene(config, scale=1.0, img_scale=1.0, n_rays=None, cache_dir=DEFAULT_
 				  quat=quat, sh=sh.astype(np.float32), sh_deg=sh_deg, far_radius=55.0 if config == 4 else 4.0,
 				  cameras=_cameras(config, img_scale))
 	if config == 5:
-		B = 16_777_216 if n_rays is None else int(n_rays)
-		rr = np.random.default_rng(2000 + SEEDS[config])
-		o = rr.uniform(-0.9, 0.9, (B, 3)).astype(np.float32)
-		scene.ray_batch = (o, _unit(rr, B).astype(np.float32))
+		scene.ray_batch = ray_batch(config, n_rays)
 	return scene
+
+
+def ray_batch(config=5, n_rays=None):
+	"""The seeded ray batch of config 5: origins uniform in [-0.9, 0.9]^3, directions uniform on S^2 ->
+	(o, d) float32 (B, 3), B = 16,777,216 unless n_rays is given."""
+	B = 16_777_216 if n_rays is None else int(n_rays)
+	rr = np.random.default_rng(2000 + SEEDS[config])
+	o = rr.uniform(-0.9, 0.9, (B, 3)).astype(np.float32)
+	return o, _unit(rr, B).astype(np.float32)
+
+
+def site_points(config, scale=1.0):
+	"""The seeded site draw of a config before triangulation (float32 (n, 3)): what the start-cell locator needs,
+	without the Qhull step (which only drops coincident points)."""
+	n = max(64, int(round(SITE_COUNTS[config] * scale)))
+	p, _ = _geometry(config, n, np.random.default_rng(SEEDS[config]))
+	return p.astype(np.float32)
