@@ -11,6 +11,8 @@ on the launch stream) and the CPU oracle timed on the host on a bounded, determi
 Other rows of the path, each as one JSON line of the same form (not the headline):
   --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
   --workload locate   start-cell location on config 5 (nearest site of 16,777,216 ray origins among 4M sites)
+  --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
+                      one 1920x1080 frame at 64 stratified samples per ray (render_rays' first round)
 """
 
 import argparse
@@ -98,8 +100,9 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
-	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate'],
-					help='foam: the headline (foam_infer, config 3); march / locate: the other rows, on config 5')
+	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field'],
+					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
+						 'the other rows')
 	args = ap.parse_args()
 	if args.steps is None:
 		args.steps = 3 if args.workload == 'march' else 20
@@ -114,6 +117,8 @@ def main():
 		return bench_march(args)
 	if args.workload == 'locate':
 		return bench_locate(args)
+	if args.workload == 'field':
+		return bench_field(args)
 	bench_foam(args)
 
 
@@ -403,6 +408,117 @@ def bench_march(args):
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+
+
+def bench_field(args):
+	"""The field operators of the NeRF path on config 3, one 1920x1080 frame (2,073,600 rays) at 64 stratified
+	samples per ray, as the first round of render_rays (render.py:77-106): walk to the sample sites, density at
+	every sample, colour at the samples whose compositing weight exceeds 1e-4; conic_forward over all sites.
+	value = samples per second through walk + density + colour. Each operator is timed on its own with HIP events
+	and beside the C/OpenMP oracle on a bounded sample.
+
+	Algorithmic bytes (cache-oblivious; E = mean self-inclusive neighbourhood, SHB = 192 B at SH degree 3):
+	  walk     per sample (1 + walk steps) (8 + 16 E) + 8     (offsets; point 12 + adj 4 per neighbour; z in, site out)
+	  density  per sample 28 + 48 E    (x, site, sigma, offsets; point 12 + adj 4 + raw 4 + log_scale 12 + quat 16)
+	  colour   per active sample 48 + E (44 + SHB)   (x, dir, site, rgb, offsets; point, adj, log_scale, quat, SH)
+	  conic    per site 60 (log_scale 12 + quat 16 in, A 24 out)."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	t0 = time.time()
+	sc = scenes.make_scene(3, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	g = model.graph
+	cam = sc.cameras[0]
+	o_np, d_np = cam.rays()
+	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
+	from vgr.sites import nearest_sites
+	start = nearest_sites(g.points, torch.tensor(cam.eye, dtype=torch.float32, device=dev)[None]).expand(len(o)).contiguous()
+	B, S = len(o), 64
+	bounds = render.ray_bounds(o, d, 0.02, sc.far_radius)
+	s_grid = (torch.linspace(0, 1, S + 1, device=dev)[:-1] + 0.5 / S).expand(B, S).contiguous()
+	t = render.s_to_t(s_grid, *bounds).contiguous()
+	fx = ext.extension()
+	sh = model.sh().contiguous()
+	stream = torch.cuda.current_stream(dev)
+	log(f'config 3 frame: {B} rays x {S} samples, {sc.n_sites} sites ({time.time() - t0:.0f} s)')
+	walk_ms, (site, steps), _ = time_steps(lambda: fx.walk(g.points, g.offsets, g.adj, o, d, t, start), args.steps,
+										   args.warmup, stream)
+	x = (o[:, None] + d[:, None] * t[..., None]).reshape(-1, 3).contiguous()
+	site_f = site.reshape(-1).contiguous()
+	dens_ms, sigma, _ = time_steps(lambda: fx.density_forward(g.points, g.offsets, g.adj, model.raw, model.d_log_scale,
+															  model.d_quat, x, site_f, 1.0), args.steps, args.warmup,
+								   stream)
+	w, _ = render.composite(sigma.view(B, S), t, bounds[2])
+	active = (w.reshape(-1) > 1e-4).nonzero().squeeze(1)
+	xa = x[active].contiguous()
+	da = d[:, None].expand(B, S, 3).reshape(-1, 3)[active].contiguous()
+	sa = site_f[active].contiguous()
+	col_ms, rgb, _ = time_steps(lambda: fx.color_forward(g.points, g.offsets, g.adj, model.c_log_scale, model.c_quat,
+														 sh, sc.sh_deg, xa, da, sa), args.steps, args.warmup, stream)
+	con_ms, _, _ = time_steps(lambda: fx.conic_forward(model.d_log_scale, model.d_quat, 0.0), args.steps, args.warmup,
+							  stream)
+	ms = {k: float(np.mean(v)) for k, v in (('walk', walk_ms), ('density', dens_ms), ('color', col_ms),
+											('conic', con_ms))}
+	m, ma = B * S, len(active)
+	E = 1.0 + len(sc.adj) / sc.n_sites
+	SHB = 12 * (sc.sh_deg + 1) ** 2
+	nb = {'walk': float((m + steps.double().sum()) * (8 + 16 * E) + 8 * m), 'density': m * (28 + 48 * E),
+		  'color': ma * (48 + E * (44 + SHB)), 'conic': sc.n_sites * 60.0}
+	gbs = {k: nb[k] / (ms[k] * 1e-3) / 1e9 for k in ms}
+	log('  '.join(f'{k} {ms[k]:.3f} ms ({gbs[k]:.0f} GB/s)' for k in ms) + f'; active samples {ma} of {m}')
+	top = max(('walk', 'density', 'color'), key=lambda k: ms[k])
+	cpu = None
+	if args.cpu_seconds > 0:
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		host = {k: v.cpu().numpy() for k, v in (('p', g.points), ('off', g.offsets), ('adj', g.adj), ('raw', model.raw),
+												('dls', model.d_log_scale), ('dq', model.d_quat),
+												('cls', model.c_log_scale), ('cq', model.c_quat), ('sh', sh))}
+		# bounded samples, about args.cpu_seconds of host time in all at the measured oracle rates
+		k_w = max(1, int(round(5.0 / max(args.cpu_seconds, 1e-3))))
+		rays = np.arange(0, B, k_w)
+		t1 = time.perf_counter()
+		ws = oracle.walk(host['p'], host['off'], host['adj'], o_np[rays], d_np[rays], t.cpu().numpy()[rays],
+						 start.cpu().numpy()[rays])
+		t_walk = time.perf_counter() - t1
+		walk_ok = bool((ws[0] == site.cpu().numpy()[rays]).all())
+		x_np, s_np = x.cpu().numpy(), site_f.cpu().numpy()
+		samp = np.arange(0, m, max(1, int(round(30.0 / max(args.cpu_seconds, 1e-3)))))
+		t1 = time.perf_counter()
+		sg = oracle.density(host['p'], host['off'], host['adj'], host['raw'], host['dls'], host['dq'], x_np[samp],
+							s_np[samp])
+		t_dens = time.perf_counter() - t1
+		err_s = float(np.abs(sg - sigma.cpu().numpy()[samp]).max() / max(1.0, float(np.abs(sg).max())))
+		ca = np.arange(0, ma, max(1, int(round(30.0 / max(args.cpu_seconds, 1e-3)))))
+		t1 = time.perf_counter()
+		cg = oracle.color(host['p'], host['off'], host['adj'], host['cls'], host['cq'], host['sh'], sc.sh_deg,
+						  xa.cpu().numpy()[ca], da.cpu().numpy()[ca], sa.cpu().numpy()[ca])
+		t_col = time.perf_counter() - t1
+		err_c = float(np.abs(cg - rgb.cpu().numpy()[ca]).max())
+		# host seconds for the whole frame, each operator's sample rate scaled to its full count
+		t_frame = t_walk * m / (len(rays) * S) + t_dens * m / len(samp) + t_col * ma / len(ca)
+		log(f'cpu oracle ({oracle.max_threads()} threads): walk {len(rays)} rays x {S} in {t_walk:.2f} s (sites equal: '
+			f'{walk_ok}), density {len(samp)} samples in {t_dens:.2f} s (max rel err {err_s:.2e}), colour {len(ca)} '
+			f'samples in {t_col:.2f} s (max abs err {err_c:.2e}); {t_frame:.1f} s per frame')
+		cpu = {'value': round(m / t_frame / 1e6, 4),
+			   'unit': 'Msamples/s', 'cores': oracle.max_threads(), 'kind': 'port',
+			   'sample': f'walk: every {k_w}th ray ({len(rays)} x {S} samples); density: {len(samp)} samples; colour: '
+						 f'{len(ca)} active samples; each rate scaled to the full frame',
+			   'parity_walk_sites_equal': walk_ok, 'parity_density_max_rel': err_s, 'parity_color_max_abs': err_c}
+	total = ms['walk'] + ms['density'] + ms['color']
+	emit('Msamples/s NeRF-path field operators walk + density + colour (config 3, 1080p, 64 samples/ray) on 1 MI355X',
+		 m / total / 1e3, 'Msamples/s', args, total,
+		 {'workload': f'config 3, camera 0: {B} rays x {S} stratified samples ({m}), colour at the {ma} samples of '
+					  f'weight > 1e-4; conic over {sc.n_sites} sites', 'samples': m, 'active_samples': ma,
+		  'ms': {k: round(v, 3) for k, v in ms.items()}, 'GBps': {k: round(v, 1) for k, v in gbs.items()},
+		  'walk_steps_per_sample': round(float(steps.double().sum()) / m, 3)},
+		 {'bound': 'hbm', 'kernel': f'{top}_forward' if top != 'walk' else 'walk', 'achieved': round(gbs[top], 1),
+		  'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs[top] / HBM_PEAK_GBS, 4), 'traffic': None,
+		  'algorithmic_bytes_per_launch': nb[top]}, cpu)
 
 
 if __name__ == '__main__':

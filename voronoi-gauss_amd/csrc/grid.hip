@@ -128,10 +128,10 @@ __global__ void __launch_bounds__(kBlock) grid_fill(int64_t n, const int* __rest
 // Nearest site of each query: lexicographic argmin of (float64 squared distance, site index).
 //
 // Rings r = 0, 1, ... of cells at Chebyshev distance r from the query's (clamped) cell are scanned. Every unscanned
-// site lies beyond a face of the scanned block that is not on the grid boundary, so after ring r no unscanned site
-// is closer than the distance lb from the query to the nearest such face; the scan stops once the best distance is
-// below lb (shrunk by a margin covering the float32 rounding of cell assignment), or when the block covers the
-// grid.
+// site lies in the grid box beyond a face of the scanned block that is not on the grid boundary, so after ring r
+// no unscanned site is closer than the distance lb from the query to the nearest such region (for a query outside
+// the grid, that includes its distance to the grid); the scan stops once the best distance is below lb (shrunk by
+// a margin covering the float32 rounding of cell assignment), or when the block covers the grid.
 __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__ pts, int stride, Geom g,
                                                        const int* __restrict__ cell_start,
                                                        const int* __restrict__ cell_sites,
@@ -173,16 +173,32 @@ __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__
                 }
             }
         }
-        double lb = 1e300;
+        // unscanned sites lie in the grid box beyond an open face of the scanned block: the squared distance from
+        // the query to each such region (an axis-aligned box) bounds theirs
+        double lb2 = 1e300;
         bool open = false;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
-            if (c[a] - r > 0) lb = fmin(lb, qa[a] - (double(g.lo[a]) + double(c[a] - r) * g.cell[a])), open = true;
-            if (c[a] + r < g.res[a] - 1)
-                lb = fmin(lb, double(g.lo[a]) + double(c[a] + r + 1) * g.cell[a] - qa[a]), open = true;
+#pragma unroll
+            for (int side = 0; side < 2; ++side) {
+                if (side == 0 ? c[a] - r <= 0 : c[a] + r >= g.res[a] - 1) continue;  // on the grid boundary
+                open = true;
+                double d2 = 0.0;
+#pragma unroll
+                for (int b = 0; b < 3; ++b) {
+                    double lo = g.lo[b], hi = double(g.lo[b]) + double(g.res[b]) * g.cell[b];
+                    if (b == a) {
+                        if (side == 0) hi = double(g.lo[a]) + double(c[a] - r) * g.cell[a];
+                        else lo = double(g.lo[a]) + double(c[a] + r + 1) * g.cell[a];
+                    }
+                    const double gap = fmax(fmax(lo - qa[b], qa[b] - hi), 0.0);
+                    d2 += gap * gap;
+                }
+                lb2 = fmin(lb2, d2);
+            }
         }
         if (!open) break;  // the scanned block covers the grid
-        lb -= margin;
+        const double lb = sqrt(lb2) - margin;
         if (lb > 0.0 && best < lb * lb) break;
     }
     out[i] = best_k;
