@@ -94,8 +94,12 @@ def main():
 	ap.add_argument('--warmup', type=int, default=None, help='untimed steps (default 3; march: 1)')
 	ap.add_argument('--config', type=int, default=3)
 	ap.add_argument('--scale', type=float, default=1.0, help='site-count scale (1 = the BASELINE config)')
-	ap.add_argument('--colors', default='fused', choices=['exact', 'fused'],
-				help='exact colour modes (eps_color = 0): lazy second pass or fused online blend')
+	ap.add_argument('--colors', default='fused', choices=['exact', 'fused', 'baked'],
+				help='exact colour modes (eps_color = 0): lazy second pass or fused online blend; baked: per-view '
+					 'site colours, baked per camera inside the timed step (approximate)')
+	ap.add_argument('--sh-half', action='store_true', help='fp16 SH coefficients (approximate)')
+	ap.add_argument('--eps-color', type=float, default=0.0, help='skip colour terms of relative weight < eps')
+	ap.add_argument('--eps-density', type=float, default=0.0, help='skip density terms below eps')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
@@ -134,7 +138,8 @@ def bench_foam(args):
 	sc = scenes.make_scene(args.config, scale=args.scale, log=log)
 	log(f'scene config {args.config}: {sc.n_sites} sites, {len(sc.adj)} adjacency entries ({time.time() - t0:.0f} s)')
 	model = VoronoiGaussField.from_scene(sc, dev)
-	pack = render.pack_foam(model, reorder=not args.no_reorder)
+	fast = args.sh_half or args.eps_color > 0 or args.eps_density > 0 or args.colors == 'baked'
+	pack = render.pack_foam(model, reorder=not args.no_reorder, sh_half=args.sh_half, eps_density=args.eps_density)
 	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile)
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	start = torch.from_numpy(start_np).to(dev)
@@ -144,12 +149,27 @@ def bench_foam(args):
 	B = len(o)
 	W, H = (sc.cameras[0].width, sc.cameras[0].height) if sc.cameras else (0, 0)
 	frames = len(sc.cameras)
-	mode = {'exact': 0, 'fused': 2}[args.colors]
+	mode = {'exact': 0, 'baked': 1, 'fused': 2}[args.colors]
+	color_cut = 2 * math.log(1 / args.eps_color) if args.eps_color > 0 else math.inf
 	empty = torch.empty(0, dtype=torch.int32, device=dev)
 	fi = ext.foam_infer_extension()
-	call = lambda: fi.foam_infer(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'],  # noqa
-								 pack['sh'], sc.sh_deg, o, d, start, near, far, 1e-4, 1e-4, math.inf, mode, 2, empty,
-								 pack['orig'])
+
+	def launch(p, sel, m=mode, cut=color_cut):
+		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
+							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'])
+
+	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
+		per = B // frames
+		centers = [torch.tensor(c.eye, dtype=torch.float32, device=dev) for c in sc.cameras]
+
+		def call():
+			outs = []
+			for f, cen in enumerate(centers):
+				render.bake_colors(model, pack, cen)
+				outs.append(launch(pack, slice(f * per, (f + 1) * per)))
+			return [torch.cat(x) for x in zip(*outs)]
+	else:
+		call = lambda: launch(pack, slice(None))  # noqa
 	log(f'{B} rays ({frames} x {W}x{H}), pack ready ({time.time() - t0:.0f} s); warmup {args.warmup}')
 	for _ in range(args.warmup):
 		out = call()
@@ -169,21 +189,36 @@ def bench_foam(args):
 	rgb, T, depth, stats = out
 	log(f'{args.steps} steps: mean {ms:.3f} ms, median {np.median(launch_ms):.3f} ms, wall {wall * 1e3 / args.steps:.3f} '
 		f'ms/step')
-	sh_bytes = 12 * (sc.sh_deg + 1) ** 2
-	args_of = lambda sel: (pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'],  # noqa
-						   sc.sh_deg, o[sel], d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, math.inf, mode, 2,
-						   empty, pack['orig'])
-	u_sh, u_rays = distinct_blended_sites(fi, pack, args_of, B, sc.sh_deg)
-	log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
+	sh_bytes = (6 if args.sh_half else 12) * (sc.sh_deg + 1) ** 2 if args.colors != 'baked' else 0
+	if fast:  # SH bytes per SH evaluation (an upper bound of the distinct sites); quality against the exact image
+		u_sh, u_rays = float(stats[:, 4].double().mean()), 0
+		exact = render.pack_foam(model, reorder=not args.no_reorder)
+		ref = launch(exact, slice(None), 2, math.inf)
+		bg = 0.5
+		img, img_ref = rgb + T[:, None] * bg, ref[0] + ref[1][:, None] * bg
+		mse = float(((img - img_ref) ** 2).double().mean())
+		quality = {'psnr_vs_exact_db': round(10 * math.log10(1 / max(mse, 1e-30)), 2),
+				   'max_abs_vs_exact': float((img - img_ref).abs().max())}
+		log(f'vs exact (fused, fp32, no skipping): PSNR {quality["psnr_vs_exact_db"]} dB, max |diff| '
+			f'{quality["max_abs_vs_exact"]:.3e}')
+		del exact
+	else:
+		args_of = lambda sel: (pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'],  # noqa
+							   pack['sh'], sc.sh_deg, o[sel], d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4,
+							   math.inf, mode, 2, empty, pack['orig'])
+		u_sh, u_rays = distinct_blended_sites(fi, pack, args_of, B, sc.sh_deg)
+		quality = None
+		log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
 	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
 	achieved = abytes / (ms * 1e-3) / 1e9
 	st = stats.double()
-	traffic = measured_traffic(f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}')
+	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}'
+	traffic = None if fast else measured_traffic(key)
 
 	cpu = None
-	if args.cpu_seconds > 0:
+	if args.cpu_seconds > 0 and args.colors != 'baked':
 		cpu = cpu_baseline(pack, sc, o_np, d_np, start.cpu().numpy(), near.cpu().numpy(), far.cpu().numpy(), mode,
-						   args.cpu_seconds, rgb.cpu().numpy(), T.cpu().numpy())
+						   args.cpu_seconds, rgb.cpu().numpy(), T.cpu().numpy(), color_cut)
 	if args.copy_probe:
 		src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
 		dst = torch.empty_like(src)
@@ -201,12 +236,14 @@ def bench_foam(args):
 						f'{frames} cameras x {W}x{H} = {B} rays per step',
 			'sites': sc.n_sites, 'rays_per_step': B, 'frames_per_step': frames,
 			'fps_1080p': round(frames / (ms * 1e-3), 2) if frames else None,
-			'colors': args.colors, 'sh': 'f32', 'sh_deg': sc.sh_deg, 'morton_reorder': not args.no_reorder,
+			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
+			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': f'{args.tile}x{args.tile} tiles', 't_thresh': 1e-4, 'w_thresh': 1e-4,
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
 			'density_terms_per_ray': round(float(st[:, 3].mean()), 1),
 			'sh_evals_per_ray': round(float(st[:, 4].mean()), 1),
-			'distinct_blended_sites_per_ray': round(u_sh, 1), 'distinct_sites_traced_rays': u_rays,
+			'distinct_blended_sites_per_ray': None if fast else round(u_sh, 1),
+			'distinct_sites_traced_rays': u_rays or None, 'quality': quality,
 			'mean_T': round(float(T.double().mean()), 4),
 		},
 		'roofline': {
@@ -220,7 +257,7 @@ def bench_foam(args):
 	print(json.dumps(res), flush=True)
 
 
-def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu):
+def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu, color_cut=math.inf):
 	"""The CPU oracle (C/OpenMP, thread per ray) on every k-th ray of the same workload, k chosen so the timed
 	loop takes about `seconds` on all host cores; also the max |rgb - GPU| on that subset."""
 	import numpy as np
@@ -231,18 +268,18 @@ def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu
 	threads = oracle.max_threads()
 	B = len(o)
 	probe = np.arange(0, B, max(1, B // 20000), dtype=np.int64)
-	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_mode=mode, rays=probe)
+	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_cut=color_cut, color_mode=mode, rays=probe)
 	rate = len(probe) / max(r['seconds'], 1e-6)
 	k = max(1, int(B / (rate * seconds)))
 	sel = np.arange(0, B, k, dtype=np.int64)
-	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_mode=mode, rays=sel)
+	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_cut=color_cut, color_mode=mode, rays=sel)
 	err = float(np.abs(r['rgb'] - rgb_gpu[sel]).max())
 	errT = float(np.abs(r['T'] - T_gpu[sel]).max())
 	log(f'cpu oracle: {len(sel)} rays (every {k}th) in {r["seconds"]:.2f} s on {threads} threads; '
 		f'max |rgb - gpu| {err:.2e}, max |T - gpu| {errT:.2e}')
 	return {'value': round(len(sel) / r['seconds'] / 1e6, 4), 'unit': 'Mrays/s', 'cores': threads, 'kind': 'port',
-			'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), exact colours, C/OpenMP '
-					  f'thread per ray',
+			'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), same pack and colour mode, '
+					  f'C/OpenMP thread per ray',
 			'parity_max_abs_rgb': err, 'parity_max_abs_T': errT}
 
 
