@@ -24,8 +24,8 @@ def declared():
 
 def test_header_declares_the_entry_points():
 	names = declared()
-	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_march_forward', 'vgr_walk', 'vgr_density_forward',
-			  'vgr_color_forward', 'vgr_conic_forward', 'vgr_grid_work_size', 'vgr_grid_build', 'vgr_grid_nearest',
+	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_march_forward', 'vgr_march_work_size', 'vgr_walk',
+			  'vgr_density_forward', 'vgr_color_forward', 'vgr_conic_forward', 'vgr_grid_work_size', 'vgr_grid_build', 'vgr_grid_nearest',
 			  'vgr_last_error', 'vgr_abi_version'):
 		assert n in names
 
@@ -66,3 +66,13 @@ def test_library_reports_argument_errors_without_a_gpu():
 	rc = lib.vgr_grid_build(None, 1, 3, f3(0, 0, 0), f3(1, 1, -1), i3(1, 1, 1), None, None, None, None)
 	assert rc == 1 and b'cell edge 2' in lib.vgr_last_error()
 	assert lib.vgr_grid_nearest(None, 1, 3, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, None, 0, None, None) == 0
+	# march: one 64-byte record per site in the caller's work buffer, checked before the pack launch
+	assert lib.vgr_march_work_size(0) == 0 and lib.vgr_march_work_size(1000) == 64 * 1000
+	fake = ctypes.c_void_p(1 << 20)
+	margs = [fake, 1000, fake, fake, 15000, fake, fake, fake, fake, 3, fake, fake, fake, fake, fake, fake, 8, 0.01, 64,
+			 1e-4, 1e-4, fake, fake, fake, fake, None, 0, None, 0, None]
+	assert lib.vgr_march_forward(*margs) == 1 and b'work must hold 64000 bytes' in lib.vgr_last_error()
+	margs[27], margs[28] = ctypes.c_void_p((1 << 20) + 16), 64000
+	assert lib.vgr_march_forward(*margs) == 1 and b'64-byte aligned' in lib.vgr_last_error()
+	margs[16] = 0  # no rays: nothing to check or launch
+	assert lib.vgr_march_forward(*margs) == 0

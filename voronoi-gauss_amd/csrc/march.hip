@@ -9,7 +9,13 @@
 // MI355X mapping: one ray per lane over 8x8 ray tiles. All lanes of a wave sit at the same sample index k
 // (the step grid is shared), adjacent pixels are at nearby points, so the neighbourhood gathers of a wave
 // mostly hit the same sites (one broadcast line instead of 64 random ones). The reference's 32-lane
-// shuffle reductions become sequential per-lane sums.
+// shuffle reductions become sequential per-lane sums. Per sample, one fused pass over the neighbourhood does the
+// walk's test, the density and the colour minimum for several consecutive samples at once; the colour blends of the
+// coloured samples of a cell share one pass, which evaluates each neighbour's SH colour once for all of them.
+//
+// Site records: a pack kernel first gathers each site's point, min(raw, 30), density conic and colour conic into
+// one 64-byte record (four float4, 64-byte aligned), so a neighbour costs one aligned 64-byte gather instead of
+// four scattered ones (incoherent rays fetch a fresh line per lane and per array).
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -18,14 +24,14 @@ namespace {
 
 constexpr int kBlock = 64;
 
+// Site record k = rec[4k .. 4k + 3]: (p_k, min(raw_k, 30)), (dA_k[0..3]), (dA_k[4..5], cA_k[0..1]), (cA_k[2..5]).
+constexpr int kRec = 4;
+
 struct MarchField {
-    const float* __restrict__ points;  // (N, 3)
-    const int* __restrict__ offsets;   // (N + 1)
-    const int* __restrict__ adj;       // (M)
-    const float* __restrict__ raw;     // (N)
-    const float* __restrict__ dA;      // (N, 6)
-    const float* __restrict__ cA;      // (N, 6)
-    const float4* __restrict__ sh;     // (N, 12)
+    const float4* __restrict__ rec;  // (N, 4)
+    const int* __restrict__ offsets;  // (N + 1)
+    const int* __restrict__ adj;      // (M)
+    const float4* __restrict__ sh;    // (N, 12)
     int sh_deg, n_sites;
 };
 
@@ -58,41 +64,73 @@ __device__ __forceinline__ int neighbor(const MarchField& F, int i, int e0, int 
     return e == 0 ? i : F.adj[e0 + e - 1];
 }
 
-__device__ __forceinline__ void offset_to(const MarchField& F, int k, const float (&x)[3], float (&v)[3]) {
-    const float* p = F.points + 3 * static_cast<int64_t>(k);
-    v[0] = x[0] - p[0], v[1] = x[1] - p[1], v[2] = x[2] - p[2];
+__global__ void __launch_bounds__(256)
+    march_pack_kernel(const float* __restrict__ points, const float* __restrict__ raw, const float* __restrict__ dA,
+                      const float* __restrict__ cA, int n, float4* __restrict__ rec) {
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= n) return;
+    const float* p = points + 3 * k;
+    const float* a = dA + 6 * k;
+    const float* c = cA + 6 * k;
+    float4* r = rec + kRec * k;
+    r[0] = make_float4(p[0], p[1], p[2], fminf(raw[k], 30.f));
+    r[1] = make_float4(a[0], a[1], a[2], a[3]);
+    r[2] = make_float4(a[4], a[5], c[0], c[1]);
+    r[3] = make_float4(c[2], c[3], c[4], c[5]);
 }
 
-__device__ __forceinline__ float conic_m(const float* __restrict__ A, int k, const float (&v)[3]) {
-    const float* a = A + 6 * static_cast<int64_t>(k);
-    return a[0] * v[0] * v[0] + a[3] * v[1] * v[1] + a[5] * v[2] * v[2] +
-           2.f * (a[1] * v[0] * v[1] + a[2] * v[0] * v[2] + a[4] * v[1] * v[2]);
+struct SiteRec {
+    float4 q0, q1, q2, q3;
+};
+
+__device__ __forceinline__ SiteRec site_rec(const MarchField& F, int k) {
+    const float4* r = F.rec + kRec * static_cast<int64_t>(k);
+    return {r[0], r[1], r[2], r[3]};
 }
 
-// 1/2 + sum_{j < (deg+1)^2} b_j sh_kj per channel, reading only the float4 that hold those coefficients.
+__device__ __forceinline__ void offset_to(const float4& p, const float (&x)[3], float (&v)[3]) {
+    v[0] = x[0] - p.x, v[1] = x[1] - p.y, v[2] = x[2] - p.z;
+}
+
+// Mahalanobis terms v^T A v of the density and colour conics of a record.
+__device__ __forceinline__ float density_m(const SiteRec& R, const float (&v)[3]) {
+    return maha(R.q1.x, R.q1.y, R.q1.z, R.q1.w, R.q2.x, R.q2.y, v[0], v[1], v[2]);
+}
+__device__ __forceinline__ float color_m(const float4& c0, const float4& c1, const float (&v)[3]) {
+    return maha(c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, v[0], v[1], v[2]);
+}
+
+// 1/2 + sum_{j < (deg+1)^2} b_j sh_kj per channel, reading only the float4 that hold those coefficients, kShChunk
+// float4 at a time (the scheduling barrier keeps the next chunk's loads from being hoisted, which bounds the
+// registers the loads occupy).
+#ifndef VGR_MARCH_SHCHUNK
+#define VGR_MARCH_SHCHUNK 4
+#endif
+constexpr int kShChunk = VGR_MARCH_SHCHUNK;
+
 template <int NV>
 __device__ __forceinline__ void sh_eval_n(const float4* __restrict__ sh, int k, const float (&b)[16], int nb,
                                           float (&c)[3]) {
     const float4* s = sh + 12 * static_cast<int64_t>(k);
     c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
-    for (int q = 0; q < NV; ++q) {
-        const float4 f = s[q];
-        const float fv[4] = {f.x, f.y, f.z, f.w};
+    for (int q0 = 0; q0 < NV; q0 += kShChunk) {
+        float4 f[kShChunk];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = 4 * q + u;
-            if (i / 3 < nb) c[i % 3] += b[i / 3] * fv[u];
+        for (int q = 0; q < kShChunk; ++q)
+            if (q0 + q < NV) f[q] = s[q0 + q];
+#pragma unroll
+        for (int q = 0; q < kShChunk; ++q) {
+            if (q0 + q < NV) {
+                const float fv[4] = {f[q].x, f[q].y, f[q].z, f[q].w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int i = 4 * (q0 + q) + u;
+                    if (i / 3 < nb) c[i % 3] += b[i / 3] * fv[u];
+                }
+            }
         }
-    }
-}
-
-__device__ __forceinline__ void sh_eval(const MarchField& F, int k, const float (&b)[16], int nb, float (&c)[3]) {
-    switch (F.sh_deg) {
-        case 0: sh_eval_n<sh_vec4_f32(0)>(F.sh, k, b, nb, c); break;
-        case 1: sh_eval_n<sh_vec4_f32(1)>(F.sh, k, b, nb, c); break;
-        case 2: sh_eval_n<sh_vec4_f32(2)>(F.sh, k, b, nb, c); break;
-        default: sh_eval_n<sh_vec4_f32(3)>(F.sh, k, b, nb, c); break;
+        if (q0 + kShChunk < NV) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -110,104 +148,194 @@ __device__ __forceinline__ void sample_at(float near, float mid, float far, int 
     }
 }
 
-// Lexicographic argmin of (|x - p|^2, index) over {cur} U adj(cur), repeated until cur wins.
-__device__ int walk_to(const MarchField& F, int cur, const float (&x)[3], int& steps) {
-    for (int it = 0; it < kWalkCap; ++it) {
-        const int e0 = F.offsets[cur], n = F.offsets[cur + 1] - e0 + 1;
-        float bd = kInf;
-        int bk = INT_MAX;
-        for (int e = 0; e < n; ++e) {
-            const int k = neighbor(F, cur, e0, e);
-            float v[3];
-            offset_to(F, k, x, v);
-            const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
-            if (dk < bd || (dk == bd && k < bk)) bd = dk, bk = k;
-        }
-        if (bk == cur) break;
-        cur = bk;
-        ++steps;
-    }
-    return cur;
+// Samples are resolved kBatch at a time: one pass over the neighbourhood {i} U adj(i) of site i evaluates, for
+// each of the next kBatch sample points x_j, the lexicographic argmin of (|x_j - p_k|^2, k) (the greedy walk's
+// test), the density sum and the smallest colour Mahalanobis distance. Sample j + 1's walk starts at sample j's
+// site, so every leading sample at which i wins is resolved by this one pass exactly as by a pass of its own (same
+// neighbours, same order, same roundings); the first sample at which i loses walks on from its argmin, and the
+// pass at the next site covers it and the samples after it. Each quantity accumulates over the neighbours in the
+// same order as the reference's separate passes.
+#ifndef VGR_MARCH_BATCH
+#define VGR_MARCH_BATCH 6
+#endif
+constexpr int kBatch = VGR_MARCH_BATCH;
+
+#ifndef VGR_MARCH_PIPE
+#define VGR_MARCH_PIPE 0
+#endif
+
+struct CellPass {
+    int best[kBatch];
+    float sigma[kBatch], mmin[kBatch];
+};
+
+// x = o + t d, rounded per operation (the product, then the sum).
+__device__ __forceinline__ void point_at(const float (&o)[3], const float (&d)[3], float t, float (&x)[3]) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) x[a] = o[a] + t * d[a];
 }
 
-__device__ float density_at(const MarchField& F, int i, const float (&x)[3]) {
+__device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const float (&d)[3],
+                          const float (&t)[kBatch], CellPass& R) {
     const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
-    float s = 0.f;
+    float bd[kBatch], s[kBatch], mm[kBatch];
+    int bk[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) bd[j] = kInf, s[j] = 0.f, mm[j] = kInf, bk[j] = INT_MAX;
+    int k = i;
+    int kn = neighbor(F, i, e0, min(1, n - 1));
+#if VGR_MARCH_PIPE
+    SiteRec rc = site_rec(F, k);
+#endif
     for (int e = 0; e < n; ++e) {
-        const int k = neighbor(F, i, e0, e);
-        float v[3];
-        offset_to(F, k, x, v);
-        s += fexp(fminf(F.raw[k], 30.f) - 0.5f * conic_m(F.dA, k, v));
+        const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));  // in flight: the neighbour after next
+#if VGR_MARCH_PIPE
+        const SiteRec rn = site_rec(F, kn);  // in flight: the next neighbour's record
+#else
+        const SiteRec rc = site_rec(F, k);
+#endif
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            float x[3], v[3];
+            point_at(o, d, t[j], x);
+            offset_to(rc.q0, x, v);
+            const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+            if (dk < bd[j] || (dk == bd[j] && k < bk[j])) bd[j] = dk, bk[j] = k;
+            s[j] += fexp(rc.q0.w - 0.5f * density_m(rc, v));
+            mm[j] = fminf(mm[j], color_m(rc.q2, rc.q3, v));
+        }
+        k = kn, kn = k2;
+#if VGR_MARCH_PIPE
+        rc = rn;
+#endif
     }
-    return s;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) R.best[j] = bk[j], R.sigma[j] = s[j], R.mmin[j] = mm[j];
 }
 
-__device__ void color_at(const MarchField& F, int i, const float (&x)[3], const float (&b)[16], float (&C)[3]) {
+// Colour samples waiting for the blend pass of their cell: up to kPend coloured samples of one cell are blended
+// together, so each neighbour's colour max(SH_k(d) + 1/2, 0), which depends only on the site and the ray
+// direction, is evaluated once for all of them.
+#ifndef VGR_MARCH_PEND
+#define VGR_MARCH_PEND 6
+#endif
+constexpr int kPend = VGR_MARCH_PEND;
+static_assert(kPend >= kBatch, "a pass resolves up to kBatch samples of one cell, all of which must fit");
+
+struct Pending {
+    float t[kPend], w[kPend], mmin[kPend];
+    int n, cell;
+};
+
+// Blends the pending samples' colours (per sample: weights exp(-(m_k - m_min) / 2) over the neighbours in order,
+// then the normalised sum) and adds w C and w t of each, in sample order, to the ray's colour and depth.
+template <int NV>
+__device__ void flush(const MarchField& F, const float (&o)[3], const float (&d)[3], Pending& P, float (&acc)[3],
+                      float& dep) {
+    if (P.n == 0) return;
+    const int i = P.cell;
     const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
     const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
-    float mmin = kInf;
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    float A[kPend], cr[kPend], cg[kPend], cb[kPend];
+#pragma unroll
+    for (int s = 0; s < kPend; ++s) A[s] = cr[s] = cg[s] = cb[s] = 0.f;
+    int k = i;
+    int kn = neighbor(F, i, e0, min(1, n - 1));
     for (int e = 0; e < n; ++e) {
-        const int k = neighbor(F, i, e0, e);
-        float v[3];
-        offset_to(F, k, x, v);
-        mmin = fminf(mmin, conic_m(F.cA, k, v));
-    }
-    float A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
-    for (int e = 0; e < n; ++e) {
-        const int k = neighbor(F, i, e0, e);
-        float v[3];
-        offset_to(F, k, x, v);
-        const float a = fexp(-0.5f * (conic_m(F.cA, k, v) - mmin));
+        const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));
+        const float4* r = F.rec + kRec * static_cast<int64_t>(k);
+        const float4 p = r[0], c0 = r[2], c1 = r[3];
         float c[3];
-        sh_eval(F, k, b, nb, c);
-        A += a, cr += a * fmaxf(c[0], 0.f), cg += a * fmaxf(c[1], 0.f), cb += a * fmaxf(c[2], 0.f);
+        sh_eval_n<NV>(F.sh, k, b, nb, c);
+        c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
+#pragma unroll
+        for (int s = 0; s < kPend; ++s) {
+            if (s < P.n) {
+                float x[3], v[3];
+                point_at(o, d, P.t[s], x);
+                offset_to(p, x, v);
+                const float a = fexp(-0.5f * (color_m(c0, c1, v) - P.mmin[s]));
+                A[s] += a, cr[s] += a * c[0], cg[s] += a * c[1], cb[s] += a * c[2];
+            }
+        }
+        k = kn, kn = k2;
     }
-    const float inv_a = 1.f / A;
-    C[0] = cr * inv_a, C[1] = cg * inv_a, C[2] = cb * inv_a;
+#pragma unroll
+    for (int s = 0; s < kPend; ++s) {
+        if (s < P.n) {
+            const float inv_a = 1.f / A[s];
+            const float C[3] = {cr[s] * inv_a, cg[s] * inv_a, cb[s] * inv_a};
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += P.w[s] * C[a];
+            dep += P.w[s] * P.t[s];
+        }
+    }
+    P.n = 0;
 }
 
-template <bool TRACE>
-__global__ void __launch_bounds__(kBlock)
-    march_forward_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
-    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
-    if (r >= R.n) return;
-    int cur = R.start[r];
-    if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground
-        O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
-        O.T[r] = 1.f, O.depth[r] = 0.f;
-        O.stats[3 * r] = O.stats[3 * r + 1] = O.stats[3 * r + 2] = 0;
-        return;
-    }
+template <int NV, bool TRACE>
+__device__ void march_ray(const MarchField& F, const MarchParams& M, const MarchRays& R, const MarchOut& O, int64_t r,
+                          int cur) {
     const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
     const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
     const int n_in = mid > near ? static_cast<int>(ceilf((mid - near) / M.dt)) : 0;
     const int n_total = n_in + M.n_bg;
-    float b[16];
-    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
     int n_samples = 0, n_color = 0, walk_steps = 0;
     float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
-    for (int k = 0; k < n_total; ++k) {
-        float t, delta, x[3];
-        sample_at(near, mid, far, n_in, M, k, t, delta);
+    Pending P;
+    P.n = 0, P.cell = -1;
 #pragma unroll
-        for (int a = 0; a < 3; ++a) x[a] = o[a] + t * d[a];
-        cur = walk_to(F, cur, x, walk_steps);
-        if (TRACE && n_samples < O.trace_cap) O.trace[r * O.trace_cap + n_samples] = cur;
-        const float alpha = 1.f - fexp(-density_at(F, cur, x) * delta);
-        const float w = T * alpha;
-        ++n_samples;
-        if (w > M.w_thresh) {
-            float C[3];
-            color_at(F, cur, x, b, C);
+    for (int s = 0; s < kPend; ++s) P.t[s] = P.w[s] = P.mmin[s] = 0.f;
+    // k: first unresolved sample; moves: greedy-walk steps taken so far for sample k
+    int k = 0, moves = 0;
+    bool live = true;
+    while (live && k < n_total) {
+        // the pass's samples must fit next to the pending ones of this cell
+        if (P.n > 0 && (P.cell != cur || P.n + kBatch > kPend)) flush<NV>(F, o, d, P, acc, dep);
+        float ts[kBatch];
 #pragma unroll
-            for (int a = 0; a < 3; ++a) acc[a] += w * C[a];
-            dep += w * t;
-            ++n_color;
+        for (int j = 0; j < kBatch; ++j) {
+            float unused;
+            sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), ts[j], unused);
         }
-        T *= 1.f - alpha;
-        if (T < M.t_thresh) break;
+        CellPass C;
+        cell_pass(F, cur, o, d, ts, C);
+        // walk bound reached: the sample takes the current site, unverified
+        const bool force = moves >= kWalkCap;
+        int nres = 0, next = cur;
+        bool run = true;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (!run || k + j >= n_total) {
+                run = false;
+            } else if (C.best[j] == cur || (j == 0 && force)) {
+                if (TRACE && n_samples < O.trace_cap) O.trace[r * O.trace_cap + n_samples] = cur;
+                float t, delta;
+                sample_at(near, mid, far, n_in, M, k + j, t, delta);
+                const float alpha = 1.f - fexp(-C.sigma[j] * delta);
+                const float w = T * alpha;
+                ++n_samples, ++nres;
+                if (w > M.w_thresh) {
+#pragma unroll
+                    for (int s = 0; s < kPend; ++s)
+                        if (s == P.n) P.t[s] = t, P.w[s] = w, P.mmin[s] = C.mmin[j];
+                    P.cell = cur, ++P.n;
+                    ++n_color;
+                }
+                T *= 1.f - alpha;
+                if (T < M.t_thresh) run = live = false;
+            } else {
+                next = C.best[j], run = false;
+            }
+        }
+        k += nres;
+        moves = nres > 0 ? 0 : moves;
+        if (live && k < n_total && next != cur) cur = next, ++walk_steps, ++moves;
     }
+    flush<NV>(F, o, d, P, acc, dep);
 #pragma unroll
     for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
     O.T[r] = T;
@@ -215,15 +343,46 @@ __global__ void __launch_bounds__(kBlock)
     O.stats[3 * r] = n_samples, O.stats[3 * r + 1] = n_color, O.stats[3 * r + 2] = walk_steps;
 }
 
+// Minimum waves per SIMD the register allocation must allow (1: no constraint; the kernel then takes 164 VGPRs,
+// 3 waves per SIMD, which measured faster than spilling down to 4).
+#ifndef VGR_MARCH_WAVES
+#define VGR_MARCH_WAVES 1
+#endif
+
+template <bool TRACE>
+__global__ void __launch_bounds__(kBlock, VGR_MARCH_WAVES)
+    march_forward_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
+    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
+    if (r >= R.n) return;
+    const int cur = R.start[r];
+    if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground
+        O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+        O.T[r] = 1.f, O.depth[r] = 0.f;
+        O.stats[3 * r] = O.stats[3 * r + 1] = O.stats[3 * r + 2] = 0;
+        return;
+    }
+    switch (F.sh_deg) {
+        case 0: march_ray<sh_vec4_f32(0), TRACE>(F, M, R, O, r, cur); break;
+        case 1: march_ray<sh_vec4_f32(1), TRACE>(F, M, R, O, r, cur); break;
+        case 2: march_ray<sh_vec4_f32(2), TRACE>(F, M, R, O, r, cur); break;
+        default: march_ray<sh_vec4_f32(3), TRACE>(F, M, R, O, r, cur); break;
+    }
+}
+
 }  // namespace
 }  // namespace vgr
+
+extern "C" int64_t vgr_march_work_size(int64_t n_sites) {
+    return n_sites > 0 ? n_sites * static_cast<int64_t>(sizeof(float4) * vgr::kRec) : 0;
+}
 
 extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                                  int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
                                  int64_t sh_deg, const float* o, const float* d, const int32_t* start,
                                  const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
                                  double dt, int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T,
-                                 float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream) {
+                                 float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* work,
+                                 int64_t work_bytes, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(n_rays >= 0, "march_forward: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
@@ -236,8 +395,13 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
     VGR_REQUIRE(points && offsets && (adj || n_adj == 0) && raw && dA && cA && sh, "march_forward: null field pointer");
     VGR_REQUIRE(o && d && start && near_t && mid_t && far_t, "march_forward: null ray pointer");
     VGR_REQUIRE(rgb && T && depth && stats, "march_forward: null output pointer");
-    const MarchField F{points, offsets, adj, raw, dA, cA, reinterpret_cast<const float4*>(sh), int(sh_deg),
-                       int(n_sites)};
+    VGR_REQUIRE(work && work_bytes >= vgr_march_work_size(n_sites), "march_forward: work must hold %lld bytes",
+                static_cast<long long>(vgr_march_work_size(n_sites)));
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 64 == 0, "march_forward: work must be 64-byte aligned");
+    float4* rec = static_cast<float4*>(work);
+    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, as_stream(stream), points, raw,
+                       dA, cA, int(n_sites), rec);
+    const MarchField F{rec, offsets, adj, reinterpret_cast<const float4*>(sh), int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
     const MarchOut O{rgb, T, depth, stats, trace, trace_cap};

@@ -21,7 +21,8 @@ SIGNATURES = {
 	'vgr_foam_infer_traced': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64,
 							  _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
-						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P],
+						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
+	'vgr_march_work_size': [_I64],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P],
@@ -33,7 +34,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _lib = None
 
 
@@ -50,6 +51,7 @@ def load():
 			fn.restype = ctypes.c_int
 		lib.vgr_last_error.restype = ctypes.c_char_p
 		lib.vgr_grid_work_size.restype = ctypes.c_int64
+		lib.vgr_march_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

@@ -125,11 +125,13 @@ class _MarchExtension:
 		out = [rgb, T, depth, stats] + ([trace] if trace is not None else [])
 		if B == 0:
 			return out
+		work_bytes = int(_lib.load().vgr_march_work_size(points.numel() // 3))
+		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
 			call('vgr_march_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(dA), ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid),
 				 ptr(far), B, float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(depth),
-				 ptr(stats), ptr(trace), int(trace_cap), stream_of(dev))
+				 ptr(stats), ptr(trace), int(trace_cap), ptr(work), work_bytes, stream_of(dev))
 		return out
 
 
