@@ -34,6 +34,17 @@ def log(*a):
 	print('[bench]', *a, file=sys.stderr, flush=True)
 
 
+def copy_probe(dev):
+	"""A 1 GiB device-to-device copy: the PMC runs scale the kernels' FETCH_SIZE / WRITE_SIZE by what the same
+	counters read for it."""
+	import torch
+	src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+	dst = torch.empty_like(src)
+	dst.copy_(src)
+	torch.cuda.synchronize()
+	log('copy probe: 1 GiB read + 1 GiB written')
+
+
 def measured_traffic(workload):
 	"""DRAM bytes per launch of this workload from the committed rocprofv3 PMC summary (a line
 	'traffic_bytes_per_launch: <bytes> workload: <key>'), or None when no summary matches."""
@@ -220,11 +231,7 @@ def bench_foam(args):
 		cpu = cpu_baseline(pack, sc, o_np, d_np, start.cpu().numpy(), near.cpu().numpy(), far.cpu().numpy(), mode,
 						   args.cpu_seconds, rgb.cpu().numpy(), T.cpu().numpy(), color_cut)
 	if args.copy_probe:
-		src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-		dst = torch.empty_like(src)
-		dst.copy_(src)
-		torch.cuda.synchronize()
-		log('copy probe: 1 GiB read + 1 GiB written')
+		copy_probe(dev)
 
 	mrays = B / (ms * 1e-3) / 1e6
 	res = {
@@ -437,6 +444,9 @@ def bench_march(args):
 			   'parity_note': 'with w_thresh = 1e-4 many config-5 samples have weight within ulps of the threshold, so '
 							  'device and host exp (the reference uses __expf, march.cu:241) colour slightly different '
 							  'sample sets; the thresholds-off figures compare the arithmetic'}
+	if args.copy_probe:
+		copy_probe(dev)
+	traffic = measured_traffic(f'config5-scale{args.scale}-march')
 	emit('Mrays/s march_forward (config 5: 4M sites, 16.7M incoherent rays) on 1 MI355X', B / ms / 1e3, 'Mrays/s',
 		 args, ms,
 		 {'workload': f'config 5 march: {sc.n_sites} sites, {B} rays, dt 1/512 inside the unit ball + {n_bg} '
@@ -444,7 +454,8 @@ def bench_march(args):
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2), 'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
+		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)
 
 
 def bench_field(args):

@@ -78,10 +78,10 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
  *   sh f32 (N, 16, 3); o, d f32 (B, 3); start i32 (B); near_t, mid_t, far_t f32 (B)
  *   outputs rgb f32 (B, 3), T f32 (B), depth f32 (B), stats i32 (B, 3) = samples, samples with colour, walk steps
  * trace (optional, NULL = none) i32 (B, trace_cap): the site of every sample.
- * work: device scratch of at least vgr_march_work_size(N) bytes, 64-byte aligned, for the packed site records
- * (overwritten by every call; calls that share it must be ordered on one stream).
+ * work: device scratch of at least vgr_march_work_size(N, sh_deg) bytes (128 or 256 per site), 256-byte aligned,
+ * for the packed site blocks (overwritten by every call; calls that share it must be ordered on one stream).
  */
-int64_t vgr_march_work_size(int64_t n_sites);
+int64_t vgr_march_work_size(int64_t n_sites, int64_t sh_deg);
 int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                       int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
                       int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,

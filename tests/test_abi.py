@@ -66,13 +66,15 @@ def test_library_reports_argument_errors_without_a_gpu():
 	rc = lib.vgr_grid_build(None, 1, 3, f3(0, 0, 0), f3(1, 1, -1), i3(1, 1, 1), None, None, None, None)
 	assert rc == 1 and b'cell edge 2' in lib.vgr_last_error()
 	assert lib.vgr_grid_nearest(None, 1, 3, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, None, 0, None, None) == 0
-	# march: one 64-byte record per site in the caller's work buffer, checked before the pack launch
-	assert lib.vgr_march_work_size(0) == 0 and lib.vgr_march_work_size(1000) == 64 * 1000
+	# march: one line-aligned block per site in the caller's work buffer (record + SH: 128 B up to sh_deg 1, else
+	# 256 B), checked before the pack launch
+	assert lib.vgr_march_work_size(0, 3) == 0 and lib.vgr_march_work_size(1000, 4) == 0
+	assert [lib.vgr_march_work_size(1000, g) for g in range(4)] == [128000, 128000, 256000, 256000]
 	fake = ctypes.c_void_p(1 << 20)
 	margs = [fake, 1000, fake, fake, 15000, fake, fake, fake, fake, 3, fake, fake, fake, fake, fake, fake, 8, 0.01, 64,
 			 1e-4, 1e-4, fake, fake, fake, fake, None, 0, None, 0, None]
-	assert lib.vgr_march_forward(*margs) == 1 and b'work must hold 64000 bytes' in lib.vgr_last_error()
-	margs[27], margs[28] = ctypes.c_void_p((1 << 20) + 16), 64000
-	assert lib.vgr_march_forward(*margs) == 1 and b'64-byte aligned' in lib.vgr_last_error()
+	assert lib.vgr_march_forward(*margs) == 1 and b'work must hold 256000 bytes' in lib.vgr_last_error()
+	margs[27], margs[28] = ctypes.c_void_p((1 << 20) + 128), 256000
+	assert lib.vgr_march_forward(*margs) == 1 and b'256-byte aligned' in lib.vgr_last_error()
 	margs[16] = 0  # no rays: nothing to check or launch
 	assert lib.vgr_march_forward(*margs) == 0

@@ -13,9 +13,11 @@
 // walk's test, the density and the colour minimum for several consecutive samples at once; the colour blends of the
 // coloured samples of a cell share one pass, which evaluates each neighbour's SH colour once for all of them.
 //
-// Site records: a pack kernel first gathers each site's point, min(raw, 30), density conic and colour conic into
-// one 64-byte record (four float4, 64-byte aligned), so a neighbour costs one aligned 64-byte gather instead of
-// four scattered ones (incoherent rays fetch a fresh line per lane and per array).
+// Site blocks: a pack kernel first gathers each site's point, min(raw, 30), density conic, colour conic and SH
+// coefficients into one line-aligned block: the 64-byte record and the first 64 bytes of SH fill one 128-byte line,
+// the rest of the SH the next. Incoherent rays fetch a fresh line per lane for every neighbour: a neighbourhood pass
+// then costs one line per neighbour (the record), a colour pass two (one when sh_deg <= 1), instead of one line per
+// scattered array.
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -24,14 +26,16 @@ namespace {
 
 constexpr int kBlock = 64;
 
-// Site record k = rec[4k .. 4k + 3]: (p_k, min(raw_k, 30)), (dA_k[0..3]), (dA_k[4..5], cA_k[0..1]), (cA_k[2..5]).
+// Site block k = rec[BLK k .. BLK k + BLK - 1] (float4): the record (p_k, min(raw_k, 30)), (dA_k[0..3]),
+// (dA_k[4..5], cA_k[0..1]), (cA_k[2..5]), then the first NV float4 of the site's SH row (N, 16, 3); BLK = 8 (one
+// 128-byte line) when they fit, else 16.
 constexpr int kRec = 4;
+__host__ __device__ constexpr int block_vec4(int nv) { return kRec + nv <= 8 ? 8 : 16; }
 
 struct MarchField {
-    const float4* __restrict__ rec;  // (N, 4)
+    const float4* __restrict__ rec;  // (N, BLK)
     const int* __restrict__ offsets;  // (N + 1)
     const int* __restrict__ adj;      // (M)
-    const float4* __restrict__ sh;    // (N, 12)
     int sh_deg, n_sites;
 };
 
@@ -66,25 +70,28 @@ __device__ __forceinline__ int neighbor(const MarchField& F, int i, int e0, int 
 
 __global__ void __launch_bounds__(256)
     march_pack_kernel(const float* __restrict__ points, const float* __restrict__ raw, const float* __restrict__ dA,
-                      const float* __restrict__ cA, int n, float4* __restrict__ rec) {
+                      const float* __restrict__ cA, const float4* __restrict__ sh, int nv, int blk, int n,
+                      float4* __restrict__ rec) {
     const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (k >= n) return;
     const float* p = points + 3 * k;
     const float* a = dA + 6 * k;
     const float* c = cA + 6 * k;
-    float4* r = rec + kRec * k;
+    float4* r = rec + blk * k;
     r[0] = make_float4(p[0], p[1], p[2], fminf(raw[k], 30.f));
     r[1] = make_float4(a[0], a[1], a[2], a[3]);
     r[2] = make_float4(a[4], a[5], c[0], c[1]);
     r[3] = make_float4(c[2], c[3], c[4], c[5]);
+    for (int q = 0; q < nv; ++q) r[kRec + q] = sh[12 * k + q];
 }
 
 struct SiteRec {
     float4 q0, q1, q2, q3;
 };
 
+template <int BLK>
 __device__ __forceinline__ SiteRec site_rec(const MarchField& F, int k) {
-    const float4* r = F.rec + kRec * static_cast<int64_t>(k);
+    const float4* r = F.rec + BLK * static_cast<int64_t>(k);
     return {r[0], r[1], r[2], r[3]};
 }
 
@@ -109,9 +116,7 @@ __device__ __forceinline__ float color_m(const float4& c0, const float4& c1, con
 constexpr int kShChunk = VGR_MARCH_SHCHUNK;
 
 template <int NV>
-__device__ __forceinline__ void sh_eval_n(const float4* __restrict__ sh, int k, const float (&b)[16], int nb,
-                                          float (&c)[3]) {
-    const float4* s = sh + 12 * static_cast<int64_t>(k);
+__device__ __forceinline__ void sh_eval_n(const float4* __restrict__ s, const float (&b)[16], int nb, float (&c)[3]) {
     c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
     for (int q0 = 0; q0 < NV; q0 += kShChunk) {
@@ -163,6 +168,9 @@ constexpr int kBatch = VGR_MARCH_BATCH;
 #ifndef VGR_MARCH_PIPE
 #define VGR_MARCH_PIPE 0
 #endif
+#ifndef VGR_MARCH_NOHOIST
+#define VGR_MARCH_NOHOIST 1
+#endif
 
 struct CellPass {
     int best[kBatch];
@@ -175,6 +183,7 @@ __device__ __forceinline__ void point_at(const float (&o)[3], const float (&d)[3
     for (int a = 0; a < 3; ++a) x[a] = o[a] + t * d[a];
 }
 
+template <int BLK>
 __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const float (&d)[3],
                           const float (&t)[kBatch], CellPass& R) {
     const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
@@ -185,19 +194,23 @@ __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const
     int k = i;
     int kn = neighbor(F, i, e0, min(1, n - 1));
 #if VGR_MARCH_PIPE
-    SiteRec rc = site_rec(F, k);
+    SiteRec rc = site_rec<BLK>(F, k);
 #endif
     for (int e = 0; e < n; ++e) {
         const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));  // in flight: the neighbour after next
 #if VGR_MARCH_PIPE
-        const SiteRec rn = site_rec(F, kn);  // in flight: the next neighbour's record
+        const SiteRec rn = site_rec<BLK>(F, kn);  // in flight: the next neighbour's record
 #else
-        const SiteRec rc = site_rec(F, k);
+        const SiteRec rc = site_rec<BLK>(F, k);
 #endif
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             float x[3], v[3];
-            point_at(o, d, t[j], x);
+            float tj = t[j];
+#if VGR_MARCH_NOHOIST
+            asm volatile("" : "+v"(tj));  // recompute x per neighbour: 3 fewer live registers per sample
+#endif
+            point_at(o, d, tj, x);
             offset_to(rc.q0, x, v);
             const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
             if (dk < bd[j] || (dk == bd[j] && k < bk[j])) bd[j] = dk, bk[j] = k;
@@ -213,14 +226,10 @@ __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const
     for (int j = 0; j < kBatch; ++j) R.best[j] = bk[j], R.sigma[j] = s[j], R.mmin[j] = mm[j];
 }
 
-// Colour samples waiting for the blend pass of their cell: up to kPend coloured samples of one cell are blended
-// together, so each neighbour's colour max(SH_k(d) + 1/2, 0), which depends only on the site and the ray
-// direction, is evaluated once for all of them.
-#ifndef VGR_MARCH_PEND
-#define VGR_MARCH_PEND 6
-#endif
-constexpr int kPend = VGR_MARCH_PEND;
-static_assert(kPend >= kBatch, "a pass resolves up to kBatch samples of one cell, all of which must fit");
+// Coloured samples of one neighbourhood pass (all in one cell), blended together by one colour pass, so each
+// neighbour's colour max(SH_k(d) + 1/2, 0), which depends only on the site and the ray direction, is evaluated once
+// for all of them.
+constexpr int kPend = kBatch;
 
 struct Pending {
     float t[kPend], w[kPend], mmin[kPend];
@@ -245,16 +254,20 @@ __device__ void flush(const MarchField& F, const float (&o)[3], const float (&d)
     int kn = neighbor(F, i, e0, min(1, n - 1));
     for (int e = 0; e < n; ++e) {
         const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));
-        const float4* r = F.rec + kRec * static_cast<int64_t>(k);
+        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
         const float4 p = r[0], c0 = r[2], c1 = r[3];
         float c[3];
-        sh_eval_n<NV>(F.sh, k, b, nb, c);
+        sh_eval_n<NV>(r + kRec, b, nb, c);
         c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
 #pragma unroll
         for (int s = 0; s < kPend; ++s) {
             if (s < P.n) {
                 float x[3], v[3];
-                point_at(o, d, P.t[s], x);
+                float ts = P.t[s];
+#if VGR_MARCH_NOHOIST
+                asm volatile("" : "+v"(ts));
+#endif
+                point_at(o, d, ts, x);
                 offset_to(p, x, v);
                 const float a = fexp(-0.5f * (color_m(c0, c1, v) - P.mmin[s]));
                 A[s] += a, cr[s] += a * c[0], cg[s] += a * c[1], cb[s] += a * c[2];
@@ -285,16 +298,10 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
     const int n_total = n_in + M.n_bg;
     int n_samples = 0, n_color = 0, walk_steps = 0;
     float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
-    Pending P;
-    P.n = 0, P.cell = -1;
-#pragma unroll
-    for (int s = 0; s < kPend; ++s) P.t[s] = P.w[s] = P.mmin[s] = 0.f;
     // k: first unresolved sample; moves: greedy-walk steps taken so far for sample k
     int k = 0, moves = 0;
     bool live = true;
     while (live && k < n_total) {
-        // the pass's samples must fit next to the pending ones of this cell
-        if (P.n > 0 && (P.cell != cur || P.n + kBatch > kPend)) flush<NV>(F, o, d, P, acc, dep);
         float ts[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -302,11 +309,16 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
             sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), ts[j], unused);
         }
         CellPass C;
-        cell_pass(F, cur, o, d, ts, C);
+        cell_pass<block_vec4(NV)>(F, cur, o, d, ts, C);
         // walk bound reached: the sample takes the current site, unverified
         const bool force = moves >= kWalkCap;
         int nres = 0, next = cur;
         bool run = true;
+        // the coloured samples this pass resolves, all in site cur, blended by one colour pass right after
+        Pending P;
+        P.n = 0, P.cell = cur;
+#pragma unroll
+        for (int s = 0; s < kPend; ++s) P.t[s] = P.w[s] = P.mmin[s] = 0.f;
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             if (!run || k + j >= n_total) {
@@ -322,7 +334,7 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
 #pragma unroll
                     for (int s = 0; s < kPend; ++s)
                         if (s == P.n) P.t[s] = t, P.w[s] = w, P.mmin[s] = C.mmin[j];
-                    P.cell = cur, ++P.n;
+                    ++P.n;
                     ++n_color;
                 }
                 T *= 1.f - alpha;
@@ -331,11 +343,11 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
                 next = C.best[j], run = false;
             }
         }
+        flush<NV>(F, o, d, P, acc, dep);
         k += nres;
         moves = nres > 0 ? 0 : moves;
         if (live && k < n_total && next != cur) cur = next, ++walk_steps, ++moves;
     }
-    flush<NV>(F, o, d, P, acc, dep);
 #pragma unroll
     for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
     O.T[r] = T;
@@ -343,10 +355,10 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
     O.stats[3 * r] = n_samples, O.stats[3 * r + 1] = n_color, O.stats[3 * r + 2] = walk_steps;
 }
 
-// Minimum waves per SIMD the register allocation must allow (1: no constraint; the kernel then takes 164 VGPRs,
-// 3 waves per SIMD, which measured faster than spilling down to 4).
+// Minimum waves per SIMD the register allocation must allow. At 4 the colour pass spills about 17 VGPRs to scratch
+// and the kernel is still 5 % faster than at its natural 3 waves (146 VGPRs): it is bound by the gathers in flight.
 #ifndef VGR_MARCH_WAVES
-#define VGR_MARCH_WAVES 1
+#define VGR_MARCH_WAVES 4
 #endif
 
 template <bool TRACE>
@@ -372,8 +384,10 @@ __global__ void __launch_bounds__(kBlock, VGR_MARCH_WAVES)
 }  // namespace
 }  // namespace vgr
 
-extern "C" int64_t vgr_march_work_size(int64_t n_sites) {
-    return n_sites > 0 ? n_sites * static_cast<int64_t>(sizeof(float4) * vgr::kRec) : 0;
+extern "C" int64_t vgr_march_work_size(int64_t n_sites, int64_t sh_deg) {
+    using namespace vgr;
+    if (n_sites <= 0 || sh_deg < 0 || sh_deg > 3) return 0;
+    return n_sites * static_cast<int64_t>(sizeof(float4)) * block_vec4(sh_vec4_f32(static_cast<int>(sh_deg)));
 }
 
 extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
@@ -395,13 +409,14 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
     VGR_REQUIRE(points && offsets && (adj || n_adj == 0) && raw && dA && cA && sh, "march_forward: null field pointer");
     VGR_REQUIRE(o && d && start && near_t && mid_t && far_t, "march_forward: null ray pointer");
     VGR_REQUIRE(rgb && T && depth && stats, "march_forward: null output pointer");
-    VGR_REQUIRE(work && work_bytes >= vgr_march_work_size(n_sites), "march_forward: work must hold %lld bytes",
-                static_cast<long long>(vgr_march_work_size(n_sites)));
-    VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 64 == 0, "march_forward: work must be 64-byte aligned");
+    const int64_t need = vgr_march_work_size(n_sites, sh_deg);
+    VGR_REQUIRE(work && work_bytes >= need, "march_forward: work must hold %lld bytes", static_cast<long long>(need));
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "march_forward: work must be 256-byte aligned");
     float4* rec = static_cast<float4*>(work);
+    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
     hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, as_stream(stream), points, raw,
-                       dA, cA, int(n_sites), rec);
-    const MarchField F{rec, offsets, adj, reinterpret_cast<const float4*>(sh), int(sh_deg), int(n_sites)};
+                       dA, cA, reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
+    const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
     const MarchOut O{rgb, T, depth, stats, trace, trace_cap};

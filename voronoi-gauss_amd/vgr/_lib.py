@@ -22,7 +22,7 @@ SIGNATURES = {
 							  _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
-	'vgr_march_work_size': [_I64],
+	'vgr_march_work_size': [_I64, _I64],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P],
@@ -34,7 +34,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _lib = None
 
 

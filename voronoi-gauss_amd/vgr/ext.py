@@ -125,7 +125,7 @@ class _MarchExtension:
 		out = [rgb, T, depth, stats] + ([trace] if trace is not None else [])
 		if B == 0:
 			return out
-		work_bytes = int(_lib.load().vgr_march_work_size(points.numel() // 3))
+		work_bytes = int(_lib.load().vgr_march_work_size(points.numel() // 3, int(sh_deg)))
 		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
 			call('vgr_march_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
