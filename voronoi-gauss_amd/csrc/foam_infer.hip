@@ -151,11 +151,20 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
 // direct-mapped slots (site k mod kSlots), stored [12][kSlots] float4 so that lanes reading different slots hit
 // different banks. The 64 rays of a tile read overlapping sets of sites (45 % of the lookups find their block in
 // LDS on the config-3 scene); the colour itself, max(SH_k(d) + 1/2, 0), is evaluated per lane since it depends on
-// the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup. 48 slots keep the cache at 9.8 KB
-// per wave, so that 16 waves (4 per SIMD) fit in a CU's 160 KB of LDS: the kernel is latency-bound, and a fourth
-// wave per SIMD gains more than the larger cache a 64-slot layout (3 waves) would give.
+// the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup. 30 slots keep the cache at 6.0 KB
+// per wave, so that 24 waves (6 per SIMD) fit in a CU's 160 KB of LDS: more waves per SIMD gain more than a
+// larger cache (48 slots at 4 waves, 36 at 5 and 26 at 7 were all slower).
 #ifndef VGR_SLOTS
-#define VGR_SLOTS 48
+#define VGR_SLOTS 30
+#endif
+// Software pipelining of the neighbourhood loops: VGR_EDGE_AHEAD = 2 loads the edge records two edges ahead,
+// VGR_REC_AHEAD (with it) the site records one ahead. Both off: the registers they hold are worth more as a sixth
+// wave per SIMD, whose loads cover the latency instead.
+#ifndef VGR_REC_AHEAD
+#define VGR_REC_AHEAD 0
+#endif
+#ifndef VGR_EDGE_AHEAD
+#define VGR_EDGE_AHEAD 0
 #endif
 constexpr int kSlots = VGR_SLOTS;
 
@@ -323,8 +332,8 @@ __device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
 
 // One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
 // Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
-// The loop is software-pipelined: the edge record of e + 2 and the site records of e + 1 are loaded while edge e is
-// evaluated (indices clamped to the cell, so every load stays in bounds).
+// With VGR_EDGE_AHEAD = 2 the loop is software-pipelined: the edge record of e + 2 (and with VGR_REC_AHEAD the site
+// records of e + 1) are loaded while edge e is evaluated, indices clamped to the cell so every load stays in bounds.
 template <int STAGE, int COLOR, bool HALF, int DEG>
 __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
                           const float (&d)[3], const float (&b)[16], ColorCache& cache, bool want_exit, CellEval& R,
@@ -337,14 +346,27 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
     const int last = e1 - 1;
     R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
     blend_init(R.B);
+#if VGR_EDGE_AHEAD >= 2
     float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
     int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
     SiteRec q = site_rec<STAGE>(S, k);
+#endif
     for (int e = e0; e < e1; ++e) {
+#if VGR_EDGE_AHEAD >= 2
         const int e2 = min(e + 2, last);
         const float4 ed2 = S.edge[e2];
         const int k2 = S.nbr[e2];
+#else
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
         const SiteRec qn = site_rec<STAGE>(S, k1);
+#else
+        const SiteRec q = site_rec<STAGE>(S, k);
+#endif
         if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
         if (STAGE >= 1) {
             float v0, v1, v2, r2;
@@ -377,12 +399,17 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                 }
             }
         }
-        ed = ed1, k = k1, ed1 = ed2, k1 = k2, q = qn;
+#if VGR_EDGE_AHEAD >= 2
+        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
+        q = qn;
+#endif
     }
 }
 
-// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin; pipelined like
-// eval_cell.
+// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin; pipelined as
+// eval_cell is.
 template <bool HALF, int DEG>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
                            const float (&d)[3], const float (&b)[16], ColorCache& cache, float (&C)[3], int& n_sh) {
@@ -392,15 +419,29 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
     const int last = e1 - 1;
     const float cut = mmin + P.color_cut;
     float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
+#if VGR_EDGE_AHEAD >= 2
     float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
     int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
     float4 q2 = S.attr[5 * static_cast<int64_t>(k) + 2], q3 = S.attr[5 * static_cast<int64_t>(k) + 3];
+#endif
     for (int e = e0; e < e1; ++e) {
+#if VGR_EDGE_AHEAD >= 2
         const int e2 = min(e + 2, last);
         const float4 ed2 = S.edge[e2];
         const int k2 = S.nbr[e2];
+#else
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
         const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
         const float4 n2 = a[2], n3 = a[3];
+#else
+        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+        const float4 q2 = a[2], q3 = a[3];
+#endif
         float v0, v1, v2, r2;
         offset_of(x, ed, v0, v1, v2, r2);
         if (r2 * cutoffs(ed.w).y <= cut) {
@@ -412,7 +453,12 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
                 accumulate(A, r, g, bl, weight_of(m, mmin), c3);
             }
         }
-        ed = ed1, k = k1, ed1 = ed2, k1 = k2, q2 = n2, q3 = n3;
+#if VGR_EDGE_AHEAD >= 2
+        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
+#endif
+#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
+        q2 = n2, q3 = n3;
+#endif
     }
     const float inv = 1.f / A;
     C[0] = r * inv, C[1] = g * inv, C[2] = bl * inv;
@@ -423,9 +469,11 @@ __device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O,
     if (TRACE && s < O.trace_cap) O.trace[r * O.trace_cap + s] = S.orig != nullptr ? S.orig[c] : c;
 }
 
-// Waves per SIMD the register allocation is bounded for (VGR_WAVES; 0 leaves it to the compiler).
+// Waves per SIMD the register allocation is bounded for (VGR_WAVES; 0 leaves it to the compiler). At 6 the
+// fused fp32 degree-3 kernel spills 12 VGPRs and is the fastest measured: 207 ms on config 3 against 233 ms at 4
+// (114 VGPRs, no spills); 7 waves spill 45 and take 257 ms.
 #ifndef VGR_WAVES
-#define VGR_WAVES 4
+#define VGR_WAVES 6
 #endif
 
 template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
