@@ -147,50 +147,55 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
 #pragma clang fp contract(off)
 // ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
-// Colour blocks of site k for this ray come through the wave-shared LDS cache of SH coefficient blocks: kSlots
-// direct-mapped slots (site k mod kSlots), stored [12][kSlots] float4 so that lanes reading different slots hit
+// Colour blocks of site k for this ray come through the wave-shared LDS cache of SH coefficient blocks: SLOTS
+// direct-mapped slots (site k mod SLOTS), stored [12][SLOTS] float4 so that lanes reading different slots hit
 // different banks. The 64 rays of a tile read overlapping sets of sites (45 % of the lookups find their block in
-// LDS on the config-3 scene); the colour itself, max(SH_k(d) + 1/2, 0), is evaluated per lane since it depends on
-// the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup. 30 slots keep the cache at 6.0 KB
-// per wave, so that 24 waves (6 per SIMD) fit in a CU's 160 KB of LDS: more waves per SIMD gain more than a
-// larger cache (48 slots at 4 waves, 36 at 5 and 26 at 7 were all slower).
-#ifndef VGR_SLOTS
-#define VGR_SLOTS 30
-#endif
-// Software pipelining of the neighbourhood loops: VGR_EDGE_AHEAD = 2 loads the edge records two edges ahead,
-// VGR_REC_AHEAD (with it) the site records one ahead. Both off: the registers they hold are worth more as a sixth
-// wave per SIMD, whose loads cover the latency instead.
-#ifndef VGR_REC_AHEAD
-#define VGR_REC_AHEAD 0
-#endif
-#ifndef VGR_EDGE_AHEAD
-#define VGR_EDGE_AHEAD 0
-#endif
-constexpr int kSlots = VGR_SLOTS;
+// LDS on the config-3 scene with 48 slots); the colour itself, max(SH_k(d) + 1/2, 0), is evaluated per lane since
+// it depends on the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup.
+//
+// Tuning per colour mode, measured on config 3. Fused and baked colours: 30 slots (6.0 KB of LDS per wave), so that
+// 24 waves (6 per SIMD) fit in a CU's 160 KB, and no software pipelining: the registers that pipelined loads hold
+// are worth more as a sixth wave, whose loads cover the latency instead (48 slots at 4 waves, 36 at 5 and 26 at 7
+// were all slower: 233, 216 and 257 ms against 207). Lazy colours keep 48 slots, 4 waves and the pipelined loops
+// (edge records two edges ahead, site records one ahead): 287 ms against 305 with the fused tuning.
+template <int COLOR>
+struct Tune {
+    static constexpr int slots = COLOR == kLazy ? 48 : 30;
+    static constexpr int waves = COLOR == kLazy ? 4 : 6;
+    static constexpr bool pipelined = COLOR == kLazy;
+};
 
-__device__ __forceinline__ int slot_of(int k) { return static_cast<int>(static_cast<uint32_t>(k) % kSlots); }
+template <int SLOTS>
+__device__ __forceinline__ int slot_of(int k) {
+    return static_cast<int>(static_cast<uint32_t>(k) % SLOTS);
+}
 
 // Volatile ints typed as LDS: the election and tag accesses stay ds_read / ds_write. Through a generic pointer
 // they would be flat accesses, after each of which the wave waits for all of its outstanding global loads.
 typedef __attribute__((address_space(3))) volatile int lds_int;
 
+template <int SLOTS>
 struct ColorCache {
-    float4* data;    // [12][kSlots] coefficient blocks
+    float4* data;    // [12][SLOTS] coefficient blocks
     lds_int* tag;    // site held by each slot (-1: empty)
     lds_int* claim;  // election word of each slot
     lds_int* req;    // sites being fetched in the current fill
 };
 
 // LDS footprint per block of the colour cache, in float4 units (tag, claim and request arrays follow the blocks).
-constexpr int cache_vec4(bool sh) { return sh ? 12 * kSlots + (3 * kSlots + 3) / 4 : 1; }
+template <int SLOTS>
+constexpr int cache_vec4(bool sh) {
+    return sh ? 12 * SLOTS + (3 * SLOTS + 3) / 4 : 1;
+}
 
-__device__ __forceinline__ ColorCache make_cache(float4* lds) {
-    ColorCache C;
+template <int SLOTS>
+__device__ __forceinline__ ColorCache<SLOTS> make_cache(float4* lds) {
+    ColorCache<SLOTS> C;
     C.data = lds;
-    C.tag = (lds_int*)(lds + 12 * kSlots);
-    C.claim = C.tag + kSlots;
-    C.req = C.claim + kSlots;
-    for (int i = threadIdx.x; i < kSlots; i += kBlock) C.tag[i] = -1, C.claim[i] = -1, C.req[i] = 0;
+    C.tag = (lds_int*)(lds + 12 * SLOTS);
+    C.claim = C.tag + SLOTS;
+    C.req = C.claim + SLOTS;
+    for (int i = threadIdx.x; i < SLOTS; i += kBlock) C.tag[i] = -1, C.claim[i] = -1, C.req[i] = 0;
     __syncthreads();
     return C;
 }
@@ -211,11 +216,11 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // lane per load, about five blocks per instruction); then every lane whose block is now in LDS reads it and
 // evaluates its colour. Lanes whose slot was pinned by, or went to, another site wait for the next pass; every pass
 // serves at least one slot, so the loop ends (usually after one pass, two in about a third of the rounds).
-template <bool HALF, int NV>
-__device__ __forceinline__ void cached_colour(ColorCache& C, const float4* __restrict__ sh, int k, const float (&b)[16],
-                                              float (&c)[3]) {
+template <bool HALF, int NV, int SLOTS>
+__device__ __forceinline__ void cached_colour(ColorCache<SLOTS>& C, const float4* __restrict__ sh, int k,
+                                              const float (&b)[16], float (&c)[3]) {
     const int lane = static_cast<int>(threadIdx.x);
-    const int slot = slot_of(k);
+    const int slot = slot_of<SLOTS>(k);
     const uint64_t active = __ballot(1);
     const int n_active = __popcll(active), rank = lanes_below(active);
     bool pending = true;
@@ -240,7 +245,7 @@ __device__ __forceinline__ void cached_colour(ColorCache& C, const float4* __res
                 if (j < total) {
                     const int r = j / NV, q = j - r * NV;
                     const int kr = C.req[r];
-                    C.data[q * kSlots + slot_of(kr)] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
+                    C.data[q * SLOTS + slot_of<SLOTS>(kr)] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
                 }
             }
             __builtin_amdgcn_wave_barrier();  // publish the tags after the blocks
@@ -255,7 +260,7 @@ __device__ __forceinline__ void cached_colour(ColorCache& C, const float4* __res
                 float4 f[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
-                    if (q0 + u < NV) f[u] = C.data[(q0 + u) * kSlots + slot];
+                    if (q0 + u < NV) f[u] = C.data[(q0 + u) * SLOTS + slot];
                 sh_accumulate<HALF>(f, q0, NV, b, c);
                 __builtin_amdgcn_sched_barrier(0);  // one chunk of the block in registers at a time
             }
@@ -332,12 +337,12 @@ __device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
 
 // One pass over the self-first neighbourhood of cell c for the sample o + t d: density, smallest colour
 // Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
-// With VGR_EDGE_AHEAD = 2 the loop is software-pipelined: the edge record of e + 2 (and with VGR_REC_AHEAD the site
-// records of e + 1) are loaded while edge e is evaluated, indices clamped to the cell so every load stays in bounds.
+// Pipelined (Tune): the edge record of e + 2 and the site records of e + 1 are loaded while edge e is evaluated,
+// indices clamped to the cell so every load stays in bounds.
 template <int STAGE, int COLOR, bool HALF, int DEG>
 __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
-                          const float (&d)[3], const float (&b)[16], ColorCache& cache, bool want_exit, CellEval& R,
-                          int& n_dens, int& n_sh) {
+                          const float (&d)[3], const float (&b)[16], ColorCache<Tune<COLOR>::slots>& cache,
+                          bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
     const float4 pc = S.points[c];
     float x[3];
@@ -346,27 +351,28 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
     const int last = e1 - 1;
     R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
     blend_init(R.B);
-#if VGR_EDGE_AHEAD >= 2
-    float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
-    int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-    SiteRec q = site_rec<STAGE>(S, k);
-#endif
+    constexpr bool PIPE = Tune<COLOR>::pipelined;
+    // the edge and site records of e (and, pipelined, of e + 1 and e + 2)
+    float4 ed, ed1;
+    int k, k1;
+    SiteRec q;
+    if constexpr (PIPE) {
+        ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
+        k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+        q = site_rec<STAGE>(S, k);
+    }
     for (int e = e0; e < e1; ++e) {
-#if VGR_EDGE_AHEAD >= 2
-        const int e2 = min(e + 2, last);
-        const float4 ed2 = S.edge[e2];
-        const int k2 = S.nbr[e2];
-#else
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-        const SiteRec qn = site_rec<STAGE>(S, k1);
-#else
-        const SiteRec q = site_rec<STAGE>(S, k);
-#endif
+        float4 ed2;
+        int k2;
+        SiteRec qn;
+        if constexpr (PIPE) {
+            const int e2 = min(e + 2, last);
+            ed2 = S.edge[e2], k2 = S.nbr[e2];
+            qn = site_rec<STAGE>(S, k1);
+        } else {
+            ed = S.edge[e], k = S.nbr[e];
+            q = site_rec<STAGE>(S, k);
+        }
         if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
         if (STAGE >= 1) {
             float v0, v1, v2, r2;
@@ -399,49 +405,43 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                 }
             }
         }
-#if VGR_EDGE_AHEAD >= 2
-        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-        q = qn;
-#endif
+        if constexpr (PIPE) ed = ed1, k = k1, ed1 = ed2, k1 = k2, q = qn;
     }
 }
 
-// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin; pipelined as
-// eval_cell is.
+// Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin (lazy mode only,
+// pipelined as eval_cell is).
 template <bool HALF, int DEG>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
-                           const float (&d)[3], const float (&b)[16], ColorCache& cache, float (&C)[3], int& n_sh) {
+                           const float (&d)[3], const float (&b)[16], ColorCache<Tune<kLazy>::slots>& cache,
+                           float (&C)[3], int& n_sh) {
     float x[3];
     sample_point(o, d, t, x);
     const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
     const int last = e1 - 1;
     const float cut = mmin + P.color_cut;
     float A = 0.f, r = 0.f, g = 0.f, bl = 0.f;
-#if VGR_EDGE_AHEAD >= 2
-    float4 ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
-    int k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-    float4 q2 = S.attr[5 * static_cast<int64_t>(k) + 2], q3 = S.attr[5 * static_cast<int64_t>(k) + 3];
-#endif
+    constexpr bool PIPE = Tune<kLazy>::pipelined;
+    float4 ed, ed1, q2, q3;
+    int k, k1;
+    if constexpr (PIPE) {
+        ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
+        k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+        q2 = S.attr[5 * static_cast<int64_t>(k) + 2], q3 = S.attr[5 * static_cast<int64_t>(k) + 3];
+    }
     for (int e = e0; e < e1; ++e) {
-#if VGR_EDGE_AHEAD >= 2
-        const int e2 = min(e + 2, last);
-        const float4 ed2 = S.edge[e2];
-        const int k2 = S.nbr[e2];
-#else
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-        const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
-        const float4 n2 = a[2], n3 = a[3];
-#else
-        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
-        const float4 q2 = a[2], q3 = a[3];
-#endif
+        float4 ed2, n2, n3;
+        int k2;
+        if constexpr (PIPE) {
+            const int e2 = min(e + 2, last);
+            ed2 = S.edge[e2], k2 = S.nbr[e2];
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k1);
+            n2 = a[2], n3 = a[3];
+        } else {
+            ed = S.edge[e], k = S.nbr[e];
+            const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+            q2 = a[2], q3 = a[3];
+        }
         float v0, v1, v2, r2;
         offset_of(x, ed, v0, v1, v2, r2);
         if (r2 * cutoffs(ed.w).y <= cut) {
@@ -453,12 +453,7 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
                 accumulate(A, r, g, bl, weight_of(m, mmin), c3);
             }
         }
-#if VGR_EDGE_AHEAD >= 2
-        ed = ed1, k = k1, ed1 = ed2, k1 = k2;
-#endif
-#if VGR_REC_AHEAD && VGR_EDGE_AHEAD >= 2
-        q2 = n2, q3 = n3;
-#endif
+        if constexpr (PIPE) ed = ed1, k = k1, ed1 = ed2, k1 = k2, q2 = n2, q3 = n3;
     }
     const float inv = 1.f / A;
     C[0] = r * inv, C[1] = g * inv, C[2] = bl * inv;
@@ -469,21 +464,18 @@ __device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O,
     if (TRACE && s < O.trace_cap) O.trace[r * O.trace_cap + s] = S.orig != nullptr ? S.orig[c] : c;
 }
 
-// Waves per SIMD the register allocation is bounded for (VGR_WAVES; 0 leaves it to the compiler). At 6 the
-// fused fp32 degree-3 kernel spills 12 VGPRs and is the fastest measured: 207 ms on config 3 against 233 ms at 4
-// (114 VGPRs, no spills); 7 waves spill 45 and take 257 ms.
-#ifndef VGR_WAVES
-#define VGR_WAVES 6
-#endif
-
+// The register allocation is bounded for Tune<COLOR>::waves waves per SIMD. At 6 the fused fp32 degree-3 kernel
+// spills 12 VGPRs and is the fastest measured (207 ms on config 3); at 4 it takes 114 VGPRs and 233 ms, at 7 it
+// spills 45 and takes 257 ms.
 template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
-__global__ void __launch_bounds__(kBlock, VGR_WAVES)
+__global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    __shared__ float4 cache_lds[cache_vec4(kSH)];
-    ColorCache cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache(cache_lds);
+    constexpr int SLOTS = Tune<COLOR>::slots;
+    __shared__ float4 cache_lds[cache_vec4<SLOTS>(kSH)];
+    ColorCache<SLOTS> cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache<SLOTS>(cache_lds);
     const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
     if (r >= R.n) return;
     const int start = R.start[r];
@@ -535,7 +527,7 @@ __global__ void __launch_bounds__(kBlock, VGR_WAVES)
             CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv, hasQ = true;
         }
         if (STAGE >= 2 && w > P.w_thresh) {
-            if (!BLEND) {
+            if constexpr (!BLEND) {
                 if (!hasP) color_lazy<HALF, DEG>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
                 color_lazy<HALF, DEG>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
                 hasQ = true;
