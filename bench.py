@@ -11,6 +11,7 @@ on the launch stream) and the CPU oracle timed on the host on a bounded, determi
 Other rows of the path, each as one JSON line of the same form (not the headline):
   --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
   --workload locate   start-cell location on config 5 (nearest site of 16,777,216 ray origins among 4M sites)
+  --workload pack     pack_foam with Z-order renumbering on config 3 (the step before the kernel)
   --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
                       one 1920x1080 frame at 64 stratified samples per ray (render_rays' first round)
 """
@@ -115,7 +116,7 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
-	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field'],
+	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
 	args = ap.parse_args()
@@ -134,6 +135,8 @@ def main():
 		return bench_locate(args)
 	if args.workload == 'field':
 		return bench_field(args)
+	if args.workload == 'pack':
+		return bench_pack(args)
 	bench_foam(args)
 
 
@@ -456,6 +459,61 @@ def bench_march(args):
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
 		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)
+
+
+def bench_pack(args):
+	"""The step before the kernel (render.py:168-225): pack_foam with the Z-order renumbering of the config-3 scene
+	(conics on the GPU, self-first CSR, edge records with the half2 cut-offs, site records, SH rows), from the model's
+	device tensors, timed whole. CPU baseline: the same pack on host tensors (torch on the host cores), whose
+	non-renumbered records must equal the GPU's bit for bit."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	sc = scenes.make_scene(args.config, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	N, M = sc.n_sites, len(sc.adj)
+	stream = torch.cuda.current_stream(dev)
+	torch.cuda.synchronize()
+	torch.cuda.reset_peak_memory_stats()
+	base = torch.cuda.memory_allocated()
+	launch_ms, pk, wall = time_steps(lambda: render.pack_foam(model, reorder=True), args.steps, args.warmup, stream)
+	peak = (torch.cuda.max_memory_allocated() - base) / 2 ** 30
+	ms = float(np.mean(launch_ms))
+	log(f'pack_foam (reorder) of {N} sites, {M} adjacency entries: mean {ms:.3f} ms, wall {wall:.3f} ms/step, '
+		f'peak +{peak:.2f} GiB')
+	# compulsory bytes: inputs (points 12, offsets 4, raw 4, log-scales 24, quaternions 32, SH 192 per site, adjacency
+	# 4 per entry) read once; outputs (points 16, offsets 4, attr 80, SH 192, perm/inv/orig 20 per site, nbr 4 and
+	# edge 16 per self-first entry) written once
+	shb = 192
+	abytes = float(N * (12 + 4 + 4 + 24 + 32 + shb) + 4 * M + N * (16 + 4 + 80 + shb + 20) + (M + N) * 20)
+	achieved = abytes / (ms * 1e-3) / 1e9
+	cpu = None
+	if args.cpu_seconds > 0:
+		# the host pack takes the device conics (conic_forward is its own row), then builds everything else
+		g = model.graph
+		dA = ext.conic(model.d_log_scale, model.d_quat, 0.0)
+		cA = ext.conic(model.c_log_scale, model.c_quat, 0.0)
+		hin = [x.detach().cpu() for x in (g.points, g.offsets, g.adj, model.raw, model.d_log_scale,
+										  model.c_log_scale, dA, cA, model.sh())]
+		t0 = time.perf_counter()
+		render.pack_foam_arrays(*hin, reorder=True)
+		t_cpu = time.perf_counter() - t0
+		g0, r0 = render.pack_foam(model, reorder=False), render.pack_foam_arrays(*hin, reorder=False)
+		same = all(torch.equal(g0[k].cpu(), r0[k]) for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh'))
+		log(f'cpu pack (torch, {torch.get_num_threads()} threads): {t_cpu:.2f} s; GPU records equal to the host '
+			f'ones without renumbering: {same}')
+		cpu = {'value': round(N / t_cpu / 1e6, 4), 'unit': 'Msites/s', 'cores': torch.get_num_threads(), 'kind': 'port',
+			   'sample': f'the whole {N}-site pack with renumbering, torch on host tensors, from the device conics',
+			   'parity_bitwise': same}
+	emit(f'Msites/s pack_foam with Z-order renumbering (config {args.config}: {N} sites) on 1 MI355X', N / ms / 1e3,
+		 'Msites/s', args, ms,
+		 {'workload': f'config {args.config} pack: {N} sites, {M} adjacency entries, SH degree {sc.sh_deg}, Z-order '
+					  f'renumbering', 'sites': N, 'adjacency': M, 'peak_extra_GiB': round(peak, 2)},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
 
 
 def bench_field(args):
