@@ -502,12 +502,18 @@ def bench_pack(args):
 		render.pack_foam_arrays(*hin, reorder=True)
 		t_cpu = time.perf_counter() - t0
 		g0, r0 = render.pack_foam(model, reorder=False), render.pack_foam_arrays(*hin, reorder=False)
-		same = all(torch.equal(g0[k].cpu(), r0[k]) for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh'))
-		log(f'cpu pack (torch, {torch.get_num_threads()} threads): {t_cpu:.2f} s; GPU records equal to the host '
-			f'ones without renumbering: {same}')
+		# copied fields must match bit for bit; the cut-off words come from torch exp on two devices (a few ulps
+		# apart) rounded to half, so a rare one may differ in its last half bit
+		same = all(torch.equal(g0[k].cpu(), r0[k]) for k in ('points', 'offsets', 'nbr', 'attr', 'sh'))
+		same = same and torch.equal(g0['edge'][:, :3].cpu(), r0['edge'][:, :3])
+		cut_g = g0['edge'][:, 3].cpu().view(torch.int32)
+		cut_r = r0['edge'][:, 3].view(torch.int32)
+		cut_diff = float((cut_g != cut_r).double().mean())
+		log(f'cpu pack (torch, {torch.get_num_threads()} threads): {t_cpu:.2f} s; copied fields equal to the host '
+			f'ones without renumbering: {same}; cut-off words differing: {cut_diff:.2e} of the edges')
 		cpu = {'value': round(N / t_cpu / 1e6, 4), 'unit': 'Msites/s', 'cores': torch.get_num_threads(), 'kind': 'port',
 			   'sample': f'the whole {N}-site pack with renumbering, torch on host tensors, from the device conics',
-			   'parity_bitwise': same}
+			   'parity_bitwise_copied_fields': same, 'parity_cut_words_differing': cut_diff}
 	emit(f'Msites/s pack_foam with Z-order renumbering (config {args.config}: {N} sites) on 1 MI355X', N / ms / 1e3,
 		 'Msites/s', args, ms,
 		 {'workload': f'config {args.config} pack: {N} sites, {M} adjacency entries, SH degree {sc.sh_deg}, Z-order '
