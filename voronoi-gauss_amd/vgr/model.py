@@ -70,3 +70,42 @@ class VoronoiGaussField(nn.Module):
 
 	def walk(self, o, d, z, start):
 		return self.graph.walk(o, d, z, start)
+
+
+# numpy types a reference checkpoint's `normalization` (center array, scale scalar) is made of: the only globals the
+# checkpoint loader lets the unpickler build, so loading executes nothing from the file
+def _numpy_safe_globals():
+	import numpy as np
+	names = [np.ndarray, np.dtype, np.float64, np.float32, type(np.dtype(np.float64)), type(np.dtype(np.float32))]
+	try:
+		from numpy._core.multiarray import _reconstruct, scalar
+	except ImportError:  # numpy < 2
+		from numpy.core.multiarray import _reconstruct, scalar
+	return names + [_reconstruct, scalar]
+
+
+def load_checkpoint(path, device='cuda'):
+	"""The dict a reference training run saves as model.pth (train.py:168-170): 'state' (the field's state_dict),
+	'points', 'offsets', 'adj', 'sh_deg', 'normalization' ((center, scale) of the COLMAP scene) and 'args'. Loaded
+	with torch.load(weights_only=True), numpy's array and scalar types allowed for the normalization; any other
+	object in the file is refused."""
+	with torch.serialization.safe_globals(_numpy_safe_globals()):
+		ck = torch.load(path, map_location=device, weights_only=True)
+	missing = [k for k in ('state', 'points', 'offsets', 'adj', 'sh_deg') if k not in ck]
+	if missing:
+		raise KeyError(f'{path}: not a voronoi-gauss checkpoint (missing {", ".join(missing)})')
+	return ck
+
+
+def load_model(path, device='cuda'):
+	"""-> (VoronoiGaussField, checkpoint dict): the trained field of a reference model.pth, frozen for rendering
+	(bench_fps.py:19-28)."""
+	ck = load_checkpoint(path, device)
+	pts = ck['points']
+	n = len(pts)
+	model = VoronoiGaussField(pts, ck['offsets'], ck['adj'], torch.zeros(n, 3, device=device),
+							  torch.ones(n, device=device))
+	model.load_state_dict(ck['state'])
+	model.sh_deg = int(ck['sh_deg'])
+	model.requires_grad_(False)
+	return model, ck
