@@ -105,7 +105,8 @@ int vgr_walk(const float* points, int64_t n_sites, const int32_t* offsets, const
  */
 int vgr_density_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                         int64_t n_adj, const float* raw, const float* log_scale, const float* quat, const float* x,
-                        const int32_t* site, int64_t m, double scale_mult, float* sigma, void* stream);
+                        const int32_t* site, int64_t m, double scale_mult, float* sigma, void* work,
+                        int64_t work_bytes, void* stream);
 
 /*
  * Normalised blend of max(SH_k(d) + 1/2, 0) over the Voronoi neighbourhood of site. Replaces color_forward()
@@ -114,7 +115,16 @@ int vgr_density_forward(const float* points, int64_t n_sites, const int32_t* off
  */
 int vgr_color_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                       int64_t n_adj, const float* log_scale, const float* quat, const float* sh, int64_t sh_deg,
-                      const float* x, const float* dirs, const int32_t* site, int64_t m, float* rgb, void* stream);
+                      const float* x, const float* dirs, const int32_t* site, int64_t m, float* rgb, void* work,
+                      int64_t work_bytes, void* stream);
+
+/*
+ * Optional device scratch of vgr_density_forward and vgr_color_forward (work may be NULL): with at least
+ * vgr_field_work_size(N) bytes (16-byte aligned) and m >= N / 8 samples, the Gaussian of every site is built once per
+ * call (rotation rows and inverse variances, the arithmetic each neighbour would repeat) and the per-sample kernels
+ * read it; results are bit-identical either way. Calls sharing one work buffer must be ordered on one stream.
+ */
+int64_t vgr_field_work_size(int64_t n_sites);
 
 /*
  * Conics A = R diag(1 / (s^2 + floor^2)) R^T as (xx, xy, xz, yy, yz, zz). Replaces conic_forward() of

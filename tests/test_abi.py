@@ -25,8 +25,8 @@ def declared():
 def test_header_declares_the_entry_points():
 	names = declared()
 	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_march_forward', 'vgr_march_work_size', 'vgr_walk',
-			  'vgr_density_forward', 'vgr_color_forward', 'vgr_conic_forward', 'vgr_grid_work_size', 'vgr_grid_build', 'vgr_grid_nearest',
-			  'vgr_last_error', 'vgr_abi_version'):
+			  'vgr_density_forward', 'vgr_color_forward', 'vgr_field_work_size', 'vgr_conic_forward',
+			  'vgr_grid_work_size', 'vgr_grid_build', 'vgr_grid_nearest', 'vgr_last_error', 'vgr_abi_version'):
 		assert n in names
 
 
@@ -78,3 +78,5 @@ def test_library_reports_argument_errors_without_a_gpu():
 	assert lib.vgr_march_forward(*margs) == 1 and b'256-byte aligned' in lib.vgr_last_error()
 	margs[16] = 0  # no rays: nothing to check or launch
 	assert lib.vgr_march_forward(*margs) == 0
+	# field records: 64 bytes per site
+	assert lib.vgr_field_work_size(0) == 0 and lib.vgr_field_work_size(1000) == 64000

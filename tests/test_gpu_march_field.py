@@ -111,6 +111,33 @@ def test_density_color_conic_vs_oracle(gpu):
 	assert empty.shape == (0,)
 
 
+def test_density_color_records_bit_identical(gpu):
+	"""density_forward / color_forward with per-site Gaussian records (a call of m >= N / 8 samples given scratch)
+	and without (no scratch, or a call too small for them) give the same bits."""
+	f = Field(seed=3, n=500, lo=-1.0, hi=1.0, raw_mu=0.5, ls_mu=-1.5)
+	rng = np.random.default_rng(9)
+	x = rng.uniform(-1, 1, (2000, 3)).astype(np.float32)
+	site = f.tree.query(x)[1].astype(np.int32)
+	dirs = rng.normal(size=(2000, 3)).astype(np.float32)
+	e = ext.extension()
+	args = [T(a, gpu) for a in (f.points, f.offsets, f.adj)]
+	for mult in (1.0, 4.0):
+		dens = [e.density_forward(*args, T(f.raw, gpu), T(f.d_log_scale, gpu), T(f.d_quat, gpu), T(x, gpu),
+								  T(site, gpu), mult, records=rec).cpu().numpy() for rec in (True, False)]
+		np.testing.assert_array_equal(dens[0], dens[1])
+	for deg in (1, 3):
+		col = [e.color_forward(*args, T(f.c_log_scale, gpu), T(f.c_quat, gpu), T(f.sh, gpu), deg, T(x, gpu),
+							   T(dirs, gpu), T(site, gpu), records=rec).cpu().numpy() for rec in (True, False)]
+		np.testing.assert_array_equal(col[0], col[1])
+	# 40 samples over 500 sites: below N / 8, the direct kernel runs with or without scratch
+	small = [e.density_forward(*args, T(f.raw, gpu), T(f.d_log_scale, gpu), T(f.d_quat, gpu), T(x[:40], gpu),
+							   T(site[:40], gpu), 2.0, records=rec).cpu().numpy() for rec in (True, False)]
+	np.testing.assert_array_equal(small[0], small[1])
+	np.testing.assert_array_equal(small[0], e.density_forward(*args, T(f.raw, gpu), T(f.d_log_scale, gpu),
+															  T(f.d_quat, gpu), T(x, gpu), T(site, gpu),
+															  2.0).cpu().numpy()[:40])
+
+
 def test_render_rays_nerf_path(gpu):
 	"""render_rays (NeRF sampling + walk/density/color kernels) on GPU equals the same host code run on CPU with
 	the oracle's operators."""

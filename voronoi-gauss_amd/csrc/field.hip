@@ -88,6 +88,78 @@ __device__ __forceinline__ float gauss_m(const Graph& g, const Gauss& G, int i, 
     return m;
 }
 
+// Per-site Gaussian records, built once per call by gauss_pack_kernel with gauss_m's own arithmetic, so that the
+// per-neighbour work is the rotation and the sum only: rec[4i .. 4i + 2] = rows of R with the inverse variances
+// (R0, R1, R2, is2_0), (R3, R4, R5, is2_1), (R6, R7, R8, is2_2); rec[4i + 3] = (p_i, min(raw_i, 30)) (0 without raw).
+// gauss_m rebuilds R from the quaternion (four divisions, a square root) and takes three exponentials and three
+// more divisions for every neighbour of every sample; a call with m samples over N sites does that m E / N times
+// per site.
+constexpr int kGRec = 4;
+
+__global__ void __launch_bounds__(kBlock)
+    gauss_pack_kernel(Graph g, Gauss G, const float* __restrict__ raw, float inv_mult2, float4* __restrict__ rec) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= g.n_sites) return;
+    const float4 q = G.quat[i];
+    const float qnorm = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
+    const float w = q.x / qnorm, a = q.y / qnorm, b = q.z / qnorm, c = q.w / qnorm;
+    const float R[9] = {1.f - 2.f * (b * b + c * c), 2.f * (a * b - w * c),       2.f * (a * c + w * b),
+                        2.f * (a * b + w * c),       1.f - 2.f * (a * a + c * c), 2.f * (b * c - w * a),
+                        2.f * (a * c - w * b),       2.f * (b * c + w * a),       1.f - 2.f * (a * a + b * b)};
+    float is2[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float s = fexp(fminf(fmaxf(G.log_scale[3 * i + k], -20.f), 20.f));
+        is2[k] = inv_mult2 / (s * s);
+    }
+    float4* r = rec + kGRec * i;
+    r[0] = make_float4(R[0], R[1], R[2], is2[0]);
+    r[1] = make_float4(R[3], R[4], R[5], is2[1]);
+    r[2] = make_float4(R[6], R[7], R[8], is2[2]);
+    r[3] = make_float4(g.points[3 * i], g.points[3 * i + 1], g.points[3 * i + 2],
+                       raw != nullptr ? fminf(raw[i], 30.f) : 0.f);
+}
+
+// gauss_m of site i from its record; raw_c = min(raw_i, 30).
+__device__ __forceinline__ float gauss_m_rec(const float4* __restrict__ rec, int i, float x, float y, float z,
+                                             float& raw_c) {
+    const float4* r = rec + kGRec * static_cast<int64_t>(i);
+    const float4 r0 = r[0], r1 = r[1], r2 = r[2], r3 = r[3];
+    const float v0 = x - r3.x, v1 = y - r3.y, v2 = z - r3.z;
+    const float c0[3] = {r0.x, r0.y, r0.z}, c1[3] = {r1.x, r1.y, r1.z}, c2[3] = {r2.x, r2.y, r2.z};
+    const float is2[3] = {r0.w, r1.w, r2.w};
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float yk = c0[k] * v0 + c1[k] * v1 + c2[k] * v2;
+        m += yk * yk * is2[k];
+    }
+    raw_c = r3.w;
+    return m;
+}
+
+__global__ void __launch_bounds__(kBlock)
+    density_forward_packed_kernel(Graph g, const float4* __restrict__ rec, const float* __restrict__ x,
+                                  const int* __restrict__ site, int64_t m, float* __restrict__ sigma) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (t >= m) return;
+    const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
+    const int i = site[t];
+    if (i < 0 || i >= g.n_sites) {
+        sigma[t] = 0.f;
+        return;
+    }
+    float s = 0.f;
+    const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
+    for (int e = e0 - 1; e < e1; ++e) {
+        const int k = e < e0 ? i : g.adj[e];
+        float raw_c;
+        const float mk = gauss_m_rec(rec, k, qx, qy, qz, raw_c);
+        s += fexp(raw_c - 0.5f * mk);
+    }
+    sigma[t] = s;
+}
+
 __global__ void __launch_bounds__(kBlock)
     density_forward_kernel(Graph g, const float* __restrict__ raw, Gauss G, const float* __restrict__ x,
                            const int* __restrict__ site, int64_t m, float inv_mult2, float* __restrict__ sigma) {
@@ -167,6 +239,49 @@ __global__ void __launch_bounds__(kBlock)
     rgb[3 * t + 2] = cb / A;
 }
 
+template <int DEG>
+__global__ void __launch_bounds__(kBlock)
+    color_forward_packed_kernel(Graph g, const float4* __restrict__ rec, const float4* __restrict__ sh, const float* __restrict__ x,
+                         const float* __restrict__ dirs, const int* __restrict__ site, int64_t m,
+                         float* __restrict__ rgb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (t >= m) return;
+    const int i = site[t];
+    if (i < 0 || i >= g.n_sites) {
+        rgb[3 * t] = rgb[3 * t + 1] = rgb[3 * t + 2] = 0.f;
+        return;
+    }
+    const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
+    float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
+    const float inv = rsqrtf(fmaxf(dx * dx + dy * dy + dz * dz, 1e-20f));
+    dx *= inv, dy *= inv, dz *= inv;
+    float b[16];
+    sh_basis(dx, dy, dz, DEG, b);
+    constexpr int nb = (DEG + 1) * (DEG + 1);
+    float mmin = kInf, A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
+    const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
+    for (int e = e0 - 1; e < e1; ++e) {
+        const int k = e < e0 ? i : g.adj[e];
+        float raw_c;
+        const float mk = gauss_m_rec(rec, k, qx, qy, qz, raw_c);
+        if (mk < mmin) {
+            const float f = mmin == kInf ? 0.f : fexp(-0.5f * (mmin - mk));
+            A *= f, cr *= f, cg *= f, cb *= f;
+            mmin = mk;
+        }
+        const float a = fexp(-0.5f * (mk - mmin));
+        float c[3];
+        sh_eval_n<sh_vec4_f32(DEG)>(sh, k, b, nb, c);
+        A += a;
+        cr += a * fmaxf(c[0], 0.f);
+        cg += a * fmaxf(c[1], 0.f);
+        cb += a * fmaxf(c[2], 0.f);
+    }
+    rgb[3 * t] = cr / A;
+    rgb[3 * t + 1] = cg / A;
+    rgb[3 * t + 2] = cb / A;
+}
+
 __global__ void __launch_bounds__(kBlock)
     conic_forward_kernel(const float* __restrict__ log_scale, const float4* __restrict__ quat, int64_t n,
                          float floor2, float* __restrict__ A) {
@@ -193,6 +308,13 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
+// The records pay for themselves once a call has about N / 8 samples (their build reads and writes each site once;
+// the gauss_m work they remove is per neighbour of every sample); both paths give the same bits.
+bool use_records(const void* work, int64_t work_bytes, int64_t n_sites, int64_t m) {
+    return work != nullptr && work_bytes >= n_sites * kGRec * static_cast<int64_t>(sizeof(float4)) &&
+           reinterpret_cast<uintptr_t>(work) % 16 == 0 && m * 8 >= n_sites;
+}
+
 int check_graph(const char* op, const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                 int64_t n_adj) {
     VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "%s: n_sites must be in [1, 2^31)", op);
@@ -203,6 +325,10 @@ int check_graph(const char* op, const float* points, int64_t n_sites, const int3
 
 }  // namespace
 }  // namespace vgr
+
+extern "C" int64_t vgr_field_work_size(int64_t n_sites) {
+    return n_sites > 0 ? n_sites * vgr::kGRec * static_cast<int64_t>(sizeof(float4)) : 0;
+}
 
 extern "C" int vgr_walk(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                         int64_t n_adj, const float* o, const float* d, const float* z, const int32_t* start,
@@ -220,7 +346,7 @@ extern "C" int vgr_walk(const float* points, int64_t n_sites, const int32_t* off
 extern "C" int vgr_density_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                                    int64_t n_adj, const float* raw, const float* log_scale, const float* quat,
                                    const float* x, const int32_t* site, int64_t m, double scale_mult, float* sigma,
-                                   void* stream) {
+                                   void* work, int64_t work_bytes, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(m >= 0, "density_forward: m must be >= 0");
     if (m == 0) return VGR_OK;
@@ -228,16 +354,25 @@ extern "C" int vgr_density_forward(const float* points, int64_t n_sites, const i
     VGR_REQUIRE(raw && log_scale && quat && x && site && sigma, "density_forward: null pointer");
     VGR_REQUIRE(scale_mult != 0.0, "density_forward: scale_mult must be non-zero");
     const float inv_mult2 = static_cast<float>(1.0 / (scale_mult * scale_mult));
-    hipLaunchKernelGGL(density_forward_kernel, dim3(grid_for(m, kBlock)), dim3(kBlock), 0, as_stream(stream),
-                       Graph{points, offsets, adj, int(n_sites)}, raw,
-                       Gauss{log_scale, reinterpret_cast<const float4*>(quat)}, x, site, m, inv_mult2, sigma);
+    const Graph g{points, offsets, adj, int(n_sites)};
+    const Gauss G{log_scale, reinterpret_cast<const float4*>(quat)};
+    if (use_records(work, work_bytes, n_sites, m)) {
+        float4* rec = static_cast<float4*>(work);
+        hipLaunchKernelGGL(gauss_pack_kernel, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, as_stream(stream), g,
+                           G, raw, inv_mult2, rec);
+        hipLaunchKernelGGL(density_forward_packed_kernel, dim3(grid_for(m, kBlock)), dim3(kBlock), 0,
+                           as_stream(stream), g, rec, x, site, m, sigma);
+        return launch_status("density_forward_packed_kernel");
+    }
+    hipLaunchKernelGGL(density_forward_kernel, dim3(grid_for(m, kBlock)), dim3(kBlock), 0, as_stream(stream), g, raw, G,
+                       x, site, m, inv_mult2, sigma);
     return launch_status("density_forward_kernel");
 }
 
 extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                                  int64_t n_adj, const float* log_scale, const float* quat, const float* sh,
                                  int64_t sh_deg, const float* x, const float* dirs, const int32_t* site, int64_t m,
-                                 float* rgb, void* stream) {
+                                 float* rgb, void* work, int64_t work_bytes, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(m >= 0, "color_forward: m must be >= 0");
     VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
@@ -249,6 +384,22 @@ extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int
     const float4* s4 = reinterpret_cast<const float4*>(sh);
     const dim3 grid(grid_for(m, kBlock)), block(kBlock);
     const hipStream_t st = as_stream(stream);
+    if (use_records(work, work_bytes, n_sites, m)) {
+        const float4* rec = static_cast<const float4*>(work);
+        hipLaunchKernelGGL(gauss_pack_kernel, dim3(grid_for(n_sites, kBlock)), block, 0, st, g, H, nullptr, 1.f,
+                           static_cast<float4*>(work));
+        switch (sh_deg) {
+            case 0: hipLaunchKernelGGL(color_forward_packed_kernel<0>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
+                                       rgb); break;
+            case 1: hipLaunchKernelGGL(color_forward_packed_kernel<1>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
+                                       rgb); break;
+            case 2: hipLaunchKernelGGL(color_forward_packed_kernel<2>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
+                                       rgb); break;
+            default: hipLaunchKernelGGL(color_forward_packed_kernel<3>, grid, block, 0, st, g, rec, s4, x, dirs, site,
+                                        m, rgb); break;
+        }
+        return launch_status("color_forward_packed_kernel");
+    }
     switch (sh_deg) {
         case 0: hipLaunchKernelGGL(color_forward_kernel<0>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
         case 1: hipLaunchKernelGGL(color_forward_kernel<1>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;

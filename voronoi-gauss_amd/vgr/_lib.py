@@ -24,8 +24,9 @@ SIGNATURES = {
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
-	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P],
-	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P],
+	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P, _I64, _P],
+	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
+	'vgr_field_work_size': [_I64],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
@@ -34,7 +35,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _lib = None
 
 
@@ -52,6 +53,7 @@ def load():
 		lib.vgr_last_error.restype = ctypes.c_char_p
 		lib.vgr_grid_work_size.restype = ctypes.c_int64
 		lib.vgr_march_work_size.restype = ctypes.c_int64
+		lib.vgr_field_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

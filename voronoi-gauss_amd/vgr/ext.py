@@ -53,7 +53,8 @@ class _FieldExtension:
 		return [site, steps]
 
 	@staticmethod
-	def density_forward(points, offsets, adj, raw, log_scale, quat, x, site, scale_mult):
+	def density_forward(points, offsets, adj, raw, log_scale, quat, x, site, scale_mult, records=True):
+		"""records: give the library scratch for per-site Gaussian records (used when m >= N / 8; same bits)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
 						 (quat, 'quat', torch.float32), (raw, 'raw', torch.float32), (x, 'x', torch.float32),
@@ -63,14 +64,16 @@ class _FieldExtension:
 		sigma = torch.empty(m, dtype=torch.float32, device=x.device)
 		if m == 0:
 			return sigma
+		work, wb = _field_work(points, m, records)
 		with torch.cuda.device(x.device):
 			call('vgr_density_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(log_scale), ptr(quat), ptr(x), ptr(site), m, float(scale_mult), ptr(sigma),
-				 stream_of(x.device))
+				 ptr(work), wb, stream_of(x.device))
 		return sigma
 
 	@staticmethod
-	def color_forward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site):
+	def color_forward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site, records=True):
+		"""records: as for density_forward."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
 						 (quat, 'quat', torch.float32), (sh, 'sh', torch.float32), (x, 'x', torch.float32),
@@ -81,10 +84,11 @@ class _FieldExtension:
 		rgb = torch.empty(m, 3, dtype=torch.float32, device=x.device)
 		if m == 0:
 			return rgb
+		work, wb = _field_work(points, m, records)
 		with torch.cuda.device(x.device):
 			call('vgr_color_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(log_scale), ptr(quat), ptr(sh), int(sh_deg), ptr(x), ptr(dirs), ptr(site), m, ptr(rgb),
-				 stream_of(x.device))
+				 ptr(work), wb, stream_of(x.device))
 		return rgb
 
 	@staticmethod
@@ -98,6 +102,16 @@ class _FieldExtension:
 		with torch.cuda.device(quat.device):
 			call('vgr_conic_forward', ptr(log_scale), ptr(quat), n, float(floor), ptr(A), stream_of(quat.device))
 		return A
+
+
+def _field_work(points, m, records):
+	"""Scratch for the per-site Gaussian records of density_forward / color_forward when the call is large enough
+	for the library to use them (m >= N / 8), else (None, 0)."""
+	n = points.numel() // 3
+	if not records or m * 8 < n:
+		return None, 0
+	wb = int(_lib.load().vgr_field_work_size(n))
+	return torch.empty(wb, dtype=torch.uint8, device=points.device), wb
 
 
 # ============================================================================ march.cu forward
