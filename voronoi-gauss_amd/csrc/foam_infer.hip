@@ -156,12 +156,13 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
 // Tuning per colour mode, measured on config 3. Fused and baked colours: 30 slots (6.0 KB of LDS per wave), so that
 // 24 waves (6 per SIMD) fit in a CU's 160 KB, and no software pipelining: the registers that pipelined loads hold
 // are worth more as a sixth wave, whose loads cover the latency instead (48 slots at 4 waves, 36 at 5 and 26 at 7
-// were all slower: 233, 216 and 257 ms against 207). Lazy colours keep 48 slots, 4 waves and the pipelined loops
-// (edge records two edges ahead, site records one ahead): 287 ms against 305 with the fused tuning.
+// were all slower: 233, 216 and 257 ms against 207). Lazy colours take 36 slots, 5 waves and the pipelined loops
+// (edge records two edges ahead, site records one ahead): 276 ms, against 287 at 4 waves and 48 slots, 305 with
+// the fused tuning and 330 at 5 waves without pipelining.
 template <int COLOR>
 struct Tune {
-    static constexpr int slots = COLOR == kLazy ? 48 : 30;
-    static constexpr int waves = COLOR == kLazy ? 4 : 6;
+    static constexpr int slots = COLOR == kLazy ? 36 : 30;
+    static constexpr int waves = COLOR == kLazy ? 5 : 6;
     static constexpr bool pipelined = COLOR == kLazy;
 };
 
