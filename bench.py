@@ -1,5 +1,5 @@
-"""Benchmark of the north-star path: foam_infer (ray / Voronoi-face renderer) on BASELINE config 3 -- the 2M-site
-surface-dominated scene seen by 4 cameras at 1920x1080 -- on one MI355X.
+"""Benchmark of the inference path: foam_infer (ray / Voronoi-face renderer) on benchmark configuration 3 -- the
+2M-site surface-dominated scene seen by 4 cameras at 1920x1080 -- on one MI355X.
 
 One step = one foam_infer launch rendering all 4 frames (8,294,400 rays) with the scene packed and the rays
 resident in HBM. Prints one JSON line: Mrays/s (value), ms per step, FPS at 1080p, the roofline of the kernel
@@ -105,7 +105,7 @@ def main():
 	ap.add_argument('--steps', type=int, default=None, help='timed steps (default 20; march: 3)')
 	ap.add_argument('--warmup', type=int, default=None, help='untimed steps (default 3; march: 1)')
 	ap.add_argument('--config', type=int, default=3)
-	ap.add_argument('--scale', type=float, default=1.0, help='site-count scale (1 = the BASELINE config)')
+	ap.add_argument('--scale', type=float, default=1.0, help='site-count scale (1 = the full configuration)')
 	ap.add_argument('--colors', default='fused', choices=['exact', 'fused', 'baked'],
 				help='exact colour modes (eps_color = 0): lazy second pass or fused online blend; baked: per-view '
 					 'site colours, baked per camera inside the timed step (approximate)')

@@ -242,7 +242,7 @@ def load_geometry(config, n_sites=None, cache_dir=DEFAULT_CACHE, log=print):
 
 
 def make_scene(config, scale=1.0, img_scale=1.0, n_rays=None, cache_dir=DEFAULT_CACHE, log=print):
-	"""Seeded synthetic scene of BASELINE config `config` (1..5) with round(scale * N) sites."""
+	"""Seeded synthetic scene of benchmark configuration `config` (1..5) with round(scale * N) sites."""
 	n = max(64, int(round(SITE_COUNTS[config] * scale)))
 	pts, offsets, adj, cls = load_geometry(config, n, cache_dir, log)
 	N = len(pts)
