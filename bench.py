@@ -12,6 +12,8 @@ Other rows of the path, each as one JSON line of the same form (not the headline
   --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
   --workload locate   start-cell location on config 5 (nearest site of 16,777,216 ray origins among 4M sites)
   --workload pack     pack_foam with Z-order renumbering on config 3 (the step before the kernel)
+  --workload traverse the cell traversal alone (foam_infer stage 0) on config 3 in both layouts: one ray per lane
+                      (foam_infer) against 16 lanes per ray testing a cell's faces in parallel
   --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
                       one 1920x1080 frame at 64 stratified samples per ray (render_rays' first round)
 """
@@ -116,7 +118,7 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
-	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack'],
+	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack', 'traverse'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
 	args = ap.parse_args()
@@ -137,6 +139,8 @@ def main():
 		return bench_field(args)
 	if args.workload == 'pack':
 		return bench_pack(args)
+	if args.workload == 'traverse':
+		return bench_traverse(args)
 	bench_foam(args)
 
 
@@ -459,6 +463,70 @@ def bench_march(args):
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
 		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)
+
+
+def bench_traverse(args):
+	"""The traversal alone (walk to the start cell, then exit faces cell to cell: foam_infer with stage 0) of the
+	config-3 workload in the two wave64 layouts: one ray per lane over 8x8 tiles (vgr_foam_infer) and a group of
+	16 lanes per ray, each testing every 16th face, with a group min-reduction (vgr_foam_traverse_faces). Both
+	must give the same per-ray statistics; the JSON line is the lane-per-face layout, the other beside it."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	sc = scenes.make_scene(args.config, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	pack = render.pack_foam(model, reorder=True)
+	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile)
+	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
+	start = pack['inv'][torch.from_numpy(start_np).to(dev).long()].int()
+	near, _, far = render.ray_bounds(o, d, 0.02, sc.far_radius)
+	B = len(o)
+	empty = torch.empty(0, dtype=torch.int32, device=dev)
+	fi = ext.foam_infer_extension()
+	stream = torch.cuda.current_stream(dev)
+	lane_ms, out_lane, _ = time_steps(
+		lambda: fi.foam_infer(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'],
+							  sc.sh_deg, o, d, start, near, far, 1e-4, 1e-4, math.inf, 0, 0, empty, pack['orig']),
+		args.steps, args.warmup, stream)
+	face_ms, stats_face, _ = time_steps(
+		lambda: ext.traverse_faces(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], o, d, start, near, far,
+								   orig=pack['orig']), args.steps, args.warmup, stream)
+	ms_lane, ms_face = float(np.mean(lane_ms)), float(np.mean(face_ms))
+	same = bool(torch.equal(out_lane[3], stats_face))
+	st = stats_face.double()
+	log(f'stage-0 traversal of {B} rays: one ray per lane {ms_lane:.3f} ms, 16 lanes per ray {ms_face:.3f} ms; '
+		f'per-ray statistics identical: {same}; {st[:, 0].mean():.1f} cells per ray')
+	cpu = None
+	if args.cpu_seconds > 0:  # the oracle's traversal (stage 0) on every k-th ray: rate and stats parity
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		pk = {k: pack[k].cpu().numpy() for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh', 'orig')}
+		args_np = (pk, sc.sh_deg, o_np, d_np, start.cpu().numpy(), near.cpu().numpy(), far.cpu().numpy())
+		probe = np.arange(0, B, max(1, B // 20000), dtype=np.int64)
+		r = oracle.foam_infer(*args_np, stage=0, rays=probe)
+		k = max(1, int(B / (len(probe) / max(r['seconds'], 1e-6) * args.cpu_seconds)))
+		sel = np.arange(0, B, k, dtype=np.int64)
+		r = oracle.foam_infer(*args_np, stage=0, rays=sel)
+		cpu_same = bool(np.array_equal(r['stats'], stats_face.cpu().numpy()[sel]))
+		log(f'cpu oracle traversal: {len(sel)} rays in {r["seconds"]:.2f} s; stats identical to the GPU: {cpu_same}')
+		cpu = {'value': round(len(sel) / r['seconds'] / 1e6, 4), 'unit': 'Mrays/s', 'cores': oracle.max_threads(),
+			   'kind': 'port', 'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), stage 0, '
+										 f'C/OpenMP thread per ray', 'identical_stats': cpu_same}
+	E = 1.0 + len(sc.adj) / sc.n_sites
+	# per visited cell: the cell position (16 B) and offsets (8 B), then per face the edge record (16 B) and nbr (4 B)
+	abytes = float(56 * B + st[:, 0].sum() * (24 + 20 * E))
+	achieved = abytes / (ms_face * 1e-3) / 1e9
+	emit(f'Mrays/s cell traversal, 16 lanes per ray (config {args.config}: {sc.n_sites} sites, 4 x 1080p)',
+		 B / ms_face / 1e3, 'Mrays/s', args, ms_face,
+		 {'workload': f'config {args.config}: foam_infer stage 0 (walk + exit faces) over {B} camera rays',
+		  'layout': '16 lanes per ray, group min-reduction of the exit face',
+		  'thread_per_ray_ms': round(ms_lane, 4), 'lane_per_face_ms': round(ms_face, 4),
+		  'identical_stats': same, 'cells_per_ray': round(float(st[:, 0].mean()), 2)},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
 
 
 def bench_pack(args):

@@ -72,6 +72,18 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
                           float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream);
 
 /*
+ * Cell traversal alone (foam_infer with stage 0: walk to the start cell, then exit faces up to far or cap) with a
+ * group of 16 lanes per ray, each testing every 16th face, and a group min-reduction of the exit parameter. No
+ * counterpart in the reference: it is the lane-per-face layout against which vgr_foam_infer's thread-per-ray layout
+ * is compared (same outputs bit for bit). stats i32 (B, 5) as vgr_foam_infer's (sample and walk-step counts, the
+ * rest 0); trace (optional, NULL = none) i32 (B, trace_cap): the cell of every sample in original numbering.
+ */
+int vgr_foam_traverse_faces(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                            const float* edge, int64_t n_edges, const float* o, const float* d, const int32_t* start,
+                            const float* near_t, const float* far_t, int64_t n_rays, const int32_t* cap,
+                            const int32_t* orig, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream);
+
+/*
  * Fused uniform-step march (forward). Replaces march_forward() of csrc/march.cu:383-403 (export :432),
  * bound by ext.march (ext.py:172-182) and called from render_rays_uniform (render.py:118-119).
  *   points f32 (N, 3), offsets i32 (N + 1), adj i32 (M) Delaunay CSR; raw f32 (N); dA, cA f32 (N, 6) conics;

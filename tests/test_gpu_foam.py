@@ -157,6 +157,35 @@ def test_random_ray_batch_config5(gpu):
 	compare(g0, r0)
 
 
+@pytest.mark.parametrize('config,scale', [(1, 1.0), (3, 0.01)])
+def test_lane_per_face_traversal_matches(gpu, config, scale):
+	"""The lane-per-face traversal (16 lanes per ray, group min-reductions) visits the same cells with the same
+	sample and walk-step counts as foam_infer's thread-per-ray stage 0, bit for bit, and as the oracle."""
+	sc = scenes.make_scene(config, scale=scale, img_scale=0.1, cache_dir=None, log=None)
+	_, pk = scene_pack(sc, reorder=True)
+	o, d, start, _ = sc.camera_rays(tile=8)
+	st = pk['inv'][start].astype(np.int32)
+	near, _, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
+	g = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=512)
+	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=gpu)  # noqa: E731
+	stats, trace = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d),
+									  t(st), t(near), t(far), orig=t(pk['orig']), trace_cap=512)
+	np.testing.assert_array_equal(stats.cpu().numpy(), g['stats'])
+	np.testing.assert_array_equal(trace.cpu().numpy(), g['trace'])
+	r = ref_foam(pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=512)
+	np.testing.assert_array_equal(trace.cpu().numpy(), r['trace'])
+	# a sample cap, and a start outside the scene
+	cap = np.full(len(o), 5, np.int32)
+	s5 = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d), t(st),
+							t(near), t(far), cap=t(cap), orig=t(pk['orig']))
+	assert (s5.cpu().numpy()[:, 0] <= 5).all()
+	bad = st.copy()
+	bad[:3] = -1
+	sb = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d), t(bad),
+							t(near), t(far), orig=t(pk['orig'])).cpu().numpy()
+	assert (sb[:3] == 0).all() and (sb[3:, 0] == g['stats'][3:, 0]).all()
+
+
 def test_render_rays_foam_infer_api(gpu, small):
 	"""render.render_rays_foam_infer end to end (bounds, Morton start remap, background) vs the oracle."""
 	f, (o, d, start, near, _, far) = small

@@ -1,0 +1,162 @@
+// Cell traversal with one group of lanes per ray (lane-per-face layout), gfx950: the layout comparison for the
+// inference renderer's traversal.
+//
+// foam_infer.hip runs one ray per lane. The other layout for wave64 tests a cell's faces in parallel: here a
+// group of 16 lanes serves one ray (four rays per wave), each lane takes every 16th edge of the cell's
+// neighbourhood, and the exit face is a group min-reduction of (t, tie order). The greedy walk to the start cell
+// is a group argmin of (distance, tie order) in the same way. This kernel covers the traversal alone (stage 0 of
+// foam_infer: walk, then exit faces from cell to cell up to far or `cap` samples; with no density T stays 1, so
+// t_thresh <= 1 never stops a ray): the same visited cells, the same sample counts and walk steps, bit for bit,
+// since a lexicographic minimum does not depend on the order in which it is reduced. Semantics:
+// csrc/foam_infer.cu:176-194 (walk_to) and :199-257 (eval_cell, exit faces) of the reference.
+#include "vgr_abi.h"
+#include "vgr_device.h"
+
+namespace vgr {
+namespace {
+
+constexpr int kGroup = 16;  // lanes per ray
+constexpr int kFacesBlock = 64;
+constexpr int kRaysPerBlock = kFacesBlock / kGroup;
+
+struct FacesScene {
+    const float4* __restrict__ points;  // (N) p, w unused
+    const int* __restrict__ offsets;    // (N + 1) self-first
+    const int* __restrict__ nbr;        // (E)
+    const float4* __restrict__ edge;    // (E) p_j, cut-off word
+    const int* __restrict__ orig;       // (N) or null
+    int n_sites;
+};
+
+// k precedes j in the tie order: the smaller original index (INT_MAX: no site, after every site).
+__device__ __forceinline__ bool before_site(const FacesScene& S, int k, int j) {
+    if (j == INT_MAX) return k != INT_MAX;
+    if (k == INT_MAX) return false;
+    return S.orig != nullptr ? S.orig[k] < S.orig[j] : k < j;
+}
+
+// (t, k) precedes (u, j) lexicographically.
+__device__ __forceinline__ bool precedes(const FacesScene& S, float t, int k, float u, int j) {
+    return t < u || (t == u && before_site(S, k, j));
+}
+
+// Group-wide lexicographic minimum of (t, k): every lane of the 16-lane group ends with it.
+__device__ __forceinline__ void group_min(const FacesScene& S, float& t, int& k) {
+#pragma unroll
+    for (int m = kGroup / 2; m >= 1; m >>= 1) {
+        const float u = __shfl_xor(t, m, kGroup);
+        const int j = __shfl_xor(k, m, kGroup);
+        if (precedes(S, u, j, t, k)) t = u, k = j;
+    }
+}
+
+template <bool TRACE>
+__global__ void __launch_bounds__(kFacesBlock)
+    foam_faces_kernel(FacesScene S, const float* __restrict__ o_, const float* __restrict__ d_,
+                      const int* __restrict__ start_, const float* __restrict__ near_, const float* __restrict__ far_,
+                      const int* __restrict__ cap, int64_t n_rays, int* __restrict__ stats, int* __restrict__ trace,
+                      int64_t trace_cap) {
+    const int g = static_cast<int>(threadIdx.x) % kGroup;
+    const int64_t r = xcd_block_id() * kRaysPerBlock + threadIdx.x / kGroup;
+    if (r >= n_rays) return;  // whole groups leave together: every shuffle stays within a live group
+    int* st = stats + 5 * r;
+    int cur = start_[r];
+    if (cur < 0 || cur >= S.n_sites) {  // not traced
+        if (g == 0) st[0] = st[1] = st[2] = st[3] = st[4] = 0;
+        return;
+    }
+    const float o[3] = {o_[3 * r], o_[3 * r + 1], o_[3 * r + 2]};
+    const float d[3] = {d_[3 * r], d_[3 * r + 1], d_[3 * r + 2]};
+    const float t_near = near_[r], t_far = far_[r];
+    const int max_samples = cap != nullptr ? cap[r] : INT_MAX;
+
+    // greedy walk to the cell of x(near): the group argmin over {c} U adj(c), repeated until c wins
+    int walk_steps = 0;
+    {
+        const float x0 = o[0] + t_near * d[0], x1 = o[1] + t_near * d[1], x2 = o[2] + t_near * d[2];
+        for (int it = 0; it < kWalkCap; ++it) {
+            const float4 pc = S.points[cur];
+            float bd = (x0 - pc.x) * (x0 - pc.x) + (x1 - pc.y) * (x1 - pc.y) + (x2 - pc.z) * (x2 - pc.z);
+            int bk = cur;
+            const int e0 = S.offsets[cur], e1 = S.offsets[cur + 1];
+            for (int e = e0 + 1 + g; e < e1; e += kGroup) {
+                const float4 ed = S.edge[e];
+                const int k = S.nbr[e];
+                const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
+                const float dk = v0 * v0 + v1 * v1 + v2 * v2;
+                if (precedes(S, dk, k, bd, bk)) bd = dk, bk = k;
+            }
+            group_min(S, bd, bk);
+            if (bk == cur) break;
+            cur = bk;
+            ++walk_steps;
+        }
+    }
+
+    // the exit face of the cell at the current sample: group minimum of the bisector-plane parameters ahead
+    auto exit_face = [&](int c, float& t_exit, int& next) {
+        const float4 pc = S.points[c];
+        t_exit = kInf, next = INT_MAX;
+        const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+        for (int e = e0 + 1 + g; e < e1; e += kGroup) {
+            const float4 ed = S.edge[e];
+            const int k = S.nbr[e];
+            const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
+            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+            if (dn > 0.f) {
+                const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
+                            m2 = 0.5f * (ed.z + pc.z) - o[2];
+                const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
+                if (precedes(S, tt, k, t_exit, next)) t_exit = tt, next = k;
+            }
+        }
+        group_min(S, t_exit, next);
+    };
+
+    if (TRACE && g == 0 && trace_cap > 0) trace[r * trace_cap] = S.orig != nullptr ? S.orig[cur] : cur;
+    float t_exit;
+    int next;
+    exit_face(cur, t_exit, next);
+    float tP = t_near;
+    int n_samples = 1;
+    for (int it = 0; it < kMaxCells; ++it) {
+        const bool last = next == INT_MAX || t_exit >= t_far || n_samples + 1 >= max_samples;
+        const float tQ = last ? t_far : fmaxf(t_exit, tP);
+        if (!last) cur = next;
+        if (TRACE && g == 0 && n_samples < trace_cap)
+            trace[r * trace_cap + n_samples] = S.orig != nullptr ? S.orig[cur] : cur;
+        ++n_samples;
+        if (last) break;
+        exit_face(cur, t_exit, next);
+        tP = tQ;
+    }
+    if (g == 0) st[0] = n_samples, st[1] = 0, st[2] = walk_steps, st[3] = 0, st[4] = 0;
+}
+
+}  // namespace
+}  // namespace vgr
+
+extern "C" int vgr_foam_traverse_faces(const float* points, int64_t n_sites, const int32_t* offsets,
+                                       const int32_t* nbr, const float* edge, int64_t n_edges, const float* o,
+                                       const float* d, const int32_t* start, const float* near_t, const float* far_t,
+                                       int64_t n_rays, const int32_t* cap, const int32_t* orig, int32_t* stats,
+                                       int32_t* trace, int64_t trace_cap, void* stream) {
+    using namespace vgr;
+    VGR_REQUIRE(n_rays >= 0, "foam_traverse_faces: n_rays must be >= 0");
+    VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_traverse_faces: trace needs trace_cap > 0");
+    if (n_rays == 0) return VGR_OK;
+    VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_traverse_faces: n_sites must be in [1, 2^31)");
+    VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_traverse_faces: n_edges must be in [N, 2^31)");
+    VGR_REQUIRE(points && offsets && nbr && edge, "foam_traverse_faces: null scene pointer");
+    VGR_REQUIRE(o && d && start && near_t && far_t && stats, "foam_traverse_faces: null ray pointer");
+    const FacesScene S{reinterpret_cast<const float4*>(points), offsets, nbr, reinterpret_cast<const float4*>(edge),
+                       orig, int(n_sites)};
+    const dim3 grid(grid_for(n_rays, kRaysPerBlock)), block(kFacesBlock);
+    if (trace != nullptr)
+        hipLaunchKernelGGL(foam_faces_kernel<true>, grid, block, 0, as_stream(stream), S, o, d, start, near_t, far_t,
+                           cap, n_rays, stats, trace, trace_cap);
+    else
+        hipLaunchKernelGGL(foam_faces_kernel<false>, grid, block, 0, as_stream(stream), S, o, d, start, near_t, far_t,
+                           cap, n_rays, stats, trace, int64_t{0});
+    return launch_status("foam_faces_kernel");
+}

@@ -201,6 +201,29 @@ class _FoamInferExtension:
 		return out
 
 
+def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0):
+	"""Cell traversal alone with a group of 16 lanes per ray (vgr_foam_traverse_faces, the lane-per-face layout):
+	the outputs foam_infer gives with stage 0 -> stats (B, 5) int32 [samples, 0, walk steps, 0, 0] (+ trace
+	(B, trace_cap), the cell of every sample in original numbering, -1 past the last, when trace_cap > 0)."""
+	for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32), (nbr, 'nbr', torch.int32),
+					 (edge, 'edge', torch.float32), (o, 'o', torch.float32), (d, 'd', torch.float32),
+					 (start, 'start', torch.int32), (near, 'near', torch.float32), (far, 'far', torch.float32)):
+		_check(t, n, dt)
+	n = points.size(0)
+	B = o.size(0)
+	dev = o.device
+	stats = torch.empty(B, 5, dtype=torch.int32, device=dev)
+	trace = torch.full((B, trace_cap), -1, dtype=torch.int32, device=dev) if trace_cap > 0 else None
+	if B > 0:
+		cp = cap if cap is not None and cap.numel() == B else None
+		og = orig if orig is not None and orig.numel() == n else None
+		with torch.cuda.device(dev):
+			call('vgr_foam_traverse_faces', ptr(points), n, ptr(offsets), ptr(nbr), ptr(edge), nbr.numel(), ptr(o),
+				 ptr(d), ptr(start), ptr(near), ptr(far), B, ptr(cp), ptr(og), ptr(stats), ptr(trace), int(trace_cap),
+				 stream_of(dev))
+	return (stats, trace) if trace is not None else stats
+
+
 _FIELD, _MARCH, _FOAM_INFER = _FieldExtension(), _MarchExtension(), _FoamInferExtension()
 
 
