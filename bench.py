@@ -118,6 +118,11 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
+	ap.add_argument('--lanes-per-ray', type=int, default=None, choices=[1, 2, 4, 8],
+					help='foam workload: ray layout (1: one ray per lane, 2 / 4 / 8: lanes per ray; default: the '
+						 'library default)')
+	ap.add_argument('--lanes', type=int, default=8, choices=[4, 8, 16],
+					help='traverse workload: lanes per ray of the layout the JSON line reports')
 	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack', 'traverse'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
@@ -174,7 +179,8 @@ def bench_foam(args):
 
 	def launch(p, sel, m=mode, cut=color_cut):
 		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
-							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'])
+							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'],
+							 lanes=args.lanes_per_ray)
 
 	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
 		per = B // frames
@@ -491,14 +497,19 @@ def bench_traverse(args):
 		lambda: fi.foam_infer(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'],
 							  sc.sh_deg, o, d, start, near, far, 1e-4, 1e-4, math.inf, 0, 0, empty, pack['orig']),
 		args.steps, args.warmup, stream)
-	face_ms, stats_face, _ = time_steps(
-		lambda: ext.traverse_faces(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], o, d, start, near, far,
-								   orig=pack['orig']), args.steps, args.warmup, stream)
-	ms_lane, ms_face = float(np.mean(lane_ms)), float(np.mean(face_ms))
-	same = bool(torch.equal(out_lane[3], stats_face))
+	ms_lane = float(np.mean(lane_ms))
+	group_ms, same = {}, True
+	for lanes in (4, 8, 16):
+		face_ms, stats_face, _ = time_steps(
+			lambda: ext.traverse_faces(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], o, d, start, near,
+									   far, orig=pack['orig'], lanes=lanes), args.steps, args.warmup, stream)
+		group_ms[lanes] = float(np.mean(face_ms))
+		same = same and bool(torch.equal(out_lane[3], stats_face))
+	ms_face = group_ms[args.lanes]
 	st = stats_face.double()
-	log(f'stage-0 traversal of {B} rays: one ray per lane {ms_lane:.3f} ms, 16 lanes per ray {ms_face:.3f} ms; '
-		f'per-ray statistics identical: {same}; {st[:, 0].mean():.1f} cells per ray')
+	log(f'stage-0 traversal of {B} rays: one ray per lane {ms_lane:.3f} ms; ' +
+		', '.join(f'{g} lanes per ray {ms:.3f} ms' for g, ms in group_ms.items()) +
+		f'; per-ray statistics identical: {same}; {st[:, 0].mean():.1f} cells per ray')
 	cpu = None
 	if args.cpu_seconds > 0:  # the oracle's traversal (stage 0) on every k-th ray: rate and stats parity
 		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
@@ -515,15 +526,18 @@ def bench_traverse(args):
 		cpu = {'value': round(len(sel) / r['seconds'] / 1e6, 4), 'unit': 'Mrays/s', 'cores': oracle.max_threads(),
 			   'kind': 'port', 'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), stage 0, '
 										 f'C/OpenMP thread per ray', 'identical_stats': cpu_same}
+	if args.copy_probe:
+		copy_probe(dev)
 	E = 1.0 + len(sc.adj) / sc.n_sites
 	# per visited cell: the cell position (16 B) and offsets (8 B), then per face the edge record (16 B) and nbr (4 B)
 	abytes = float(56 * B + st[:, 0].sum() * (24 + 20 * E))
 	achieved = abytes / (ms_face * 1e-3) / 1e9
-	emit(f'Mrays/s cell traversal, 16 lanes per ray (config {args.config}: {sc.n_sites} sites, 4 x 1080p)',
+	emit(f'Mrays/s cell traversal, {args.lanes} lanes per ray (config {args.config}: {sc.n_sites} sites, 4 x 1080p)',
 		 B / ms_face / 1e3, 'Mrays/s', args, ms_face,
 		 {'workload': f'config {args.config}: foam_infer stage 0 (walk + exit faces) over {B} camera rays',
-		  'layout': '16 lanes per ray, group min-reduction of the exit face',
-		  'thread_per_ray_ms': round(ms_lane, 4), 'lane_per_face_ms': round(ms_face, 4),
+		  'layout': f'{args.lanes} lanes per ray, DPP group min-reduction of the exit face',
+		  'thread_per_ray_ms': round(ms_lane, 4),
+		  'lane_per_face_ms': {str(g): round(ms, 4) for g, ms in group_ms.items()},
 		  'identical_stats': same, 'cells_per_ray': round(float(st[:, 0].mean()), 2)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)

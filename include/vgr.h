@@ -72,16 +72,35 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
                           float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream);
 
 /*
+ * vgr_foam_infer_traced with the ray layout chosen by the caller: lanes_per_ray 1 runs one ray per lane, 2, 4 or 8
+ * a group of that many lanes per ray (each lane takes every lanes_per_ray-th edge of a cell's neighbourhood; the
+ * group combines exit faces by a lexicographic minimum, so the visited cells are the same, and density and colour
+ * terms by sums, so only their summation order differs), 0 the library's default (the layout vgr_foam_infer
+ * runs: 4 lanes per ray for stages 0 and 1 and lazy colours, one ray per lane for fused and baked colours). Fused and baked colours with a finite color_cut always run one ray per lane (their neighbour skipping
+ * follows the edge order). trace may be NULL (then trace_cap is ignored). No counterpart in the reference: the layout comparison
+ * for vgr_foam_infer, whose arguments and outputs it otherwise shares.
+ */
+int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                         const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
+                         int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                         const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
+                         int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
+                         float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                         int64_t lanes_per_ray, void* stream);
+
+/*
  * Cell traversal alone (foam_infer with stage 0: walk to the start cell, then exit faces up to far or cap) with a
- * group of 16 lanes per ray, each testing every 16th face, and a group min-reduction of the exit parameter. No
- * counterpart in the reference: it is the lane-per-face layout against which vgr_foam_infer's thread-per-ray layout
- * is compared (same outputs bit for bit). stats i32 (B, 5) as vgr_foam_infer's (sample and walk-step counts, the
- * rest 0); trace (optional, NULL = none) i32 (B, trace_cap): the cell of every sample in original numbering.
+ * group of lanes_per_ray lanes (4, 8 or 16; 0 = 8) per ray, each testing every lanes_per_ray-th face, and a group
+ * min-reduction of the exit parameter. No counterpart in the reference: it is the lane-per-face layout against
+ * which vgr_foam_infer's thread-per-ray layout is compared (same outputs bit for bit). stats i32 (B, 5) as
+ * vgr_foam_infer's (sample and walk-step counts, the rest 0); trace (optional, NULL = none) i32 (B, trace_cap):
+ * the cell of every sample in original numbering.
  */
 int vgr_foam_traverse_faces(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                             const float* edge, int64_t n_edges, const float* o, const float* d, const int32_t* start,
                             const float* near_t, const float* far_t, int64_t n_rays, const int32_t* cap,
-                            const int32_t* orig, int32_t* stats, int32_t* trace, int64_t trace_cap, void* stream);
+                            const int32_t* orig, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                            int64_t lanes_per_ray, void* stream);
 
 /*
  * Fused uniform-step march (forward). Replaces march_forward() of csrc/march.cu:383-403 (export :432),

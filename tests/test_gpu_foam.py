@@ -25,7 +25,7 @@ def ref_foam(*args, **kw):
 
 
 def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, color_cut=math.inf,
-			 color_mode=0, stage=2, cap=None, trace_cap=0):
+			 color_mode=0, stage=2, cap=None, trace_cap=0, lanes=None):
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)  # noqa: E731
 	empty = torch.empty(0, dtype=torch.int32, device=dev)
 	orig = pk.get('orig')
@@ -33,7 +33,7 @@ def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e
 		t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(pk['attr']), t(pk['sh']), sh_deg, t(o),
 		t(d), t(start), t(near), t(far), t_thresh, w_thresh, color_cut, color_mode, stage,
 		empty if cap is None else t(cap.astype(np.int32)), t(orig) if orig is not None and len(orig) else empty,
-		trace_cap=trace_cap)
+		trace_cap=trace_cap, lanes=lanes)
 	torch.cuda.synchronize()
 	res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
 	res.setdefault('trace', None)
@@ -157,10 +157,75 @@ def test_random_ray_batch_config5(gpu):
 	compare(g0, r0)
 
 
+@pytest.mark.parametrize('lanes', [1, 2, 4, 8])
+def test_layouts_small_field(gpu, small, lanes):
+	"""Every ray layout of vgr_foam_infer_lanes (one ray per lane, a group of 2, 4 or 8 lanes per ray), whichever
+	the default is: every stage and colour mode against the oracle; thresholds off, every statistic equal and the
+	cell sequences bit-exact."""
+	f, (o, d, start, near, _, far) = small
+	pk = f.pack()
+	for stage in (0, 1, 2):
+		g = gpu_foam(gpu, pk, 3, o, d, start, near, far, 0.0, -1.0, stage=stage, trace_cap=512, lanes=lanes)
+		r = ref_foam(pk, 3, o, d, start, near, far, 0.0, -1.0, stage=stage, trace_cap=512)
+		compare(g, r)
+	for color_mode in (0, 2):
+		for sh_half in (False, True):
+			pk = f.pack(sh_half=sh_half, reorder=True)
+			st = pk['inv'][start].astype(np.int32)
+			g = gpu_foam(gpu, pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512, lanes=lanes)
+			r = ref_foam(pk, 3, o, d, st, near, far, color_mode=color_mode, trace_cap=512)
+			compare(g, r, exact_trace=False, stats_frac=0.98)
+	pk = f.pack(eps_density=1e-3)
+	center = np.array([0.1, 0.2, 2.5], np.float32)
+	dirs = f.points - center
+	dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+	b = render.sh_basis(torch.from_numpy(dirs.astype(np.float32)), 3).numpy()
+	pk['attr'][:, 16:19] = np.maximum((b[:, :, None] * f.sh).sum(1) + 0.5, 0)
+	cut = 2 * math.log(1 / 1e-3)
+	for mode in (1, 2, 0):
+		g = gpu_foam(gpu, pk, 3, o, d, start, near, far, color_cut=cut, color_mode=mode, trace_cap=512, lanes=lanes)
+		r = ref_foam(pk, 3, o, d, start, near, far, color_cut=cut, color_mode=mode, trace_cap=512)
+		compare(g, r, exact_trace=False, stats_frac=0.98)
+	cap = np.maximum(2, r['stats'][:, 0] // 2).astype(np.int32)
+	g = gpu_foam(gpu, pk, 3, o, d, start, near, far, stage=0, cap=cap, trace_cap=512, lanes=lanes)
+	np.testing.assert_array_equal(g['stats'][:, 0], cap)
+	bad = start.copy()
+	bad[:4] = -1
+	g = gpu_foam(gpu, pk, 3, o, d, bad, near, far, lanes=lanes)
+	assert (g['T'][:4] == 1).all() and (g['rgb'][:4] == 0).all() and (g['stats'][:4] == 0).all()
+
+
+@pytest.mark.parametrize('lanes', [1, 2, 4, 8])
+@pytest.mark.parametrize('config,scale,img', [(1, 1.0, 1.0), (3, 0.02, 0.08), (5, 0.005, 0.0)])
+def test_layouts_scenes(gpu, lanes, config, scale, img):
+	"""Every ray layout on benchmark scenes (exact colours and fused colours) against the oracle, and against the
+	one-ray-per-lane layout: the same cells (stage 0 statistics bit-equal)."""
+	if config == 5:
+		sc = scenes.make_scene(5, scale=scale, n_rays=4096, cache_dir=None, log=None)
+	else:
+		sc = scenes.make_scene(config, scale=scale, img_scale=img, cache_dir=None, log=None)
+	model, pk = scene_pack(sc, reorder=config != 5)
+	o, d, start, _ = sc.camera_rays(tile=8) if config != 5 else sc.camera_rays()
+	near, _, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
+	st = pk['inv'][start].astype(np.int32) if pk['inv'] is not None else start
+	if len(o) > 60000:
+		sel = np.arange(0, len(o), len(o) // 60000 + 1)
+		o, d, st, near, far = o[sel], d[sel], st[sel], near[sel], far[sel]
+	for mode in (0, 2):
+		g = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, color_mode=mode, trace_cap=256, lanes=lanes)
+		r = ref_foam(pk, sc.sh_deg, o, d, st, near, far, color_mode=mode, trace_cap=256)
+		compare(g, r, exact_trace=False, stats_frac=0.99)
+		assert psnr(g['rgb'], r['rgb']) >= 60.0
+	g0 = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=256, lanes=lanes)
+	l0 = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=256, lanes=1)
+	np.testing.assert_array_equal(g0['stats'], l0['stats'])
+	np.testing.assert_array_equal(g0['trace'], l0['trace'])
+
+
 @pytest.mark.parametrize('config,scale', [(1, 1.0), (3, 0.01)])
 def test_lane_per_face_traversal_matches(gpu, config, scale):
-	"""The lane-per-face traversal (16 lanes per ray, group min-reductions) visits the same cells with the same
-	sample and walk-step counts as foam_infer's thread-per-ray stage 0, bit for bit, and as the oracle."""
+	"""The lane-per-face traversal (4, 8 or 16 lanes per ray, group min-reductions) visits the same cells with the
+	same sample and walk-step counts as foam_infer's thread-per-ray stage 0, bit for bit, and as the oracle."""
 	sc = scenes.make_scene(config, scale=scale, img_scale=0.1, cache_dir=None, log=None)
 	_, pk = scene_pack(sc, reorder=True)
 	o, d, start, _ = sc.camera_rays(tile=8)
@@ -168,12 +233,17 @@ def test_lane_per_face_traversal_matches(gpu, config, scale):
 	near, _, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
 	g = gpu_foam(gpu, pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=512)
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=gpu)  # noqa: E731
-	stats, trace = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d),
-									  t(st), t(near), t(far), orig=t(pk['orig']), trace_cap=512)
-	np.testing.assert_array_equal(stats.cpu().numpy(), g['stats'])
-	np.testing.assert_array_equal(trace.cpu().numpy(), g['trace'])
 	r = ref_foam(pk, sc.sh_deg, o, d, st, near, far, stage=0, trace_cap=512)
-	np.testing.assert_array_equal(trace.cpu().numpy(), r['trace'])
+	for lanes in (4, 8, 16):
+		stats, trace = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o),
+										  t(d), t(st), t(near), t(far), orig=t(pk['orig']), trace_cap=512,
+										  lanes=lanes)
+		np.testing.assert_array_equal(stats.cpu().numpy(), g['stats'])
+		np.testing.assert_array_equal(trace.cpu().numpy(), g['trace'])
+		np.testing.assert_array_equal(trace.cpu().numpy(), r['trace'])
+	with pytest.raises(RuntimeError, match='lanes_per_ray'):
+		ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d), t(st),
+						   t(near), t(far), lanes=5)
 	# a sample cap, and a start outside the scene
 	cap = np.full(len(o), 5, np.int32)
 	s5 = ext.traverse_faces(t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(o), t(d), t(st),

@@ -1,23 +1,28 @@
 // Cell traversal with one group of lanes per ray (lane-per-face layout), gfx950: the layout comparison for the
 // inference renderer's traversal.
 //
-// foam_infer.hip runs one ray per lane. The other layout for wave64 tests a cell's faces in parallel: here a
-// group of 16 lanes serves one ray (four rays per wave), each lane takes every 16th edge of the cell's
-// neighbourhood, and the exit face is a group min-reduction of (t, tie order). The greedy walk to the start cell
-// is a group argmin of (distance, tie order) in the same way. This kernel covers the traversal alone (stage 0 of
-// foam_infer: walk, then exit faces from cell to cell up to far or `cap` samples; with no density T stays 1, so
-// t_thresh <= 1 never stops a ray): the same visited cells, the same sample counts and walk steps, bit for bit,
-// since a lexicographic minimum does not depend on the order in which it is reduced. Semantics:
-// csrc/foam_infer.cu:176-194 (walk_to) and :199-257 (eval_cell, exit faces) of the reference.
+// foam_infer.hip runs one ray per lane. The other layout for wave64 tests a cell's faces in parallel: a group of
+// G lanes (4, 8 or 16) serves one ray, 64 / G rays per wave; lane g of the group takes edges e0 + 1 + g,
+// e0 + 1 + g + G, ... of the cell's neighbourhood, and the exit face is a group min-reduction of (t, tie order).
+// The greedy walk to the start cell is a group argmin of (distance, tie order) in the same way. This kernel
+// covers the traversal alone (stage 0 of foam_infer: walk, then exit faces from cell to cell up to far or `cap`
+// samples; with no density T stays 1, so t_thresh <= 1 never stops a ray): the same visited cells, the same
+// sample counts and walk steps, bit for bit, since a lexicographic minimum does not depend on the order in which
+// it is reduced. Semantics: csrc/foam_infer.cu:176-194 (walk_to) and :199-257 (eval_cell, exit faces) of the
+// reference.
+//
+// The reduction runs on DPP row permutations (a VALU move each, no LDS): xor 1 and xor 2 within a quad, then the
+// half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i). After the steps up to width G every lane
+// of the group holds the group minimum, and no step reads outside the group, so groups whose ray has finished
+// (inactive lanes) are never read. Exact ties in t, which the tie order settles, are rare: they take a
+// wave-uniform slow path, so the common path has no per-lane branches.
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
 namespace vgr {
 namespace {
 
-constexpr int kGroup = 16;  // lanes per ray
-constexpr int kFacesBlock = 64;
-constexpr int kRaysPerBlock = kFacesBlock / kGroup;
+constexpr int kFacesBlock = 64;  // one wave per workgroup
 
 struct FacesScene {
     const float4* __restrict__ points;  // (N) p, w unused
@@ -29,36 +34,56 @@ struct FacesScene {
 };
 
 // k precedes j in the tie order: the smaller original index (INT_MAX: no site, after every site).
-__device__ __forceinline__ bool before_site(const FacesScene& S, int k, int j) {
+__device__ __noinline__ bool before_site(const FacesScene& S, int k, int j) {
     if (j == INT_MAX) return k != INT_MAX;
     if (k == INT_MAX) return false;
     return S.orig != nullptr ? S.orig[k] < S.orig[j] : k < j;
 }
 
-// (t, k) precedes (u, j) lexicographically.
-__device__ __forceinline__ bool precedes(const FacesScene& S, float t, int k, float u, int j) {
-    return t < u || (t == u && before_site(S, k, j));
-}
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
-// Group-wide lexicographic minimum of (t, k): every lane of the 16-lane group ends with it.
-__device__ __forceinline__ void group_min(const FacesScene& S, float& t, int& k) {
-#pragma unroll
-    for (int m = kGroup / 2; m >= 1; m >>= 1) {
-        const float u = __shfl_xor(t, m, kGroup);
-        const int j = __shfl_xor(k, m, kGroup);
-        if (precedes(S, u, j, t, k)) t = u, k = j;
+// Keeps the lexicographic minimum of (t, k) and the candidate (u, j): strict `<` on t, the tie order on equal t.
+__device__ __forceinline__ void keep_min(const FacesScene& S, float u, int j, float& t, int& k) {
+    bool take = u < t;
+    const bool tie = u == t && j != k;
+    if (wave_any(tie)) {  // wave-uniform branch; inside, only the tied lanes look up the tie order
+        if (tie) take = before_site(S, j, k);
     }
+    if (take) t = u, k = j;
 }
 
-template <bool TRACE>
+template <int CTRL>
+__device__ __forceinline__ int row_perm(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void reduce_step(const FacesScene& S, float& t, int& k) {
+    const float u = __int_as_float(row_perm<CTRL>(__float_as_int(t)));
+    const int j = row_perm<CTRL>(k);
+    keep_min(S, u, j, t, k);
+}
+
+// Group-wide lexicographic minimum of (t, k) over the G lanes of the group: every lane ends with it.
+template <int G>
+__device__ __forceinline__ void group_min(const FacesScene& S, float& t, int& k) {
+    static_assert(G == 4 || G == 8 || G == 16, "group width");
+    reduce_step<0xB1>(S, t, k);                  // quad_perm [1, 0, 3, 2]: lane ^ 1
+    reduce_step<0x4E>(S, t, k);                  // quad_perm [2, 3, 0, 1]: lane ^ 2
+    if constexpr (G >= 8) reduce_step<0x141>(S, t, k);   // row_half_mirror: i <-> 7 - i within 8
+    if constexpr (G >= 16) reduce_step<0x140>(S, t, k);  // row_mirror: i <-> 15 - i within 16
+}
+
+template <int G, bool TRACE>
 __global__ void __launch_bounds__(kFacesBlock)
     foam_faces_kernel(FacesScene S, const float* __restrict__ o_, const float* __restrict__ d_,
                       const int* __restrict__ start_, const float* __restrict__ near_, const float* __restrict__ far_,
                       const int* __restrict__ cap, int64_t n_rays, int* __restrict__ stats, int* __restrict__ trace,
                       int64_t trace_cap) {
-    const int g = static_cast<int>(threadIdx.x) % kGroup;
-    const int64_t r = xcd_block_id() * kRaysPerBlock + threadIdx.x / kGroup;
-    if (r >= n_rays) return;  // whole groups leave together: every shuffle stays within a live group
+    constexpr int kRaysPerBlock = kFacesBlock / G;
+    const int g = static_cast<int>(threadIdx.x) % G;
+    const int64_t r = xcd_block_id() * kRaysPerBlock + threadIdx.x / G;
+    if (r >= n_rays) return;  // whole groups leave together: every reduction stays within a live group
     int* st = stats + 5 * r;
     int cur = start_[r];
     if (cur < 0 || cur >= S.n_sites) {  // not traced
@@ -79,38 +104,46 @@ __global__ void __launch_bounds__(kFacesBlock)
             float bd = (x0 - pc.x) * (x0 - pc.x) + (x1 - pc.y) * (x1 - pc.y) + (x2 - pc.z) * (x2 - pc.z);
             int bk = cur;
             const int e0 = S.offsets[cur], e1 = S.offsets[cur + 1];
-            for (int e = e0 + 1 + g; e < e1; e += kGroup) {
+            for (int e = e0 + 1 + g; e < e1; e += G) {
                 const float4 ed = S.edge[e];
                 const int k = S.nbr[e];
                 const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
-                const float dk = v0 * v0 + v1 * v1 + v2 * v2;
-                if (precedes(S, dk, k, bd, bk)) bd = dk, bk = k;
+                keep_min(S, v0 * v0 + v1 * v1 + v2 * v2, k, bd, bk);
             }
-            group_min(S, bd, bk);
+            group_min<G>(S, bd, bk);
             if (bk == cur) break;
             cur = bk;
             ++walk_steps;
         }
     }
 
-    // the exit face of the cell at the current sample: group minimum of the bisector-plane parameters ahead
+    // the exit face of cell c: group minimum of the bisector-plane parameters of the faces ahead (n . d > 0)
+    auto face_t = [&](const float4& pc, const float4& ed, bool& ahead) {
+        const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
+        const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+        const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
+                    m2 = 0.5f * (ed.z + pc.z) - o[2];
+        ahead = dn > 0.f;
+        return (m0 * n0 + m1 * n1 + m2 * n2) / dn;
+    };
     auto exit_face = [&](int c, float& t_exit, int& next) {
         const float4 pc = S.points[c];
         t_exit = kInf, next = INT_MAX;
         const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
-        for (int e = e0 + 1 + g; e < e1; e += kGroup) {
-            const float4 ed = S.edge[e];
-            const int k = S.nbr[e];
-            const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
-            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
-            if (dn > 0.f) {
-                const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
-                            m2 = 0.5f * (ed.z + pc.z) - o[2];
-                const float tt = (m0 * n0 + m1 * n1 + m2 * n2) / dn;
-                if (precedes(S, tt, k, t_exit, next)) t_exit = tt, next = k;
-            }
+        for (int e = e0 + 1 + g; e < e1; e += 2 * G) {  // two faces per lane per trip, both loads issued first
+            const bool second = e + G < e1;
+            const float4 ea = S.edge[e];
+            const int ka = S.nbr[e];
+            float4 eb = ea;
+            int kb = INT_MAX;
+            if (second) eb = S.edge[e + G], kb = S.nbr[e + G];
+            bool ahead_a, ahead_b;
+            const float ta = face_t(pc, ea, ahead_a);
+            if (ahead_a) keep_min(S, ta, ka, t_exit, next);
+            const float tb = face_t(pc, eb, ahead_b);
+            if (second && ahead_b) keep_min(S, tb, kb, t_exit, next);
         }
-        group_min(S, t_exit, next);
+        group_min<G>(S, t_exit, next);
     };
 
     if (TRACE && g == 0 && trace_cap > 0) trace[r * trace_cap] = S.orig != nullptr ? S.orig[cur] : cur;
@@ -133,6 +166,19 @@ __global__ void __launch_bounds__(kFacesBlock)
     if (g == 0) st[0] = n_samples, st[1] = 0, st[2] = walk_steps, st[3] = 0, st[4] = 0;
 }
 
+template <int G>
+void launch_faces(const FacesScene& S, const float* o, const float* d, const int32_t* start, const float* near_t,
+                  const float* far_t, int64_t n_rays, const int32_t* cap, int32_t* stats, int32_t* trace,
+                  int64_t trace_cap, hipStream_t stream) {
+    const dim3 grid(grid_for(n_rays, kFacesBlock / G)), block(kFacesBlock);
+    if (trace != nullptr)
+        hipLaunchKernelGGL((foam_faces_kernel<G, true>), grid, block, 0, stream, S, o, d, start, near_t, far_t, cap,
+                           n_rays, stats, trace, trace_cap);
+    else
+        hipLaunchKernelGGL((foam_faces_kernel<G, false>), grid, block, 0, stream, S, o, d, start, near_t, far_t, cap,
+                           n_rays, stats, trace, int64_t{0});
+}
+
 }  // namespace
 }  // namespace vgr
 
@@ -140,10 +186,12 @@ extern "C" int vgr_foam_traverse_faces(const float* points, int64_t n_sites, con
                                        const int32_t* nbr, const float* edge, int64_t n_edges, const float* o,
                                        const float* d, const int32_t* start, const float* near_t, const float* far_t,
                                        int64_t n_rays, const int32_t* cap, const int32_t* orig, int32_t* stats,
-                                       int32_t* trace, int64_t trace_cap, void* stream) {
+                                       int32_t* trace, int64_t trace_cap, int64_t lanes_per_ray, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(n_rays >= 0, "foam_traverse_faces: n_rays must be >= 0");
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_traverse_faces: trace needs trace_cap > 0");
+    VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 4 || lanes_per_ray == 8 || lanes_per_ray == 16,
+                "foam_traverse_faces: lanes_per_ray must be 4, 8 or 16 (0: the default, 8)");
     if (n_rays == 0) return VGR_OK;
     VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_traverse_faces: n_sites must be in [1, 2^31)");
     VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_traverse_faces: n_edges must be in [N, 2^31)");
@@ -151,12 +199,11 @@ extern "C" int vgr_foam_traverse_faces(const float* points, int64_t n_sites, con
     VGR_REQUIRE(o && d && start && near_t && far_t && stats, "foam_traverse_faces: null ray pointer");
     const FacesScene S{reinterpret_cast<const float4*>(points), offsets, nbr, reinterpret_cast<const float4*>(edge),
                        orig, int(n_sites)};
-    const dim3 grid(grid_for(n_rays, kRaysPerBlock)), block(kFacesBlock);
-    if (trace != nullptr)
-        hipLaunchKernelGGL(foam_faces_kernel<true>, grid, block, 0, as_stream(stream), S, o, d, start, near_t, far_t,
-                           cap, n_rays, stats, trace, trace_cap);
-    else
-        hipLaunchKernelGGL(foam_faces_kernel<false>, grid, block, 0, as_stream(stream), S, o, d, start, near_t, far_t,
-                           cap, n_rays, stats, trace, int64_t{0});
+    const hipStream_t s = as_stream(stream);
+    switch (lanes_per_ray) {
+        case 4: launch_faces<4>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
+        case 16: launch_faces<16>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
+        default: launch_faces<8>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
+    }
     return launch_status("foam_faces_kernel");
 }

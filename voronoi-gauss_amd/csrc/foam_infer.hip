@@ -9,6 +9,9 @@
 // its lanes walk mostly the same cells (the per-edge loads of a cell are then one broadcast line per wave);
 // workgroups are remapped so each XCD renders a contiguous band of tiles (L2 locality). SH coefficient blocks
 // are cached per wave in LDS (the tile's rays read mostly the same sites); colours are evaluated per lane.
+// A second layout, a group of 2, 4 or 8 lanes per ray (foam_group_kernel below), splits each cell's
+// neighbourhood over the group's lanes; it is the faster one for traversal, density and lazy colours, one ray per
+// lane for fused and baked colours (default_lanes).
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -552,8 +555,331 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
 }
 
+// ------------------------------------------------------------------ group-per-ray layout
+//
+// The other wave64 layout: a group of G lanes (2, 4 or 8) serves one ray, 64 / G rays per wave (consecutive rays of
+// the host's pixel tiles). Lane g of the group takes edges e0 + g, e0 + g + G, ... of each cell's self-first
+// neighbourhood: its exit candidates, density terms and colour terms. The group then combines them with DPP row
+// permutations (xor 1, then xor 2 within a quad, then the half-row mirror i <-> 7 - i): the exit face is the
+// lexicographic minimum of (t, tie order), the same face as a sequential scan, so the visited cells are identical;
+// sums (density, lazy colour weights, the sample statistics) and fused colour blends are combined in a butterfly,
+// whose pairwise operations are commutative, so every lane of the group ends with the same bits and the group
+// runs the compositing in lockstep. Only the summation order of the field terms differs from a sequential scan
+// (a few ulps). Per lane this layout runs the same face and field arithmetic as one ray per lane, but 64 / G rays
+// per wave keep more independent loads in flight per wave, and a wave's loads of one cell are contiguous.
+
+template <int CTRL>
+__device__ __forceinline__ int row_perm(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float row_perm(float v) {
+    return __int_as_float(row_perm<CTRL>(__float_as_int(v)));
+}
+
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141;  // DPP: quad_perm [1,0,3,2], [2,3,0,1]; row_half_mirror
+
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// k precedes j in the tie order, INT_MAX (no face) after every site.
+__device__ __noinline__ bool before_or_none(const FoamScene& S, int k, int j) {
+    if (j == INT_MAX) return k != INT_MAX;
+    if (k == INT_MAX) return false;
+    return before(S, k, j);
+}
+
+// Keeps the lexicographic minimum of (t, k) and the candidate (u, j). Exact ties in t are rare: they take a
+// wave-uniform branch, inside which only the tied lanes look up the tie order.
+__device__ __forceinline__ void keep_min(const FoamScene& S, float u, int j, float& t, int& k) {
+    bool take = u < t;
+    const bool tie = u == t && j != k;
+    if (wave_any(tie)) {
+        if (tie) take = before_or_none(S, j, k);
+    }
+    if (take) t = u, k = j;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void min_step(const FoamScene& S, float& t, int& k) {
+    const float u = row_perm<CTRL>(t);
+    const int j = row_perm<CTRL>(k);
+    keep_min(S, u, j, t, k);
+}
+
+template <int G>
+__device__ __forceinline__ void group_min(const FoamScene& S, float& t, int& k) {
+    static_assert(G == 2 || G == 4 || G == 8, "group width");
+    min_step<kXor1>(S, t, k);
+    if constexpr (G >= 4) min_step<kXor2>(S, t, k);
+    if constexpr (G == 8) min_step<kHalfMirror>(S, t, k);
+}
+
+template <int G, typename V>
+__device__ __forceinline__ V group_sum(V v) {
+    v = v + row_perm<kXor1>(v);
+    if constexpr (G >= 4) v = v + row_perm<kXor2>(v);
+    if constexpr (G == 8) v = v + row_perm<kHalfMirror>(v);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_fmin(float v) {
+    v = fminf(v, row_perm<kXor1>(v));
+    if constexpr (G >= 4) v = fminf(v, row_perm<kXor2>(v));
+    if constexpr (G == 8) v = fminf(v, row_perm<kHalfMirror>(v));
+    return v;
+}
+
+// Two running blends combined: both rescaled to the smaller Mahalanobis distance. The products are rounded
+// separately (no contraction), so merge(A, B) and merge(B, A) give the same bits.
+template <int CTRL>
+__device__ __forceinline__ void blend_step(Blend& B) {
+    const float m2 = row_perm<CTRL>(B.m), a2 = row_perm<CTRL>(B.a), r2 = row_perm<CTRL>(B.r),
+                g2 = row_perm<CTRL>(B.g), b2 = row_perm<CTRL>(B.b);
+    const float m = fminf(B.m, m2);
+    const float s1 = fexp(-0.5f * (B.m - m)), s2 = fexp(-0.5f * (m2 - m));
+    const float pa = B.a * s1, qa = a2 * s2, pr = B.r * s1, qr = r2 * s2;
+    const float pg = B.g * s1, qg = g2 * s2, pb = B.b * s1, qb = b2 * s2;
+    B.a = pa + qa, B.r = pr + qr, B.g = pg + qg, B.b = pb + qb, B.m = m;
+}
+
+template <int G>
+__device__ __forceinline__ void group_blend(Blend& B) {
+    blend_step<kXor1>(B);
+    if constexpr (G >= 4) blend_step<kXor2>(B);
+    if constexpr (G == 8) blend_step<kHalfMirror>(B);
+}
+
+template <int G>
+__device__ int walk_group(const FoamScene& S, int c, int g, float x0, float x1, float x2, int& steps) {
+    for (int it = 0; it < kWalkCap; ++it) {
+        const float4 pc = S.points[c];
+        float bd = (x0 - pc.x) * (x0 - pc.x) + (x1 - pc.y) * (x1 - pc.y) + (x2 - pc.z) * (x2 - pc.z);
+        int bk = c;
+        const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+        for (int e = e0 + 1 + g; e < e1; e += G) {
+            const float4 ed = S.edge[e];
+            const int k = S.nbr[e];
+            const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
+            keep_min(S, v0 * v0 + v1 * v1 + v2 * v2, k, bd, bk);
+        }
+        group_min<G>(S, bd, bk);
+        if (bk == c) break;
+        c = bk;
+        ++steps;
+    }
+    return c;
+}
+
+// eval_cell for lane g of a group: the lane's share of the neighbourhood, then the group reductions.
+template <int STAGE, int COLOR, bool HALF, int DEG, int G>
+__device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, const float (&o)[3],
+                                const float (&d)[3], const float (&b)[16], ColorCache<Tune<COLOR>::slots>& cache,
+                                bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
+    constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
+    const float4 pc = S.points[c];
+    float x[3];
+    sample_point(o, d, t, x);
+    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
+    blend_init(R.B);
+    for (int e = e0 + g; e < e1; e += G) {
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+        const SiteRec q = site_rec<STAGE>(S, k);
+        if (want_exit && e > e0) {
+            const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
+            const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
+            if (dn > 0.f) {
+                const float m0 = 0.5f * (ed.x + pc.x) - o[0], m1 = 0.5f * (ed.y + pc.y) - o[1],
+                            m2 = 0.5f * (ed.z + pc.z) - o[2];
+                keep_min(S, (m0 * n0 + m1 * n1 + m2 * n2) / dn, k, R.t_exit, R.next);
+            }
+        }
+        if (STAGE >= 1) {
+            float v0, v1, v2, r2;
+            offset_of(x, ed, v0, v1, v2, r2);
+            const float2 cut = cutoffs(ed.w);
+            if (r2 <= cut.x) {
+                R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
+                ++n_dens;
+            }
+            if (STAGE >= 2) {
+                const float lb = r2 * cut.y;
+                if (BLEND) {
+                    const float lim = R.B.m + P.color_cut;
+                    if (lb <= lim) {
+                        const float m = maha_f(q.q2, q.q3, v0, v1, v2);
+                        if (m <= lim) {
+                            float c3[3];
+                            if (COLOR == kBaked) {
+                                const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
+                                c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
+                            } else {
+                                ++n_sh;
+                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                            }
+                            blend_add(R.B, m, c3[0], c3[1], c3[2]);
+                        }
+                    }
+                } else if (lb < R.mmin) {
+                    R.mmin = fminf(R.mmin, maha_f(q.q2, q.q3, v0, v1, v2));
+                }
+            }
+        }
+    }
+    if (want_exit) group_min<G>(S, R.t_exit, R.next);
+    if (STAGE >= 1) R.sigma = group_sum<G>(R.sigma);
+    if (STAGE >= 2 && !BLEND) R.mmin = group_fmin<G>(R.mmin);
+    if (BLEND) group_blend<G>(R.B);
+}
+
+// color_lazy for lane g of a group: weights relative to the group's mmin, so the colour-cut tests are those of a
+// sequential scan; the weighted sums are combined at the end.
+template <bool HALF, int DEG, int G>
+__device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, float mmin,
+                                 const float (&o)[3], const float (&d)[3], const float (&b)[16],
+                                 ColorCache<Tune<kLazy>::slots>& cache, float (&C)[3], int& n_sh) {
+    float x[3];
+    sample_point(o, d, t, x);
+    const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
+    const float cut = mmin + P.color_cut;
+    float A = 0.f, r = 0.f, gr = 0.f, bl = 0.f;
+    for (int e = e0 + g; e < e1; e += G) {
+        const float4 ed = S.edge[e];
+        const int k = S.nbr[e];
+        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+        const float4 q2 = a[2], q3 = a[3];
+        float v0, v1, v2, r2;
+        offset_of(x, ed, v0, v1, v2, r2);
+        if (r2 * cutoffs(ed.w).y <= cut) {
+            const float m = maha_f(q2, q3, v0, v1, v2);
+            if (m <= cut) {
+                float c3[3];
+                ++n_sh;
+                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                accumulate(A, r, gr, bl, weight_of(m, mmin), c3);
+            }
+        }
+    }
+    A = group_sum<G>(A), r = group_sum<G>(r), gr = group_sum<G>(gr), bl = group_sum<G>(bl);
+    const float inv = 1.f / A;
+    C[0] = r * inv, C[1] = gr * inv, C[2] = bl * inv;
+}
+
+// foam_infer_kernel with a group of G lanes per ray; same outputs (the group's lane 0 writes them).
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, int G>
+__global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
+    foam_group_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
+    constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
+    constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
+    constexpr int SLOTS = Tune<COLOR>::slots;
+    __shared__ float4 cache_lds[cache_vec4<SLOTS>(kSH)];
+    ColorCache<SLOTS> cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache<SLOTS>(cache_lds);
+    const int g = static_cast<int>(threadIdx.x) % G;
+    const int64_t r = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
+    if (r >= R.n) return;  // whole groups leave together
+    const bool writer = g == 0;
+    const int start = R.start[r];
+    if (start < 0 || start >= S.n_sites) {  // not traced: empty foreground
+        if (writer) {
+            O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+            O.T[r] = 1.f, O.depth[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) O.stats[5 * r + i] = 0;
+        }
+        return;
+    }
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float t_near = R.t_near[r], t_far = R.t_far[r];
+    const int max_samples = R.cap != nullptr ? R.cap[r] : INT_MAX;
+    float b[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) b[i] = 0.f;
+    if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
+
+    int walk_steps = 0, n_dens = 0, n_sh = 0;
+    int c = walk_group<G>(S, start, g, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
+    CellEval E;
+    eval_cell_group<STAGE, COLOR, HALF, DEG, G>(S, P, c, g, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    if (writer) trace_cell<TRACE>(S, O, r, 0, c);
+    float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
+    bool hasP = false;
+    int cP = c;
+    if (BLEND) {
+        const float inv = 1.f / E.B.a;
+        CP[0] = E.B.r * inv, CP[1] = E.B.g * inv, CP[2] = E.B.b * inv, hasP = true;
+    }
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    int n_samples = 1, n_color = 0;
+    for (int it = 0; it < kMaxCells; ++it) {
+        const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
+        const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
+        const int cQ = last ? c : E.next;
+        eval_cell_group<STAGE, COLOR, HALF, DEG, G>(S, P, cQ, g, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        if (writer) trace_cell<TRACE>(S, O, r, n_samples, cQ);
+        ++n_samples;
+        const float sQ = E.sigma, mQ = E.mmin;
+        const float delta = tQ - tP;
+        const float alpha = 1.f - fexp(-0.5f * (sP + sQ) * delta);
+        const float w = T * alpha;
+        float CQ[3] = {0.f, 0.f, 0.f};
+        bool hasQ = false;
+        if (BLEND) {
+            const float inv = 1.f / E.B.a;
+            CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv, hasQ = true;
+        }
+        if (STAGE >= 2 && w > P.w_thresh) {
+            if constexpr (!BLEND) {
+                if (!hasP) color_lazy_group<HALF, DEG, G>(S, P, cP, g, tP, mP, o, d, b, cache, CP, n_sh);
+                color_lazy_group<HALF, DEG, G>(S, P, cQ, g, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                hasQ = true;
+            }
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (CP[a] + CQ[a]);
+            dep += w * 0.5f * (tP + tQ);
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        tP = tQ, sP = sQ, mP = mQ, hasP = hasQ, cP = cQ, c = cQ;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
+        if (last || T < P.t_thresh) break;
+    }
+    n_dens = group_sum<G>(n_dens), n_sh = group_sum<G>(n_sh);
+    if (writer) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
+        O.T[r] = T;
+        O.depth[r] = dep;
+        int* st = O.stats + 5 * r;
+        st[0] = n_samples, st[1] = n_color, st[2] = walk_steps, st[3] = n_dens, st[4] = n_sh;
+    }
+}
+
+// lanes: 1 = one ray per lane (foam_infer_kernel), 2, 4 or 8 = a group of that many lanes per ray
+// (foam_group_kernel).
 template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
-int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
+int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes,
+           hipStream_t stream) {
+    if (lanes == 2) {
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 2>), dim3(grid_for(R.n, kBlock / 2)),
+                           dim3(kBlock), 0, stream, S, P, R, O);
+        return launch_status("foam_group_kernel");
+    }
+    if (lanes == 4) {
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 4>), dim3(grid_for(R.n, kBlock / 4)),
+                           dim3(kBlock), 0, stream, S, P, R, O);
+        return launch_status("foam_group_kernel");
+    }
+    if (lanes == 8) {
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 8>), dim3(grid_for(R.n, kBlock / 8)),
+                           dim3(kBlock), 0, stream, S, P, R, O);
+        return launch_status("foam_group_kernel");
+    }
     hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, DEG, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock),
                        0, stream, S, P, R, O);
     return launch_status("foam_infer_kernel");
@@ -561,26 +887,39 @@ int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const Foa
 
 // Kernels with SH colours are specialised on the SH degree (block size and basis known at compile time).
 template <int COLOR, bool HALF, bool TRACE>
-int launch_sh(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
+int launch_sh(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes,
+              hipStream_t stream) {
     switch (P.sh_deg) {
-        case 0: return launch<2, COLOR, HALF, 0, TRACE>(S, P, R, O, stream);
-        case 1: return launch<2, COLOR, HALF, 1, TRACE>(S, P, R, O, stream);
-        case 2: return launch<2, COLOR, HALF, 2, TRACE>(S, P, R, O, stream);
-        default: return launch<2, COLOR, HALF, 3, TRACE>(S, P, R, O, stream);
+        case 0: return launch<2, COLOR, HALF, 0, TRACE>(S, P, R, O, lanes, stream);
+        case 1: return launch<2, COLOR, HALF, 1, TRACE>(S, P, R, O, lanes, stream);
+        case 2: return launch<2, COLOR, HALF, 2, TRACE>(S, P, R, O, lanes, stream);
+        default: return launch<2, COLOR, HALF, 3, TRACE>(S, P, R, O, lanes, stream);
     }
 }
 
 template <bool TRACE>
 int dispatch(int stage, int color_mode, bool half, const FoamScene& S, const FoamParams& P, const FoamRays& R,
-             const FoamOut& O, hipStream_t stream) {
-    if (stage == 0) return launch<0, kLazy, false, 0, TRACE>(S, P, R, O, stream);
-    if (stage == 1) return launch<1, kLazy, false, 0, TRACE>(S, P, R, O, stream);
-    if (color_mode == kBaked) return launch<2, kBaked, false, 0, TRACE>(S, P, R, O, stream);
+             const FoamOut& O, int lanes, hipStream_t stream) {
+    if (stage == 0) return launch<0, kLazy, false, 0, TRACE>(S, P, R, O, lanes, stream);
+    if (stage == 1) return launch<1, kLazy, false, 0, TRACE>(S, P, R, O, lanes, stream);
+    if (color_mode == kBaked) return launch<2, kBaked, false, 0, TRACE>(S, P, R, O, lanes, stream);
     if (color_mode == kLazy)
-        return half ? launch_sh<kLazy, true, TRACE>(S, P, R, O, stream)
-                    : launch_sh<kLazy, false, TRACE>(S, P, R, O, stream);
-    return half ? launch_sh<kFused, true, TRACE>(S, P, R, O, stream)
-                : launch_sh<kFused, false, TRACE>(S, P, R, O, stream);
+        return half ? launch_sh<kLazy, true, TRACE>(S, P, R, O, lanes, stream)
+                    : launch_sh<kLazy, false, TRACE>(S, P, R, O, lanes, stream);
+    return half ? launch_sh<kFused, true, TRACE>(S, P, R, O, lanes, stream)
+                : launch_sh<kFused, false, TRACE>(S, P, R, O, lanes, stream);
+}
+
+// Lanes per ray of vgr_foam_infer and vgr_foam_infer_traced, the faster layout per path on config 3 (8.29M rays,
+// 2M sites, SH degree 3). Traversal and density: 4 lanes per ray (stage 0: 42.6 ms against 60.6 with one ray per
+// lane; stage 1: 59.3 against 67.2); lazy colours: 4 (262.8 against 276.6 ms). Fused and baked colours: one ray
+// per lane (205.9 against 223.0, 249.9 and 290.6 ms at 2, 4 and 8 lanes; baked 107.6 against 109.3 at 2): their
+// colour lookups run for every neighbour of every sample, and the 64 rays of a tile, in the same cell, step through
+// its neighbours together, one site per lookup, where a group's lanes ask for different sites at once (29 % more
+// VALU and LDS instructions per launch at 4 lanes).
+constexpr int kDefaultLanes = 0;
+inline int default_lanes(int64_t stage, int64_t color_mode) {
+    return stage < 2 || color_mode == kLazy ? 4 : 1;
 }
 
 int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr, const float* edge,
@@ -588,8 +927,12 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
                double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
-               int32_t* trace, int64_t trace_cap, void* stream) {
+               int32_t* trace, int64_t trace_cap, int64_t lanes, void* stream) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
+    if (lanes == kDefaultLanes) lanes = default_lanes(stage, color_mode);
+    VGR_REQUIRE(lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8,
+                "foam_infer: lanes_per_ray must be 1, 2, 4 or 8 (got %lld)",
+                static_cast<long long>(lanes));
     VGR_REQUIRE(color_mode >= kLazy && color_mode <= kFused,
                 "color_mode must be 0 (lazy), 1 (baked) or 2 (fused)");
     VGR_REQUIRE(stage >= 0 && stage <= 2, "stage must be 0, 1 or 2");
@@ -617,8 +960,11 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     const FoamRays R{o, d, start, near_t, far_t, cap, n_rays};
     const FoamOut O{rgb, T, depth, stats, trace, trace_cap};
     const hipStream_t s = as_stream(stream);
-    if (trace != nullptr) return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, s);
-    return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, s);
+    // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
+    // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
+    if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
+    if (trace != nullptr) return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
+    return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
 }
 
 }  // namespace
@@ -633,7 +979,7 @@ extern "C" int vgr_foam_infer(const float* points, int64_t n_sites, const int32_
                               int32_t* stats, void* stream) {
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, nullptr, 0, stream);
+                           T, depth, stats, nullptr, 0, vgr::kDefaultLanes, stream);
 }
 
 extern "C" int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* offsets,
@@ -647,5 +993,20 @@ extern "C" int vgr_foam_infer_traced(const float* points, int64_t n_sites, const
     VGR_REQUIRE(trace != nullptr && trace_cap > 0, "foam_infer_traced: trace must be non-null with trace_cap > 0");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, trace, trace_cap, stream);
+                           T, depth, stats, trace, trace_cap, vgr::kDefaultLanes, stream);
+}
+
+extern "C" int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                                    const float* edge, int64_t n_edges, const float* attr, const void* sh,
+                                    int32_t sh_half, int64_t sh_deg, const float* o, const float* d,
+                                    const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
+                                    double t_thresh, double w_thresh, double color_cut, int64_t color_mode,
+                                    int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
+                                    float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                                    int64_t lanes_per_ray, void* stream) {
+    VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_lanes: trace needs trace_cap > 0");
+    return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
+                           near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
+                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap,
+                           lanes_per_ray, stream);
 }

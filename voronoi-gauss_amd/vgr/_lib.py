@@ -20,10 +20,13 @@ SIGNATURES = {
 					   _I64, _I64, _P, _P, _P, _P, _P, _P, _P],
 	'vgr_foam_infer_traced': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64,
 							  _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+	'vgr_foam_infer_lanes': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64,
+							 _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P],
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
-	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P],
+	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
+								_P],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P, _I64, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
@@ -36,7 +39,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 8
 _lib = None
 
 

@@ -154,9 +154,11 @@ class _MarchExtension:
 class _FoamInferExtension:
 	@staticmethod
 	def foam_infer(points, offsets, nbr, edge, attr, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-				   color_cut, color_mode, stage, cap, orig, trace_cap=0):
+				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 5) int32] (+ trace (B, trace_cap) int32, the cell of
-		every sample in original numbering, -1 past the last sample, when trace_cap > 0)."""
+		every sample in original numbering, -1 past the last sample, when trace_cap > 0). lanes: None for the
+		library's default layout, else 1 (one ray per lane) or 2 / 4 / 8 (that many lanes per ray,
+		vgr_foam_infer_lanes)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32), (attr, 'attr', torch.float32),
 						 (o, 'o', torch.float32), (d, 'd', torch.float32), (start, 'start', torch.int32),
@@ -194,16 +196,19 @@ class _FoamInferExtension:
 				float(t_thresh), float(w_thresh), float(color_cut), int(color_mode), int(stage), ptr(cp), ptr(og),
 				ptr(rgb), ptr(T), ptr(depth), ptr(stats)]
 		with torch.cuda.device(dev):
-			if trace is None:
+			if lanes is not None:
+				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0, int(lanes),
+					 stream_of(dev))
+			elif trace is None:
 				call('vgr_foam_infer', *args, stream_of(dev))
 			else:
 				call('vgr_foam_infer_traced', *args, ptr(trace), int(trace_cap), stream_of(dev))
 		return out
 
 
-def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0):
-	"""Cell traversal alone with a group of 16 lanes per ray (vgr_foam_traverse_faces, the lane-per-face layout):
-	the outputs foam_infer gives with stage 0 -> stats (B, 5) int32 [samples, 0, walk steps, 0, 0] (+ trace
+def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0, lanes=8):
+	"""Cell traversal alone with a group of `lanes` (4, 8 or 16) lanes per ray (vgr_foam_traverse_faces, the
+	lane-per-face layout): the outputs foam_infer gives with stage 0 -> stats (B, 5) int32 [samples, 0, walk steps, 0, 0] (+ trace
 	(B, trace_cap), the cell of every sample in original numbering, -1 past the last, when trace_cap > 0)."""
 	for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32), (nbr, 'nbr', torch.int32),
 					 (edge, 'edge', torch.float32), (o, 'o', torch.float32), (d, 'd', torch.float32),
@@ -220,7 +225,7 @@ def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None,
 		with torch.cuda.device(dev):
 			call('vgr_foam_traverse_faces', ptr(points), n, ptr(offsets), ptr(nbr), ptr(edge), nbr.numel(), ptr(o),
 				 ptr(d), ptr(start), ptr(near), ptr(far), B, ptr(cp), ptr(og), ptr(stats), ptr(trace), int(trace_cap),
-				 stream_of(dev))
+				 int(lanes), stream_of(dev))
 	return (stats, trace) if trace is not None else stats
 
 
