@@ -121,7 +121,7 @@ def main():
 	ap.add_argument('--lanes-per-ray', type=int, default=None, choices=[1, 2, 4, 8],
 					help='foam workload: ray layout (1: one ray per lane, 2 / 4 / 8: lanes per ray; default: the '
 						 'library default)')
-	ap.add_argument('--lanes', type=int, default=8, choices=[4, 8, 16],
+	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
 	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack', 'traverse'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
@@ -473,9 +473,10 @@ def bench_march(args):
 
 def bench_traverse(args):
 	"""The traversal alone (walk to the start cell, then exit faces cell to cell: foam_infer with stage 0) of the
-	config-3 workload in the two wave64 layouts: one ray per lane over 8x8 tiles (vgr_foam_infer) and a group of
-	16 lanes per ray, each testing every 16th face, with a group min-reduction (vgr_foam_traverse_faces). Both
-	must give the same per-ray statistics; the JSON line is the lane-per-face layout, the other beside it."""
+	config-3 workload in the two wave64 layouts: one ray per lane over 8x8 tiles (vgr_foam_infer_lanes with 1 lane
+	per ray) and a group of 4, 8 or 16 lanes per ray, each testing every 4th / 8th / 16th face, with a group
+	min-reduction (vgr_foam_traverse_faces). All must give the same per-ray statistics; the JSON line is the
+	lane-per-face layout of --lanes, the others beside it."""
 	import numpy as np
 	import torch
 
@@ -495,7 +496,8 @@ def bench_traverse(args):
 	stream = torch.cuda.current_stream(dev)
 	lane_ms, out_lane, _ = time_steps(
 		lambda: fi.foam_infer(pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'],
-							  sc.sh_deg, o, d, start, near, far, 1e-4, 1e-4, math.inf, 0, 0, empty, pack['orig']),
+							  sc.sh_deg, o, d, start, near, far, 1e-4, 1e-4, math.inf, 0, 0, empty, pack['orig'],
+							  lanes=1),
 		args.steps, args.warmup, stream)
 	ms_lane = float(np.mean(lane_ms))
 	group_ms, same = {}, True

@@ -90,7 +90,7 @@ int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* of
 
 /*
  * Cell traversal alone (foam_infer with stage 0: walk to the start cell, then exit faces up to far or cap) with a
- * group of lanes_per_ray lanes (4, 8 or 16; 0 = 8) per ray, each testing every lanes_per_ray-th face, and a group
+ * group of lanes_per_ray lanes (4, 8 or 16; 0 = 4) per ray, each testing every lanes_per_ray-th face, and a group
  * min-reduction of the exit parameter. No counterpart in the reference: it is the lane-per-face layout against
  * which vgr_foam_infer's thread-per-ray layout is compared (same outputs bit for bit). stats i32 (B, 5) as
  * vgr_foam_infer's (sample and walk-step counts, the rest 0); trace (optional, NULL = none) i32 (B, trace_cap):

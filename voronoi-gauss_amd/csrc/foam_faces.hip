@@ -191,7 +191,7 @@ extern "C" int vgr_foam_traverse_faces(const float* points, int64_t n_sites, con
     VGR_REQUIRE(n_rays >= 0, "foam_traverse_faces: n_rays must be >= 0");
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_traverse_faces: trace needs trace_cap > 0");
     VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 4 || lanes_per_ray == 8 || lanes_per_ray == 16,
-                "foam_traverse_faces: lanes_per_ray must be 4, 8 or 16 (0: the default, 8)");
+                "foam_traverse_faces: lanes_per_ray must be 4, 8 or 16 (0: the default, 4)");
     if (n_rays == 0) return VGR_OK;
     VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_traverse_faces: n_sites must be in [1, 2^31)");
     VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_traverse_faces: n_edges must be in [N, 2^31)");
@@ -201,9 +201,9 @@ extern "C" int vgr_foam_traverse_faces(const float* points, int64_t n_sites, con
                        orig, int(n_sites)};
     const hipStream_t s = as_stream(stream);
     switch (lanes_per_ray) {
-        case 4: launch_faces<4>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
+        case 8: launch_faces<8>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
         case 16: launch_faces<16>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
-        default: launch_faces<8>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
+        default: launch_faces<4>(S, o, d, start, near_t, far_t, n_rays, cap, stats, trace, trace_cap, s); break;
     }
     return launch_status("foam_faces_kernel");
 }

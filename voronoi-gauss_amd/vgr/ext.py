@@ -206,10 +206,11 @@ class _FoamInferExtension:
 		return out
 
 
-def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0, lanes=8):
+def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0, lanes=4):
 	"""Cell traversal alone with a group of `lanes` (4, 8 or 16) lanes per ray (vgr_foam_traverse_faces, the
-	lane-per-face layout): the outputs foam_infer gives with stage 0 -> stats (B, 5) int32 [samples, 0, walk steps, 0, 0] (+ trace
-	(B, trace_cap), the cell of every sample in original numbering, -1 past the last, when trace_cap > 0)."""
+	lane-per-face layout): the outputs foam_infer gives with stage 0 -> stats (B, 5) int32 [samples, 0, walk
+	steps, 0, 0] (+ trace (B, trace_cap), the cell of every sample in original numbering, -1 past the last, when
+	trace_cap > 0)."""
 	for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32), (nbr, 'nbr', torch.int32),
 					 (edge, 'edge', torch.float32), (o, 'o', torch.float32), (d, 'd', torch.float32),
 					 (start, 'start', torch.int32), (near, 'near', torch.float32), (far, 'far', torch.float32)):
