@@ -257,6 +257,7 @@ def bench_foam(args):
 			'sites': sc.n_sites, 'rays_per_step': B, 'frames_per_step': frames,
 			'fps_1080p': round(frames / (ms * 1e-3), 2) if frames else None,
 			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
+			'lanes_per_ray': args.lanes_per_ray or (4 if args.colors == 'exact' else 1),
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': f'{args.tile}x{args.tile} tiles', 't_thresh': 1e-4, 'w_thresh': 1e-4,
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
