@@ -75,9 +75,10 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
  * vgr_foam_infer_traced with the ray layout chosen by the caller: lanes_per_ray 1 runs one ray per lane, 2, 4 or 8
  * a group of that many lanes per ray (each lane takes every lanes_per_ray-th edge of a cell's neighbourhood; the
  * group combines exit faces by a lexicographic minimum, so the visited cells are the same, and density and colour
- * terms by sums, so only their summation order differs), 0 the library's default (the layout vgr_foam_infer
- * runs: 4 lanes per ray for stages 0 and 1 and lazy colours, one ray per lane for fused and baked colours). Fused and baked colours with a finite color_cut always run one ray per lane (their neighbour skipping
- * follows the edge order). trace may be NULL (then trace_cap is ignored). No counterpart in the reference: the layout comparison
+ * terms by sums, so only their summation order differs), 0 the library's default (the layout vgr_foam_infer runs:
+ * 4 lanes per ray for stages 0 and 1 and lazy colours, one ray per lane for fused and baked colours). Fused and
+ * baked colours with a finite color_cut always run one ray per lane (their neighbour skipping follows the edge
+ * order). trace may be NULL (then trace_cap is ignored). No counterpart in the reference: the layout comparison
  * for vgr_foam_infer, whose arguments and outputs it otherwise shares.
  */
 int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
