@@ -166,6 +166,36 @@ int64_t vgr_field_work_size(int64_t n_sites);
 int vgr_conic_forward(const float* log_scale, const float* quat, int64_t n, double floor, float* A, void* stream);
 
 /*
+ * Gradients of vgr_density_forward (scale_mult 1) for dL/dsigma = grad_sigma (m). Replaces density_backward() of
+ * csrc/vgf.cu:477-492 (export :568), bound by ext._Density.backward (ext.py:69-75). Accumulated into g_raw (N),
+ * g_ls (N, 3) and g_quat (N, 4), which the caller zeroes; terms with rho_k G_k |dL/dsigma| <= 1e-12 are skipped.
+ * The per-site sums use fp32 atomics, so their last bits vary from run to run.
+ */
+int vgr_density_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                         int64_t n_adj, const float* raw, const float* log_scale, const float* quat, const float* x,
+                         const int32_t* site, int64_t m, const float* grad_sigma, float* g_raw, float* g_ls,
+                         float* g_quat, void* stream);
+
+/*
+ * Gradients of vgr_color_forward for dL/drgb = grad_rgb (m, 3), given its output rgb (m, 3). Replaces
+ * color_backward() of csrc/vgf.cu:515-533 (export :570), bound by ext._Color.backward (ext.py:99-105).
+ * Accumulated into g_ls (N, 3), g_quat (N, 4) and g_sh (N, 16, 3), which the caller zeroes; normalised weights below
+ * 1e-7 get no gradient. fp32 atomics, as vgr_density_backward.
+ */
+int vgr_color_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                       int64_t n_adj, const float* log_scale, const float* quat, const float* sh, int64_t sh_deg,
+                       const float* x, const float* dirs, const int32_t* site, int64_t m, const float* rgb,
+                       const float* grad_rgb, float* g_ls, float* g_quat, float* g_sh, void* stream);
+
+/*
+ * Gradients of vgr_conic_forward for dL/dA = gA (n, 6) (off-diagonal entries standing for both A_ab and A_ba),
+ * written to g_ls (n, 3) and g_quat (n, 4). Replaces conic_backward() of csrc/vgf.cu:548-560 (export :565),
+ * bound by ext._Conic.backward (ext.py:127-131).
+ */
+int vgr_conic_backward(const float* log_scale, const float* quat, int64_t n, double floor, const float* gA,
+                       float* g_ls, float* g_quat, void* stream);
+
+/*
  * Uniform grid over the sites for exact nearest-site queries: the start-cell locator. No kernel of the reference
  * corresponds; it replaces the host-side cKDTree query of nearest_sites() (sites.py:38-39), which finds the start
  * site per camera centre (bench_infer.py:60, eval_scene.py:69, bench_fps.py:156) and per ray origin of a ray batch.

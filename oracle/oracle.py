@@ -26,6 +26,9 @@ _SIGS = {
 	'oracle_density': ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _F32, _P, _I32], None),
 	'oracle_color': ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _I32], None),
 	'oracle_conic': ([_P, _P, _I64, _F32, _P], None),
+	'oracle_density_backward': ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P], None),
+	'oracle_color_backward': ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _P, _P, _P], None),
+	'oracle_conic_backward': ([_P, _P, _I64, _F32, _P, _P, _P], None),
 	'oracle_sh_basis': ([_F32, _F32, _F32, _I32, _P], None),
 	'oracle_sample_at': ([_F32, _F32, _F32, _I32, _F32, _I32, _I32, _P, _P], None),
 	'oracle_omp_max_threads': ([], ctypes.c_int),
@@ -151,6 +154,38 @@ def conic(log_scale, quat, floor=0.0):
 	A = np.zeros((len(q), 6), np.float32)
 	load().oracle_conic(_p(ls), _p(q), len(q), float(np.float32(floor * floor)), _p(A))
 	return A
+
+
+def density_backward(points, offsets, adj, raw, log_scale, quat, x, site, grad_sigma):
+	"""-> g_raw (N,), g_ls (N, 3), g_quat (N, 4), accumulated in sample order on one thread."""
+	arrs = [_a(points, np.float32), _a(offsets, np.int32), _a(adj, np.int32), _a(raw, np.float32),
+			_a(log_scale, np.float32), _a(quat, np.float32), _a(x, np.float32), _a(site, np.int32)]
+	n, m = len(arrs[3]), len(arrs[6])
+	g_raw, g_ls, g_quat = np.zeros(n, np.float32), np.zeros((n, 3), np.float32), np.zeros((n, 4), np.float32)
+	load().oracle_density_backward(*[_p(a) for a in arrs], m, _p(_a(grad_sigma, np.float32)), _p(g_raw), _p(g_ls),
+								   _p(g_quat))
+	return g_raw, g_ls, g_quat
+
+
+def color_backward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site, rgb, grad_rgb):
+	"""-> g_ls (N, 3), g_quat (N, 4), g_sh (N, 16, 3), accumulated in sample order on one thread."""
+	arrs = [_a(points, np.float32), _a(offsets, np.int32), _a(adj, np.int32), _a(log_scale, np.float32),
+			_a(quat, np.float32), _a(sh, np.float32)]
+	tail = [_a(x, np.float32), _a(dirs, np.float32), _a(site, np.int32)]
+	n, m = len(arrs[4]), len(tail[0])
+	g_ls, g_quat, g_sh = np.zeros((n, 3), np.float32), np.zeros((n, 4), np.float32), np.zeros((n, 16, 3), np.float32)
+	load().oracle_color_backward(*[_p(a) for a in arrs], int(sh_deg), *[_p(a) for a in tail], m,
+								 _p(_a(rgb, np.float32)), _p(_a(grad_rgb, np.float32)), _p(g_ls), _p(g_quat), _p(g_sh))
+	return g_ls, g_quat, g_sh
+
+
+def conic_backward(log_scale, quat, gA, floor=0.0):
+	"""-> g_ls (n, 3), g_quat (n, 4)."""
+	ls, q = _a(log_scale, np.float32), _a(quat, np.float32)
+	g_ls, g_quat = np.zeros((len(q), 3), np.float32), np.zeros((len(q), 4), np.float32)
+	load().oracle_conic_backward(_p(ls), _p(q), len(q), float(np.float32(floor * floor)), _p(_a(gA, np.float32)),
+								 _p(g_ls), _p(g_quat))
+	return g_ls, g_quat
 
 
 def sh_basis(d, deg):

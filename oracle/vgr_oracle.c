@@ -13,6 +13,7 @@
  *   density       csrc/vgf.cu:98-119,152-177
  *   color         csrc/vgf.cu:202-282
  *   conic         csrc/vgf.cu:340-380
+ *   density, color and conic backward   csrc/vgf.cu:121-148,179-198,284-333,382-424
  * Arithmetic contract shared with the HIP kernels: fp32, every expression evaluated left to right as
  * written, no contraction into FMA (-ffp-contract=off), IEEE division and sqrt, fminf/fmaxf. Transcendentals
  * (expf) are libm's; the kernels call the device exp, so values agree to a few ulps, not bitwise.
@@ -678,6 +679,174 @@ void oracle_conic(const float* log_scale, const float* quat, int64_t n, float fl
             A[6 * i + e] = R[3 * x] * R[3 * y] * iv[0] + R[3 * x + 1] * R[3 * y + 1] * iv[1] +
                            R[3 * x + 2] * R[3 * y + 2] * iv[2];
         }
+    }
+}
+
+/* ============================================================================ vgf backward operators */
+
+/* Gaussian i seen from x: offset v = x - p_i, normalised quaternion qn (and the norm it was divided by), rotation
+ * R (row-major, columns = the Gaussian's axes), y = R^T v, inverse variances is2 and m = sum_k y_k^2 is2_k;
+ * vgf.cu:87-119 (gauss_local). */
+typedef struct {
+    float v[3], y[3], is2[3], qn[4], qnorm, R[9], m;
+} GFrame;
+
+static void gauss_frame(const float* points, const float* log_scale, const float* quat, int i, float x, float y,
+                        float z, GFrame* L) {
+    const int64_t i3 = 3 * (int64_t)i;
+    L->v[0] = x - points[i3];
+    L->v[1] = y - points[i3 + 1];
+    L->v[2] = z - points[i3 + 2];
+    const float* q = quat + 4 * (int64_t)i;
+    L->qnorm = fmaxf(sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]), 1e-12f);
+    for (int k = 0; k < 4; ++k) L->qn[k] = q[k] / L->qnorm;
+    const float w = L->qn[0], a = L->qn[1], b = L->qn[2], c = L->qn[3];
+    float* R = L->R;
+    R[0] = 1.f - 2.f * (b * b + c * c); R[1] = 2.f * (a * b - w * c); R[2] = 2.f * (a * c + w * b);
+    R[3] = 2.f * (a * b + w * c); R[4] = 1.f - 2.f * (a * a + c * c); R[5] = 2.f * (b * c - w * a);
+    R[6] = 2.f * (a * c - w * b); R[7] = 2.f * (b * c + w * a); R[8] = 1.f - 2.f * (a * a + b * b);
+    L->m = 0.f;
+    for (int k = 0; k < 3; ++k) {
+        L->y[k] = R[k] * L->v[0] + R[3 + k] * L->v[1] + R[6 + k] * L->v[2];
+        const float s = expf(fminf(fmaxf(log_scale[i3 + k], -20.f), 20.f));
+        L->is2[k] = 1.f / (s * s);
+        L->m += L->y[k] * L->y[k] * L->is2[k];
+    }
+}
+
+/* dL/dquat of a unit-quaternion rotation from dL/dR (row-major), through the normalisation q / |q|: the product
+ * rule on R(qn) above, then the tangent projection (dq - (dq . qn) qn) / |q|; vgf.cu:132-147 and :412-423. */
+static void quat_grad(const float qn[4], float qnorm, const float dR[9], float out[4]) {
+    const float w = qn[0], x = qn[1], y = qn[2], z = qn[3];
+    float dq[4];
+    dq[0] = 2.f * (-z * dR[1] + y * dR[2] + z * dR[3] - x * dR[5] - y * dR[6] + x * dR[7]);
+    dq[1] = 2.f * (y * dR[1] + z * dR[2] + y * dR[3] - 2.f * x * dR[4] - w * dR[5] + z * dR[6] + w * dR[7] -
+                   2.f * x * dR[8]);
+    dq[2] = 2.f * (-2.f * y * dR[0] + x * dR[1] + w * dR[2] + x * dR[3] + z * dR[5] - w * dR[6] + z * dR[7] -
+                   2.f * y * dR[8]);
+    dq[3] = 2.f * (-2.f * z * dR[0] - w * dR[1] + x * dR[2] + w * dR[3] - 2.f * z * dR[4] + y * dR[5] + x * dR[6] +
+                   y * dR[7]);
+    const float proj = dq[0] * w + dq[1] * x + dq[2] * y + dq[3] * z;
+    for (int k = 0; k < 4; ++k) out[k] = (dq[k] - proj * qn[k]) / qnorm;
+}
+
+/* Adds dL/dlog_scale and dL/dquat of Gaussian i given gm = dL/dm; vgf.cu:121-148 (scatter_gauss_grad). With
+ * m = sum_k y_k^2 / s_k^2: dm/dlog_s_k = -2 y_k^2 is2_k, dm/dy_k = 2 y_k is2_k, and dy_b/dR_ab = v_a. */
+static void gauss_grad(const GFrame* L, float gm, int i, float* g_ls, float* g_quat) {
+    float yk[3], dR[9], gq[4];
+    for (int k = 0; k < 3; ++k) {
+        yk[k] = 2.f * gm * L->y[k] * L->is2[k];
+        g_ls[3 * (int64_t)i + k] += -2.f * gm * L->y[k] * L->y[k] * L->is2[k];
+    }
+    for (int a = 0; a < 3; ++a)
+        for (int b = 0; b < 3; ++b) dR[3 * a + b] = L->v[a] * yk[b];
+    quat_grad(L->qn, L->qnorm, dR, gq);
+    for (int k = 0; k < 4; ++k) g_quat[4 * (int64_t)i + k] += gq[k];
+}
+
+/* Gradients of oracle_density (scale_mult 1) for dL/dsigma = grad_sigma, accumulated into g_raw (N), g_ls (N, 3),
+ * g_quat (N, 4) in sample order; terms with rho_k G_k |dL/dsigma| <= 1e-12 are skipped; vgf.cu:179-198. */
+void oracle_density_backward(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                             const float* log_scale, const float* quat, const float* x, const int32_t* site, int64_t m,
+                             const float* grad_sigma, float* g_raw, float* g_ls, float* g_quat) {
+    for (int64_t t = 0; t < m; ++t) {
+        const float gs = grad_sigma[t];
+        if (gs == 0.f) continue;
+        const int i = site[t];
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            GFrame L;
+            gauss_frame(points, log_scale, quat, k, x[3 * t], x[3 * t + 1], x[3 * t + 2], &L);
+            const float c = expf(fminf(raw[k], 30.f) - 0.5f * L.m);
+            if (c * fabsf(gs) > 1e-12f) {
+                g_raw[k] += gs * c;
+                gauss_grad(&L, -0.5f * gs * c, k, g_ls, g_quat);
+            }
+        }
+    }
+}
+
+/* Gradients of oracle_color for dL/drgb = grad_rgb given the forward rgb, accumulated into g_ls, g_quat and g_sh
+ * (N, 16, 3) in sample order; vgf.cu:284-333. With a_k the normalised weights and C = sum a_k c_k:
+ * dL/dc_k = a_k dL/dC (where SH_k + 1/2 > 0), dL/dm_k = -a_k / 2 (<dL/dC, c_k> - <dL/dC, C>); weights below 1e-7
+ * get no gradient. */
+void oracle_color_backward(const float* points, const int32_t* offsets, const int32_t* adj, const float* log_scale,
+                           const float* quat, const float* sh, int sh_deg, const float* x, const float* dirs,
+                           const int32_t* site, int64_t m, const float* rgb, const float* grad_rgb, float* g_ls,
+                           float* g_quat, float* g_sh) {
+    for (int64_t t = 0; t < m; ++t) {
+        const float gr = grad_rgb[3 * t], gg = grad_rgb[3 * t + 1], gb = grad_rgb[3 * t + 2];
+        if (gr == 0.f && gg == 0.f && gb == 0.f) continue;
+        const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
+        const int i = site[t];
+        float mmin = K_INF, A = 0.f;
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            mmin = fminf(mmin, gauss_m(points, log_scale, quat, k, qx, qy, qz, 1.f));
+        }
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            A += expf(-0.5f * (gauss_m(points, log_scale, quat, k, qx, qy, qz, 1.f) - mmin));
+        }
+        const float inv_a = 1.f / A;
+        const float gCC = gr * rgb[3 * t] + gg * rgb[3 * t + 1] + gb * rgb[3 * t + 2];
+        float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
+        const float inv = 1.f / sqrtf(fmaxf(dx * dx + dy * dy + dz * dz, 1e-20f));
+        dx *= inv; dy *= inv; dz *= inv;
+        float b[16];
+        sh_basis(dx, dy, dz, sh_deg, b);
+        const int nb = (sh_deg + 1) * (sh_deg + 1);
+        for (int e = offsets[i] - 1; e < offsets[i + 1]; ++e) {
+            const int k = e < offsets[i] ? i : adj[e];
+            GFrame L;
+            gauss_frame(points, log_scale, quat, k, qx, qy, qz, &L);
+            const float a = expf(-0.5f * (L.m - mmin)) * inv_a;
+            if (a < 1e-7f) continue;
+            float c[3];
+            sh_eval(sh, k, b, nb, c);
+            const float dc[3] = {c[0] > 0.f ? a * gr : 0.f, c[1] > 0.f ? a * gg : 0.f, c[2] > 0.f ? a * gb : 0.f};
+            float* gs = g_sh + 48 * (int64_t)k;
+            for (int j = 0; j < nb; ++j)
+                for (int ch = 0; ch < 3; ++ch) gs[3 * j + ch] += b[j] * dc[ch];
+            const float ga = gr * fmaxf(c[0], 0.f) + gg * fmaxf(c[1], 0.f) + gb * fmaxf(c[2], 0.f);
+            const float gm = -0.5f * a * (ga - gCC);
+            if (gm != 0.f) gauss_grad(&L, gm, k, g_ls, g_quat);
+        }
+    }
+}
+
+/* Gradients of oracle_conic for dL/dA = gA (N, 6), written to g_ls (N, 3) and g_quat (N, 4); vgf.cu:382-424. The
+ * off-diagonal entries of A stand for both A_ab and A_ba, so dL/dA is the symmetric G with G_ab = gA_ab / 2 off the
+ * diagonal; with A = R diag(iv) R^T: dL/div_k = (R^T G R)_kk, div_k/dlog_s_k = -2 s_k^2 iv_k^2, dL/dR = 2 G R
+ * diag(iv). */
+void oracle_conic_backward(const float* log_scale, const float* quat, int64_t n, float floor2, const float* gA,
+                           float* g_ls, float* g_quat) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float* q = quat + 4 * i;
+        const float qnorm = fmaxf(sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]), 1e-12f);
+        float qn[4], R[9], iv[3], s2[3];
+        for (int k = 0; k < 4; ++k) qn[k] = q[k] / qnorm;
+        const float w = qn[0], a = qn[1], b = qn[2], c = qn[3];
+        R[0] = 1.f - 2.f * (b * b + c * c); R[1] = 2.f * (a * b - w * c); R[2] = 2.f * (a * c + w * b);
+        R[3] = 2.f * (a * b + w * c); R[4] = 1.f - 2.f * (a * a + c * c); R[5] = 2.f * (b * c - w * a);
+        R[6] = 2.f * (a * c - w * b); R[7] = 2.f * (b * c + w * a); R[8] = 1.f - 2.f * (a * a + b * b);
+        for (int k = 0; k < 3; ++k) {
+            s2[k] = expf(2.f * fminf(fmaxf(log_scale[3 * i + k], -20.f), 20.f));
+            iv[k] = 1.f / (s2[k] + floor2);
+        }
+        const float* g = gA + 6 * i;
+        const float G[9] = {g[0], 0.5f * g[1], 0.5f * g[2], 0.5f * g[1], g[3], 0.5f * g[4], 0.5f * g[2], 0.5f * g[4],
+                            g[5]};
+        float GR[9], dR[9];
+        for (int r = 0; r < 3; ++r)
+            for (int k = 0; k < 3; ++k) GR[3 * r + k] = G[3 * r] * R[k] + G[3 * r + 1] * R[3 + k] + G[3 * r + 2] * R[6 + k];
+        for (int k = 0; k < 3; ++k) {
+            const float g_iv = R[k] * GR[k] + R[3 + k] * GR[3 + k] + R[6 + k] * GR[6 + k];
+            g_ls[3 * i + k] = g_iv * (-2.f * s2[k] * iv[k] * iv[k]);
+        }
+        for (int r = 0; r < 3; ++r)
+            for (int k = 0; k < 3; ++k) dR[3 * r + k] = 2.f * GR[3 * r + k] * iv[k];
+        quat_grad(qn, qnorm, dR, g_quat + 4 * i);
     }
 }
 

@@ -31,6 +31,9 @@ SIGNATURES = {
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P, _I64, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
 	'vgr_field_work_size': [_I64],
+	'vgr_density_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P],
+	'vgr_color_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
+	'vgr_conic_backward': [_P, _P, _I64, _F64, _P, _P, _P, _P],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
@@ -39,7 +42,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 _lib = None
 
 

@@ -103,6 +103,59 @@ class _FieldExtension:
 			call('vgr_conic_forward', ptr(log_scale), ptr(quat), n, float(floor), ptr(A), stream_of(quat.device))
 		return A
 
+	@staticmethod
+	def density_backward(points, offsets, adj, raw, log_scale, quat, x, site, grad_sigma):
+		"""-> g_raw (N,), g_ls (N, 3), g_quat (N, 4) (vgf.cu:477-492)."""
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (log_scale, 'log_scale', torch.float32),
+						 (quat, 'quat', torch.float32), (x, 'x', torch.float32), (site, 'site', torch.int32),
+						 (grad_sigma, 'grad_sigma', torch.float32)):
+			_check(t, n, dt)
+		g_raw, g_ls, g_quat = torch.zeros_like(raw), torch.zeros_like(log_scale), torch.zeros_like(quat)
+		m = x.size(0)
+		if m == 0:
+			return g_raw, g_ls, g_quat
+		with torch.cuda.device(x.device):
+			call('vgr_density_backward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+				 ptr(raw), ptr(log_scale), ptr(quat), ptr(x), ptr(site), m, ptr(grad_sigma), ptr(g_raw), ptr(g_ls),
+				 ptr(g_quat), stream_of(x.device))
+		return g_raw, g_ls, g_quat
+
+	@staticmethod
+	def color_backward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site, rgb, grad_rgb):
+		"""-> g_ls (N, 3), g_quat (N, 4), g_sh (N, 16, 3) (vgf.cu:515-533)."""
+		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
+						 (quat, 'quat', torch.float32), (sh, 'sh', torch.float32), (x, 'x', torch.float32),
+						 (dirs, 'dirs', torch.float32), (site, 'site', torch.int32), (rgb, 'rgb', torch.float32),
+						 (grad_rgb, 'grad_rgb', torch.float32)):
+			_check(t, n, dt)
+		_require(sh.dim() == 3 and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+		g_ls, g_quat, g_sh = torch.zeros_like(log_scale), torch.zeros_like(quat), torch.zeros_like(sh)
+		m = x.size(0)
+		if m == 0:
+			return g_ls, g_quat, g_sh
+		with torch.cuda.device(x.device):
+			call('vgr_color_backward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+				 ptr(log_scale), ptr(quat), ptr(sh), int(sh_deg), ptr(x), ptr(dirs), ptr(site), m, ptr(rgb),
+				 ptr(grad_rgb), ptr(g_ls), ptr(g_quat), ptr(g_sh), stream_of(x.device))
+		return g_ls, g_quat, g_sh
+
+	@staticmethod
+	def conic_backward(log_scale, quat, floor, gA):
+		"""-> g_ls (n, 3), g_quat (n, 4) (vgf.cu:548-560)."""
+		for t, n, dt in ((log_scale, 'log_scale', torch.float32), (quat, 'quat', torch.float32),
+						 (gA, 'gA', torch.float32)):
+			_check(t, n, dt)
+		g_ls, g_quat = torch.empty_like(log_scale), torch.empty_like(quat)
+		n = quat.size(0)
+		if n == 0:
+			return g_ls, g_quat
+		with torch.cuda.device(quat.device):
+			call('vgr_conic_backward', ptr(log_scale), ptr(quat), n, float(floor), ptr(gA), ptr(g_ls), ptr(g_quat),
+				 stream_of(quat.device))
+		return g_ls, g_quat
+
 
 def _field_work(points, m, records):
 	"""Scratch for the per-site Gaussian records of density_forward / color_forward when the call is large enough
@@ -271,34 +324,55 @@ class Graph:
 		return site, steps
 
 
-class _ForwardOnly(torch.autograd.Function):
-	"""Wraps a forward result so that parameters requiring gradients keep a graph edge whose backward raises:
-	the training kernels are out of scope."""
+class _Density(torch.autograd.Function):
+	"""sigma with the backward of vgr_density_backward (ext.py:61-75)."""
 
 	@staticmethod
-	def forward(ctx, out, *params):
-		return out.clone()
+	def forward(ctx, raw, log_scale, quat, x, site, graph):
+		sigma = extension().density_forward(graph.points, graph.offsets, graph.adj, raw, log_scale, quat, x, site, 1.0)
+		ctx.save_for_backward(raw, log_scale, quat, x, site)
+		ctx.graph = graph
+		return sigma
 
 	@staticmethod
-	def backward(ctx, *grads):
-		raise RuntimeError('backward of the voronoi-gauss field is out of scope of this build (forward/inference only)')
-
-
-def _forward_only(out, params):
-	if torch.is_grad_enabled() and any(isinstance(p, torch.Tensor) and p.requires_grad for p in params):
-		return _ForwardOnly.apply(out, *params)
-	return out
+	def backward(ctx, grad_sigma):
+		raw, log_scale, quat, x, site = ctx.saved_tensors
+		g = ctx.graph
+		g_raw, g_ls, g_quat = extension().density_backward(g.points, g.offsets, g.adj, raw, log_scale, quat, x, site,
+														   grad_sigma.float().contiguous())
+		return g_raw, g_ls, g_quat, None, None, None
 
 
 def density(graph, raw, log_scale, quat, x, site, scale_mult=1.0):
 	"""sigma(x) = sum over the Voronoi neighborhood of site of exp(raw_k) G_k(x); scale_mult widens the
-	Gaussians (proposal passes). Reference: ext.py:78-87."""
+	Gaussians (proposal passes, no gradient). Reference: ext.py:78-87."""
 	x = x.detach().float().contiguous()
 	site = site.int().contiguous()
 	params = [p.contiguous() for p in (raw, log_scale, quat)]
-	out = extension().density_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params], x, site,
-									  float(scale_mult))
-	return out if scale_mult != 1.0 else _forward_only(out, params)
+	if scale_mult != 1.0 or not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
+		return extension().density_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params], x,
+										   site, float(scale_mult))
+	return _Density.apply(*params, x, site, graph)
+
+
+class _Color(torch.autograd.Function):
+	"""rgb with the backward of vgr_color_backward (ext.py:90-105)."""
+
+	@staticmethod
+	def forward(ctx, log_scale, quat, sh, x, dirs, site, graph, sh_deg):
+		rgb = extension().color_forward(graph.points, graph.offsets, graph.adj, log_scale, quat, sh, sh_deg, x, dirs,
+										site)
+		ctx.save_for_backward(log_scale, quat, sh, x, dirs, site, rgb)
+		ctx.graph, ctx.sh_deg = graph, sh_deg
+		return rgb
+
+	@staticmethod
+	def backward(ctx, grad_rgb):
+		log_scale, quat, sh, x, dirs, site, rgb = ctx.saved_tensors
+		g = ctx.graph
+		g_ls, g_quat, g_sh = extension().color_backward(g.points, g.offsets, g.adj, log_scale, quat, sh, ctx.sh_deg,
+														x, dirs, site, rgb, grad_rgb.float().contiguous())
+		return g_ls, g_quat, g_sh, None, None, None, None, None
 
 
 def color(graph, log_scale, quat, sh, x, dirs, site, sh_deg=3):
@@ -308,16 +382,31 @@ def color(graph, log_scale, quat, sh, x, dirs, site, sh_deg=3):
 	dirs = dirs.detach().float().contiguous()
 	site = site.int().contiguous()
 	params = [p.contiguous() for p in (log_scale, quat, sh)]
-	out = extension().color_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
-									int(sh_deg), x, dirs, site)
-	return _forward_only(out, params)
+	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
+		return extension().color_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
+										 int(sh_deg), x, dirs, site)
+	return _Color.apply(*params, x, dirs, site, graph, int(sh_deg))
+
+
+class _Conic(torch.autograd.Function):
+	"""Conics with the backward of vgr_conic_backward (ext.py:120-131)."""
+
+	@staticmethod
+	def forward(ctx, log_scale, quat, floor):
+		ctx.save_for_backward(log_scale, quat)
+		ctx.floor = floor
+		return extension().conic_forward(log_scale, quat, floor)
+
+	@staticmethod
+	def backward(ctx, gA):
+		log_scale, quat = ctx.saved_tensors
+		g_ls, g_quat = extension().conic_backward(log_scale, quat, ctx.floor, gA.float().contiguous())
+		return g_ls, g_quat, None
 
 
 def conic(log_scale, quat, floor=0.0):
 	"""(N, 6) inverse covariances (xx, xy, xz, yy, yz, zz) of R diag(s^2 + floor^2) R^T (ext.py:134-136)."""
-	params = [log_scale.contiguous(), quat.contiguous()]
-	out = extension().conic_forward(params[0].detach(), params[1].detach(), float(floor))
-	return _forward_only(out, params)
+	return _Conic.apply(log_scale.contiguous(), quat.contiguous(), float(floor))
 
 
 def conic_reference(log_scale, quat, floor=0.0):
@@ -331,6 +420,25 @@ def conic_reference(log_scale, quat, floor=0.0):
 	inv_var = 1.0 / (torch.exp(2 * log_scale.clamp(-20, 20)) + floor * floor)
 	A = (R * inv_var[:, None, :]) @ R.transpose(1, 2).contiguous()
 	return torch.stack([A[:, 0, 0], A[:, 0, 1], A[:, 0, 2], A[:, 1, 1], A[:, 1, 2], A[:, 2, 2]], -1).contiguous()
+
+
+class _ForwardOnly(torch.autograd.Function):
+	"""Wraps a forward result so that parameters requiring gradients keep a graph edge whose backward raises: the
+	march's backward (csrc/march.cu:264-345) is not part of this build."""
+
+	@staticmethod
+	def forward(ctx, out, *params):
+		return out.clone()
+
+	@staticmethod
+	def backward(ctx, *grads):
+		raise RuntimeError('backward of the uniform march is not part of this build (march.cu forward only)')
+
+
+def _forward_only(out, params):
+	if torch.is_grad_enabled() and any(isinstance(p, torch.Tensor) and p.requires_grad for p in params):
+		return _ForwardOnly.apply(out, *params)
+	return out
 
 
 def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg, t_thresh=1e-4, w_thresh=1e-4):
