@@ -12,6 +12,7 @@ Other rows of the path, each as one JSON line of the same form (not the headline
   --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
   --workload locate   start-cell location on config 5 (nearest site of 16,777,216 ray origins among 4M sites)
   --workload pack     pack_foam with Z-order renumbering on config 3 (the step before the kernel)
+  --workload grad     the backward of the field operators on the frame of --workload field
   --workload traverse the cell traversal alone (foam_infer stage 0) on config 3 in both layouts: one ray per lane
                       (foam_infer) against 16 lanes per ray testing a cell's faces in parallel
   --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
@@ -118,12 +119,14 @@ def main():
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
+	ap.add_argument('--batch', type=int, default=4096, help='grad workload: random rays per training step')
 	ap.add_argument('--lanes-per-ray', type=int, default=None, choices=[1, 2, 4, 8],
 					help='foam workload: ray layout (1: one ray per lane, 2 / 4 / 8: lanes per ray; default: the '
 						 'library default)')
 	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
-	ap.add_argument('--workload', default='foam', choices=['foam', 'march', 'locate', 'field', 'pack', 'traverse'],
+	ap.add_argument('--workload', default='foam',
+					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
 	args = ap.parse_args()
@@ -146,6 +149,8 @@ def main():
 		return bench_pack(args)
 	if args.workload == 'traverse':
 		return bench_traverse(args)
+	if args.workload == 'grad':
+		return bench_grad(args)
 	bench_foam(args)
 
 
@@ -715,6 +720,121 @@ def bench_field(args):
 		  'walk_steps_per_sample': round(float(steps.double().sum()) / m, 3)},
 		 {'bound': 'hbm', 'kernel': f'{top}_forward' if top != 'walk' else 'walk', 'achieved': round(gbs[top], 1),
 		  'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs[top] / HBM_PEAK_GBS, 4), 'traffic': None,
+		  'algorithmic_bytes_per_launch': nb[top]}, cpu)
+
+
+def bench_grad(args):
+	"""Backward of the NeRF-path field operators for one training step on config 3: --batch random rays (train.py's
+	default 4096, drawn uniformly over the pixels of the 4 cameras as scene.random_rays does, train.py:132) x 64
+	stratified samples: density_backward at every sample, color_backward at the samples of compositing weight
+	> 1e-4 (upstream gradients random normal, as the loss supplies them), conic_backward over all sites.
+	value = samples per second through density + colour backward. CPU baseline: the C oracle's backward on one
+	thread over a bounded sample.
+
+	Algorithmic bytes (cache-oblivious; E = mean self-inclusive neighbourhood, SHB = 192 B at SH degree 3):
+	  density  per sample 32 + 80 E       (x, site, dL/dsigma, offsets; per neighbour point 12 + adj 4 + raw 4 +
+	                                        log_scale 12 + quat 16, and the gradients raw 4 + log_scale 12 + quat 16)
+	  colour   per active sample 60 + E (3 x 44 + SHB + 28 + SHB)   (x, dir, site, rgb, dL/drgb, offsets; three
+	                                        sweeps of point, adj, log_scale, quat; SH read, gradients of log_scale,
+	                                        quat and SH written)
+	  conic    per site 76 (log_scale 12 + quat 16 + dL/dA 24 in, gradients 28 out)."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, render, scenes
+	from vgr.model import VoronoiGaussField
+	from vgr.sites import nearest_sites
+	dev = torch.device('cuda:0')
+	sc = scenes.make_scene(3, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	g = model.graph
+	rng = np.random.default_rng(0)
+	cams = rng.integers(0, len(sc.cameras), args.batch)
+	o_l, d_l, e_l = [], [], []
+	for c in range(len(sc.cameras)):
+		n_c = int((cams == c).sum())
+		o_c, d_c = sc.cameras[c].rays()
+		pick = rng.choice(len(o_c), n_c, replace=False)
+		o_l.append(o_c[pick]), d_l.append(d_c[pick]), e_l.append(np.repeat(sc.cameras[c].eye[None], n_c, 0))
+	o = torch.from_numpy(np.concatenate(o_l)).to(dev)
+	d = torch.from_numpy(np.concatenate(d_l)).to(dev)
+	start = nearest_sites(g.points, torch.from_numpy(np.concatenate(e_l).astype(np.float32)).to(dev))
+	B, S = len(o), 64
+	bounds = render.ray_bounds(o, d, 0.02, sc.far_radius)
+	s_grid = (torch.linspace(0, 1, S + 1, device=dev)[:-1] + 0.5 / S).expand(B, S).contiguous()
+	t = render.s_to_t(s_grid, *bounds).contiguous()
+	fx = ext.extension()
+	sh = model.sh().contiguous()
+	site, _ = fx.walk(g.points, g.offsets, g.adj, o, d, t, start.contiguous())
+	x = (o[:, None] + d[:, None] * t[..., None]).reshape(-1, 3).contiguous()
+	site_f = site.reshape(-1).contiguous()
+	sigma = fx.density_forward(g.points, g.offsets, g.adj, model.raw, model.d_log_scale, model.d_quat, x, site_f, 1.0)
+	w, _ = render.composite(sigma.view(B, S), t, bounds[2])
+	active = (w.reshape(-1) > 1e-4).nonzero().squeeze(1)
+	xa = x[active].contiguous()
+	da = d[:, None].expand(B, S, 3).reshape(-1, 3)[active].contiguous()
+	sa = site_f[active].contiguous()
+	rgb = fx.color_forward(g.points, g.offsets, g.adj, model.c_log_scale, model.c_quat, sh, sc.sh_deg, xa, da, sa)
+	gen = torch.Generator(device=dev).manual_seed(0)
+	m, ma = B * S, len(active)
+	g_sigma = torch.randn(m, device=dev, generator=gen)
+	g_rgb = torch.randn(ma, 3, device=dev, generator=gen)
+	gA = torch.randn(sc.n_sites, 6, device=dev, generator=gen)
+	stream = torch.cuda.current_stream(dev)
+	log(f'config 3 training batch: {B} random rays x {S} samples, {ma} active, {sc.n_sites} sites')
+	dens_ms, dgrad, _ = time_steps(lambda: fx.density_backward(g.points, g.offsets, g.adj, model.raw,
+															   model.d_log_scale, model.d_quat, x, site_f, g_sigma),
+								   args.steps, args.warmup, stream)
+	col_ms, cgrad, _ = time_steps(lambda: fx.color_backward(g.points, g.offsets, g.adj, model.c_log_scale,
+															model.c_quat, sh, sc.sh_deg, xa, da, sa, rgb, g_rgb),
+								  args.steps, args.warmup, stream)
+	con_ms, _, _ = time_steps(lambda: fx.conic_backward(model.d_log_scale, model.d_quat, 0.0, gA), args.steps,
+							  args.warmup, stream)
+	ms = {k: float(np.mean(v)) for k, v in (('density', dens_ms), ('color', col_ms), ('conic', con_ms))}
+	E = 1.0 + len(sc.adj) / sc.n_sites
+	SHB = 12 * (sc.sh_deg + 1) ** 2
+	nb = {'density': m * (32 + 80 * E), 'color': ma * (60 + E * (3 * 44 + 2 * SHB + 28)), 'conic': sc.n_sites * 76.0}
+	gbs = {k: nb[k] / (ms[k] * 1e-3) / 1e9 for k in ms}
+	log('  '.join(f'{k} backward {ms[k]:.3f} ms ({gbs[k]:.0f} GB/s)' for k in ms))
+	top = max(('density', 'color'), key=lambda k: ms[k])
+	cpu = None
+	if args.cpu_seconds > 0:
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		host = {k: v.detach().cpu().numpy() for k, v in (('p', g.points), ('off', g.offsets), ('adj', g.adj),
+														  ('raw', model.raw), ('dls', model.d_log_scale),
+														  ('dq', model.d_quat), ('cls', model.c_log_scale),
+														  ('cq', model.c_quat), ('sh', sh))}
+		# bounded samples; the oracle's gradients are sums over the sampled subset only, so they are timed here
+		# and checked against the GPU in tests/test_gpu_field_grad.py
+		ks = max(1, int(m / (4000.0 * max(args.cpu_seconds, 1e-3))))
+		samp = np.arange(0, m, ks)
+		t1 = time.perf_counter()
+		oracle.density_backward(host['p'], host['off'], host['adj'], host['raw'], host['dls'], host['dq'],
+								x.cpu().numpy()[samp], site_f.cpu().numpy()[samp], g_sigma.cpu().numpy()[samp])
+		t_dens = time.perf_counter() - t1
+		ca = np.arange(0, ma, max(1, int(ma / (700.0 * max(args.cpu_seconds, 1e-3)))))
+		t1 = time.perf_counter()
+		oracle.color_backward(host['p'], host['off'], host['adj'], host['cls'], host['cq'], host['sh'], sc.sh_deg,
+							  xa.cpu().numpy()[ca], da.cpu().numpy()[ca], sa.cpu().numpy()[ca], rgb.cpu().numpy()[ca],
+							  g_rgb.cpu().numpy()[ca])
+		t_col = time.perf_counter() - t1
+		t_frame = t_dens * m / len(samp) + t_col * ma / len(ca)
+		log(f'cpu oracle (1 thread): density backward {len(samp)} samples in {t_dens:.2f} s, colour backward '
+			f'{len(ca)} samples in {t_col:.2f} s; {t_frame:.1f} s per batch')
+		cpu = {'value': round(m / t_frame / 1e6, 4), 'unit': 'Msamples/s', 'cores': 1, 'kind': 'port',
+			   'sample': f'density backward: every {ks}th sample ({len(samp)}); colour backward: {len(ca)} active '
+						 f'samples; each rate scaled to the whole batch'}
+	total = ms['density'] + ms['color']
+	emit(f'Msamples/s NeRF-path field backward density + colour (config 3, training batch of {B} random rays x {S} '
+		 f'samples) on 1 MI355X', m / total / 1e3, 'Msamples/s', args, total,
+		 {'workload': f'config 3: {B} random rays of the 4 cameras x {S} stratified samples ({m}); colour backward '
+					  f'at the {ma} samples of weight > 1e-4; conic backward over {sc.n_sites} sites', 'samples': m,
+		  'active_samples': ma, 'ms': {k: round(v, 3) for k, v in ms.items()},
+		  'GBps': {k: round(v, 1) for k, v in gbs.items()},
+		  'grad_norms': {'raw': float(dgrad[0].norm()), 'sh': float(cgrad[2].norm())}},
+		 {'bound': 'hbm', 'kernel': f'{top}_backward', 'achieved': round(gbs[top], 1), 'peak': HBM_PEAK_GBS,
+		  'unit': 'GB/s', 'frac': round(gbs[top] / HBM_PEAK_GBS, 4), 'traffic': None,
 		  'algorithmic_bytes_per_launch': nb[top]}, cpu)
 
 
