@@ -216,7 +216,8 @@ def bench_foam(args):
 	launch_ms = [a.elapsed_time(b) for a, b in ev]
 	ms = float(np.mean(launch_ms))
 	rgb, T, depth, stats = out
-	log(f'{args.steps} steps: mean {ms:.3f} ms, median {np.median(launch_ms):.3f} ms, wall {wall * 1e3 / args.steps:.3f} '
+	log(f'{args.steps} steps: mean {ms:.3f} ms, median {np.median(launch_ms):.3f} ms, '
+		f'wall {wall * 1e3 / args.steps:.3f} '
 		f'ms/step')
 	sh_bytes = (6 if args.sh_half else 12) * (sc.sh_deg + 1) ** 2 if args.colors != 'baked' else 0
 	if fast:  # SH bytes per SH evaluation (an upper bound of the distinct sites); quality against the exact image
@@ -386,7 +387,8 @@ def bench_locate(args):
 	emit('Mqueries/s nearest-site start location (config 5: 4M sites, 16.7M ray origins) on 1 MI355X', B / ms / 1e3,
 		 'Mqueries/s', args, ms,
 		 {'workload': f'config 5 start cells: nearest of {N} sites (seeded uniform draw) for each of {B} ray '
-					  f'origins', 'sites': N, 'queries': B, 'grid_res': g.res, 'grid_build_ms': round(float(np.mean(build_ms)), 3)},
+					  f'origins', 'sites': N, 'queries': B, 'grid_res': g.res,
+		  'grid_build_ms': round(float(np.mean(build_ms)), 3)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
 
@@ -429,7 +431,8 @@ def bench_march(args):
 	E = 1.0 + len(sc.adj) / sc.n_sites  # mean self-inclusive neighbourhood
 	SHB = 12 * (sc.sh_deg + 1) ** 2
 	# per sample: walk steps (8 + 16 E) each, density (8 + E (16 + 28)), colour when active E (24 + SHB); rays 56 B
-	abytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) + st[:, 1].sum() * E * (24 + SHB))
+	abytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
+				   st[:, 1].sum() * E * (24 + SHB))
 	achieved = abytes / (ms * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
@@ -470,7 +473,8 @@ def bench_march(args):
 		 args, ms,
 		 {'workload': f'config 5 march: {sc.n_sites} sites, {B} rays, dt 1/512 inside the unit ball + {n_bg} '
 					  f'disparity steps, starts from the GPU grid', 'sites': sc.n_sites, 'rays': B,
-		  'samples_per_ray': round(float(st[:, 0].mean()), 2), 'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
+		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
+		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
@@ -638,7 +642,8 @@ def bench_field(args):
 	o_np, d_np = cam.rays()
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	from vgr.sites import nearest_sites
-	start = nearest_sites(g.points, torch.tensor(cam.eye, dtype=torch.float32, device=dev)[None]).expand(len(o)).contiguous()
+	eye = torch.tensor(cam.eye, dtype=torch.float32, device=dev)[None]
+	start = nearest_sites(g.points, eye).expand(len(o)).contiguous()
 	B, S = len(o), 64
 	bounds = render.ray_bounds(o, d, 0.02, sc.far_radius)
 	s_grid = (torch.linspace(0, 1, S + 1, device=dev)[:-1] + 0.5 / S).expand(B, S).contiguous()

@@ -839,7 +839,8 @@ void oracle_conic_backward(const float* log_scale, const float* quat, int64_t n,
                             g[5]};
         float GR[9], dR[9];
         for (int r = 0; r < 3; ++r)
-            for (int k = 0; k < 3; ++k) GR[3 * r + k] = G[3 * r] * R[k] + G[3 * r + 1] * R[3 + k] + G[3 * r + 2] * R[6 + k];
+            for (int k = 0; k < 3; ++k)
+                GR[3 * r + k] = G[3 * r] * R[k] + G[3 * r + 1] * R[3 + k] + G[3 * r + 2] * R[6 + k];
         for (int k = 0; k < 3; ++k) {
             const float g_iv = R[k] * GR[k] + R[3 + k] * GR[3 + k] + R[6 + k] * GR[6 + k];
             g_ls[3 * i + k] = g_iv * (-2.f * s2[k] * iv[k] * iv[k]);

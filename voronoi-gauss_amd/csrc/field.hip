@@ -241,9 +241,9 @@ __global__ void __launch_bounds__(kBlock)
 
 template <int DEG>
 __global__ void __launch_bounds__(kBlock)
-    color_forward_packed_kernel(Graph g, const float4* __restrict__ rec, const float4* __restrict__ sh, const float* __restrict__ x,
-                         const float* __restrict__ dirs, const int* __restrict__ site, int64_t m,
-                         float* __restrict__ rgb) {
+    color_forward_packed_kernel(Graph g, const float4* __restrict__ rec, const float4* __restrict__ sh,
+                                const float* __restrict__ x, const float* __restrict__ dirs,
+                                const int* __restrict__ site, int64_t m, float* __restrict__ rgb) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (t >= m) return;
     const int i = site[t];
@@ -404,7 +404,9 @@ extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int
         case 0: hipLaunchKernelGGL(color_forward_kernel<0>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
         case 1: hipLaunchKernelGGL(color_forward_kernel<1>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
         case 2: hipLaunchKernelGGL(color_forward_kernel<2>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
-        default: hipLaunchKernelGGL(color_forward_kernel<3>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
+        default:
+            hipLaunchKernelGGL(color_forward_kernel<3>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb);
+            break;
     }
     return launch_status("color_forward_kernel");
 }

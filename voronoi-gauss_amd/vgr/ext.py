@@ -107,9 +107,9 @@ class _FieldExtension:
 	def density_backward(points, offsets, adj, raw, log_scale, quat, x, site, grad_sigma):
 		"""-> g_raw (N,), g_ls (N, 3), g_quat (N, 4) (vgf.cu:477-492)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
-						 (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (log_scale, 'log_scale', torch.float32),
-						 (quat, 'quat', torch.float32), (x, 'x', torch.float32), (site, 'site', torch.int32),
-						 (grad_sigma, 'grad_sigma', torch.float32)):
+						 (adj, 'adj', torch.int32), (raw, 'raw', torch.float32),
+						 (log_scale, 'log_scale', torch.float32), (quat, 'quat', torch.float32), (x, 'x', torch.float32),
+						 (site, 'site', torch.int32), (grad_sigma, 'grad_sigma', torch.float32)):
 			_check(t, n, dt)
 		g_raw, g_ls, g_quat = torch.zeros_like(raw), torch.zeros_like(log_scale), torch.zeros_like(quat)
 		m = x.size(0)
