@@ -169,23 +169,31 @@ int vgr_conic_forward(const float* log_scale, const float* quat, int64_t n, doub
  * Gradients of vgr_density_forward (scale_mult 1) for dL/dsigma = grad_sigma (m). Replaces density_backward() of
  * csrc/vgf.cu:477-492 (export :568), bound by ext._Density.backward (ext.py:69-75). Accumulated into g_raw (N),
  * g_ls (N, 3) and g_quat (N, 4), which the caller zeroes; terms with rho_k G_k |dL/dsigma| <= 1e-12 are skipped.
- * The per-site sums use fp32 atomics, so their last bits vary from run to run.
+ * work: NULL (the per-site sums are scattered with fp32 atomics, one sample per lane), or device scratch of
+ * vgr_density_backward_work_size(N, m) bytes, 256-byte aligned, with which the samples are counting-sorted by site
+ * and each site gathers its gradients from the samples of its own and its neighbours' cells (no atomics on the
+ * gradients). Either way the summation order, and so the last bits, vary from run to run. Calls sharing a
+ * workspace must be ordered on one stream.
  */
+int64_t vgr_density_backward_work_size(int64_t n_sites, int64_t m);
 int vgr_density_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                          int64_t n_adj, const float* raw, const float* log_scale, const float* quat, const float* x,
                          const int32_t* site, int64_t m, const float* grad_sigma, float* g_raw, float* g_ls,
-                         float* g_quat, void* stream);
+                         float* g_quat, void* work, int64_t work_bytes, void* stream);
 
 /*
  * Gradients of vgr_color_forward for dL/drgb = grad_rgb (m, 3), given its output rgb (m, 3). Replaces
  * color_backward() of csrc/vgf.cu:515-533 (export :570), bound by ext._Color.backward (ext.py:99-105).
  * Accumulated into g_ls (N, 3), g_quat (N, 4) and g_sh (N, 16, 3), which the caller zeroes; normalised weights below
- * 1e-7 get no gradient. fp32 atomics, as vgr_density_backward.
+ * 1e-7 get no gradient. work: NULL (fp32 atomics) or the gather's scratch, as vgr_density_backward, of
+ * vgr_color_backward_work_size(N, m) bytes.
  */
+int64_t vgr_color_backward_work_size(int64_t n_sites, int64_t m);
 int vgr_color_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                        int64_t n_adj, const float* log_scale, const float* quat, const float* sh, int64_t sh_deg,
                        const float* x, const float* dirs, const int32_t* site, int64_t m, const float* rgb,
-                       const float* grad_rgb, float* g_ls, float* g_quat, float* g_sh, void* stream);
+                       const float* grad_rgb, float* g_ls, float* g_quat, float* g_sh, void* work,
+                       int64_t work_bytes, void* stream);
 
 /*
  * Gradients of vgr_conic_forward for dL/dA = gA (n, 6) (off-diagonal entries standing for both A_ab and A_ba),

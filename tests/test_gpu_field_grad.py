@@ -1,8 +1,9 @@
 """GPU parity of the backward field operators (vgr_density_backward, vgr_color_backward, vgr_conic_backward through
 the C ABI): against the C oracle's sequential sums on identical inputs, and end to end through ext.density /
 ext.color / ext.conic autograd against float64 PyTorch autograd of the dense fields, the check of the reference's
-test_grad.py:88-114. The kernels scatter with fp32 atomics, so sums agree to rounding, not bitwise: the bar is a
-relative error (vector norm) of 1e-5 against the oracle and 1e-4 against float64."""
+test_grad.py:88-114. The kernels scatter with fp32 atomics (and gather dL/dsh per site in another order), so sums
+agree to rounding, not bitwise: the bar is a relative error (vector norm) of 1e-5 against the oracle and 1e-4 against
+float64."""
 
 import numpy as np
 import pytest
@@ -30,12 +31,14 @@ def case(gpu):
 	return f, x, site, dirs, rng, T, graph
 
 
-def test_density_backward_matches_oracle(case):
+@pytest.mark.parametrize('gather', [True, False])
+def test_density_backward_matches_oracle(case, gather):
+	"""Gradients gathered per site (counting sort of the samples by site) and scattered with atomics."""
 	f, x, site, _, rng, T, graph = case
 	g_sigma = rng.normal(size=len(x)).astype(np.float32)
 	g_sigma[10:20] = 0
 	out = ext.extension().density_backward(graph.points, graph.offsets, graph.adj, T(f.raw), T(f.d_log_scale),
-										   T(f.d_quat), T(x), T(site), T(g_sigma))
+										   T(f.d_quat), T(x), T(site), T(g_sigma), gather=gather)
 	ok = site >= 0
 	ref = oracle.density_backward(f.points, f.offsets, f.adj, f.raw, f.d_log_scale, f.d_quat, x[ok], site[ok],
 								  g_sigma[ok])
@@ -43,8 +46,11 @@ def test_density_backward_matches_oracle(case):
 		assert rel(a.cpu().numpy(), r) < 1e-5
 
 
+@pytest.mark.parametrize('gather', [True, False])
 @pytest.mark.parametrize('sh_deg', [3, 2, 0])
-def test_color_backward_matches_oracle(case, sh_deg):
+def test_color_backward_matches_oracle(case, sh_deg, gather):
+	"""Gradients gathered per site through the workspace (counting sort of the samples by site) and scattered with
+	atomics: both against the oracle."""
 	f, x, site, dirs, rng, T, graph = case
 	sh = f.sh.copy()
 	sh[:, (sh_deg + 1) ** 2:] = 0
@@ -52,8 +58,9 @@ def test_color_backward_matches_oracle(case, sh_deg):
 	fx = ext.extension()
 	rgb = fx.color_forward(graph.points, graph.offsets, graph.adj, T(f.c_log_scale), T(f.c_quat), T(sh), sh_deg, T(x),
 						   T(dirs), T(site))
+	g_rgb[20:40] = 0  # samples without an upstream gradient take no record slot
 	out = fx.color_backward(graph.points, graph.offsets, graph.adj, T(f.c_log_scale), T(f.c_quat), T(sh), sh_deg,
-							T(x), T(dirs), T(site), rgb, T(g_rgb))
+							T(x), T(dirs), T(site), rgb, T(g_rgb), gather=gather)
 	ok = site >= 0
 	ref = oracle.color_backward(f.points, f.offsets, f.adj, f.c_log_scale, f.c_quat, sh, sh_deg, x[ok], dirs[ok],
 								site[ok], rgb.cpu().numpy()[ok], g_rgb[ok])

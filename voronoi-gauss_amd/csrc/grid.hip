@@ -8,14 +8,12 @@
 // where two sites are at exactly the same float64 distance.
 #include "vgr_abi.h"
 #include "vgr_device.h"
+#include "vgr_scan.h"
 
 namespace vgr {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kScanThreads = 1024;                   // threads of a scan block
-constexpr int kScanItems = 4;                        // counts per scan thread
-constexpr int kScanTile = kScanThreads * kScanItems;  // counts per scan block
 constexpr int64_t kMaxCells = int64_t(kScanTile) * kScanTile;
 
 struct Geom {
@@ -43,77 +41,6 @@ __global__ void __launch_bounds__(kBlock) grid_count(const float* __restrict__ p
     const int c = (cz * g.res[1] + cy) * g.res[0] + cx;
     cell_of[i] = c;
     atomicAdd(count + c, 1);
-}
-
-// Exclusive scan of one tile of kScanTile counts within the tile; the tile total goes to tile_sum.
-__global__ void __launch_bounds__(kScanThreads) scan_tiles(const int* __restrict__ count, int64_t n_cells,
-                                                           int* __restrict__ start, int* __restrict__ tile_sum) {
-    __shared__ int part[kScanThreads];
-    const int64_t base = int64_t(blockIdx.x) * kScanTile + int64_t(threadIdx.x) * kScanItems;
-    int v[kScanItems], sum = 0;
-#pragma unroll
-    for (int u = 0; u < kScanItems; ++u) {
-        v[u] = base + u < n_cells ? count[base + u] : 0;
-        sum += v[u];
-    }
-    part[threadIdx.x] = sum;
-    __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive scan of the thread sums
-        const int add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-        __syncthreads();
-        part[threadIdx.x] += add;
-        __syncthreads();
-    }
-    int run = part[threadIdx.x] - sum;
-#pragma unroll
-    for (int u = 0; u < kScanItems; ++u) {
-        if (base + u < n_cells) start[base + u] = run;
-        run += v[u];
-    }
-    if (threadIdx.x == kScanThreads - 1) tile_sum[blockIdx.x] = part[threadIdx.x];
-}
-
-// Exclusive scan of the tile totals (at most kScanTile of them) in place, by one block; the grand total goes to
-// tile_sum[n_tiles].
-__global__ void __launch_bounds__(kScanThreads) scan_tile_sums(int* __restrict__ tile_sum, int n_tiles) {
-    __shared__ int part[kScanThreads];
-    const int base = threadIdx.x * kScanItems;
-    int v[kScanItems], sum = 0;
-#pragma unroll
-    for (int u = 0; u < kScanItems; ++u) {
-        v[u] = base + u < n_tiles ? tile_sum[base + u] : 0;
-        sum += v[u];
-    }
-    part[threadIdx.x] = sum;
-    __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {
-        const int add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-        __syncthreads();
-        part[threadIdx.x] += add;
-        __syncthreads();
-    }
-    int run = part[threadIdx.x] - sum;
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kScanItems; ++u) {
-        if (base + u < n_tiles) tile_sum[base + u] = run;
-        run += v[u];
-    }
-    if (threadIdx.x == kScanThreads - 1) tile_sum[n_tiles] = part[threadIdx.x];
-}
-
-// Adds the tile offsets: start becomes the global exclusive scan (start[n_cells] = total), and the count array is
-// overwritten with it, as the fill cursor.
-__global__ void __launch_bounds__(kBlock) scan_add(int* __restrict__ start, int* __restrict__ cursor, int64_t n_cells,
-                                                   const int* __restrict__ tile_sum, int n_tiles) {
-    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-    if (i < n_cells) {
-        const int s = start[i] + tile_sum[i / kScanTile];
-        start[i] = s;
-        cursor[i] = s;
-    } else if (i == n_cells) {
-        start[i] = tile_sum[n_tiles];
-    }
 }
 
 // Scatter: every site takes the next slot of its cell (the order within a cell is arbitrary; queries do not
@@ -247,20 +174,14 @@ extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stri
     int* cell_of = work;
     int* count = work + n_sites;
     int* tile_sum = count + n_cells;
-    const int n_tiles = static_cast<int>((n_cells + kScanTile - 1) / kScanTile);
     if (hipMemsetAsync(count, 0, sizeof(int) * n_cells, s) != hipSuccess) return launch_status("grid_build memset");
     if (n_sites > 0) {
         hipLaunchKernelGGL(grid_count, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, s, points, int(stride),
                            n_sites, g, cell_of, count);
         if (int rc = launch_status("grid_count")) return rc;
     }
-    hipLaunchKernelGGL(scan_tiles, dim3(n_tiles), dim3(kScanThreads), 0, s, count, n_cells, cell_start, tile_sum);
-    if (int rc = launch_status("scan_tiles")) return rc;
-    hipLaunchKernelGGL(scan_tile_sums, dim3(1), dim3(kScanThreads), 0, s, tile_sum, n_tiles);
-    if (int rc = launch_status("scan_tile_sums")) return rc;
-    hipLaunchKernelGGL(scan_add, dim3(grid_for(n_cells + 1, kBlock)), dim3(kBlock), 0, s, cell_start, count, n_cells,
-                       tile_sum, n_tiles);
-    if (int rc = launch_status("scan_add")) return rc;
+    exclusive_scan(count, n_cells, cell_start, count, tile_sum, s);  // count becomes the fill cursor
+    if (int rc = launch_status("grid_build scan")) return rc;
     if (n_sites > 0) {
         hipLaunchKernelGGL(grid_fill, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, s, n_sites, cell_of, count,
                            cell_sites);

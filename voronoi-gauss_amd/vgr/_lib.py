@@ -31,8 +31,11 @@ SIGNATURES = {
 	'vgr_density_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _P, _P, _I64, _P],
 	'vgr_color_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
 	'vgr_field_work_size': [_I64],
-	'vgr_density_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P],
-	'vgr_color_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
+	'vgr_density_backward_work_size': [_I64, _I64],
+	'vgr_density_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P],
+	'vgr_color_backward_work_size': [_I64, _I64],
+	'vgr_color_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64,
+						   _P],
 	'vgr_conic_backward': [_P, _P, _I64, _F64, _P, _P, _P, _P],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
@@ -42,7 +45,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 11
 _lib = None
 
 
@@ -61,6 +64,8 @@ def load():
 		lib.vgr_grid_work_size.restype = ctypes.c_int64
 		lib.vgr_march_work_size.restype = ctypes.c_int64
 		lib.vgr_field_work_size.restype = ctypes.c_int64
+		lib.vgr_color_backward_work_size.restype = ctypes.c_int64
+		lib.vgr_density_backward_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

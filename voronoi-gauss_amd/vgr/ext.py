@@ -104,8 +104,11 @@ class _FieldExtension:
 		return A
 
 	@staticmethod
-	def density_backward(points, offsets, adj, raw, log_scale, quat, x, site, grad_sigma):
-		"""-> g_raw (N,), g_ls (N, 3), g_quat (N, 4) (vgf.cu:477-492)."""
+	def density_backward(points, offsets, adj, raw, log_scale, quat, x, site, grad_sigma, gather=False):
+		"""-> g_raw (N,), g_ls (N, 3), g_quat (N, 4) (vgf.cu:477-492). gather: the gradients gathered per site through
+		a workspace from torch's allocator (vgr_density_backward_work_size), else (the default, faster for density:
+		8 atomics per sample and neighbour against a per-site loop that is as long as the busiest site of its wave)
+		scattered with atomics."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (adj, 'adj', torch.int32), (raw, 'raw', torch.float32),
 						 (log_scale, 'log_scale', torch.float32), (quat, 'quat', torch.float32), (x, 'x', torch.float32),
@@ -115,15 +118,21 @@ class _FieldExtension:
 		m = x.size(0)
 		if m == 0:
 			return g_raw, g_ls, g_quat
+		work, wb = None, 0
+		if gather:
+			wb = int(_lib.load().vgr_density_backward_work_size(points.numel() // 3, m))
+			work = torch.empty(wb, dtype=torch.uint8, device=x.device)
 		with torch.cuda.device(x.device):
 			call('vgr_density_backward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(log_scale), ptr(quat), ptr(x), ptr(site), m, ptr(grad_sigma), ptr(g_raw), ptr(g_ls),
-				 ptr(g_quat), stream_of(x.device))
+				 ptr(g_quat), ptr(work), wb, stream_of(x.device))
 		return g_raw, g_ls, g_quat
 
 	@staticmethod
-	def color_backward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site, rgb, grad_rgb):
-		"""-> g_ls (N, 3), g_quat (N, 4), g_sh (N, 16, 3) (vgf.cu:515-533)."""
+	def color_backward(points, offsets, adj, log_scale, quat, sh, sh_deg, x, dirs, site, rgb, grad_rgb, gather=True):
+		"""-> g_ls (N, 3), g_quat (N, 4), g_sh (N, 16, 3) (vgf.cu:515-533). gather (the default): the gradients
+		gathered per site through a workspace from torch's allocator (vgr_color_backward_work_size), else scattered
+		with up to 55 atomics per sample and neighbour."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (adj, 'adj', torch.int32), (log_scale, 'log_scale', torch.float32),
 						 (quat, 'quat', torch.float32), (sh, 'sh', torch.float32), (x, 'x', torch.float32),
@@ -135,10 +144,14 @@ class _FieldExtension:
 		m = x.size(0)
 		if m == 0:
 			return g_ls, g_quat, g_sh
+		work, wb = None, 0
+		if gather:
+			wb = int(_lib.load().vgr_color_backward_work_size(points.numel() // 3, m))
+			work = torch.empty(wb, dtype=torch.uint8, device=x.device)
 		with torch.cuda.device(x.device):
 			call('vgr_color_backward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(log_scale), ptr(quat), ptr(sh), int(sh_deg), ptr(x), ptr(dirs), ptr(site), m, ptr(rgb),
-				 ptr(grad_rgb), ptr(g_ls), ptr(g_quat), ptr(g_sh), stream_of(x.device))
+				 ptr(grad_rgb), ptr(g_ls), ptr(g_quat), ptr(g_sh), ptr(work), wb, stream_of(x.device))
 		return g_ls, g_quat, g_sh
 
 	@staticmethod
