@@ -204,6 +204,32 @@ int vgr_conic_backward(const float* log_scale, const float* quat, int64_t n, dou
                        float* g_ls, float* g_quat, void* stream);
 
 /*
+ * The inference records of foam_infer from the model's tensors. Replaces the body of pack_foam()
+ * (render.py:179-225, called by bench_infer.py:37-41 and eval_scene.py:69 before rendering).
+ *   points f32 (N, 3), offsets i32 (N + 1), adj i32 (M): the Delaunay CSR; raw f32 (N); d_log_scale, c_log_scale
+ *   f32 (N, 3); dA, cA f32 (N, 6) conics (vgr_conic_forward with scale_floor); sh f32 (N, 16, 3); perm i32 (N)
+ *   new -> old renumbering (render.py:168-176) or NULL for none.
+ *   -> points4 f32 (N, 4), offsets_sf i32 (N + 1) self-first, nbr i32 (M + N), edge f32 (M + N, 4) =
+ *   (p_j, half2(r2_j, lam_j) bits), attr f32 (N, 20), sh32 f32 (N, 16, 3), sh16 (optional, NULL = none) f16
+ *   (N, 16, 3); all in the new numbering. work: device scratch of vgr_pack_work_size(N) bytes, 256-byte aligned.
+ */
+int64_t vgr_pack_work_size(int64_t n_sites);
+
+/*
+ * Z-order keys of points f32 (n, 3) over their bounding box, bits per axis (<= 21): the keys morton_order()
+ * (render.py:168-176) sorts to renumber the sites, with its arithmetic (q = trunc((p - lo) / max(hi - lo, 1e-12) *
+ * (2^bits - 1)), bit b of axis a at bit 3 b + a) -> code i64 (n). work: vgr_morton_work_size(n) bytes.
+ */
+int64_t vgr_morton_work_size(int64_t n);
+int vgr_morton_codes(const float* points, int64_t n, int32_t bits, int64_t* code, void* work, int64_t work_bytes,
+                     void* stream);
+int vgr_pack_foam(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj, int64_t n_adj,
+                  const float* raw, const float* d_log_scale, const float* c_log_scale, const float* dA,
+                  const float* cA, const float* sh, const int32_t* perm, double scale_floor, double eps_density,
+                  float* points4, int32_t* offsets_sf, int32_t* nbr, float* edge, float* attr, float* sh32,
+                  void* sh16, void* work, int64_t work_bytes, void* stream);
+
+/*
  * Uniform grid over the sites for exact nearest-site queries: the start-cell locator. No kernel of the reference
  * corresponds; it replaces the host-side cKDTree query of nearest_sites() (sites.py:38-39), which finds the start
  * site per camera centre (bench_infer.py:60, eval_scene.py:69, bench_fps.py:156) and per ray origin of a ray batch.

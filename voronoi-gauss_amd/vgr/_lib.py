@@ -37,6 +37,11 @@ SIGNATURES = {
 	'vgr_color_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64,
 						   _P],
 	'vgr_conic_backward': [_P, _P, _I64, _F64, _P, _P, _P, _P],
+	'vgr_pack_work_size': [_I64],
+	'vgr_morton_work_size': [_I64],
+	'vgr_morton_codes': [_P, _I64, _I32, _P, _P, _I64, _P],
+	'vgr_pack_foam': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P,
+					  _I64, _P],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
@@ -45,7 +50,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 13
 _lib = None
 
 
@@ -66,6 +71,8 @@ def load():
 		lib.vgr_field_work_size.restype = ctypes.c_int64
 		lib.vgr_color_backward_work_size.restype = ctypes.c_int64
 		lib.vgr_density_backward_work_size.restype = ctypes.c_int64
+		lib.vgr_pack_work_size.restype = ctypes.c_int64
+		lib.vgr_morton_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

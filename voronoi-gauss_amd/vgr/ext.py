@@ -296,6 +296,52 @@ def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None,
 	return (stats, trace) if trace is not None else stats
 
 
+def pack_foam(points, offsets, adj, raw, d_log_scale, c_log_scale, dA, cA, sh, perm=None, scale_floor=0.0,
+			  eps_density=0.0, sh_half=False):
+	"""The inference records on the GPU (vgr_pack_foam, render.py:179-225) from the model's device tensors and the
+	conics; perm (N,) new -> old renumbers the sites (None: none). -> points (N, 4), offsets (N + 1), nbr (E),
+	edge (E, 4), attr (N, 20), sh32 (N, 16, 3) fp32, sh16 (N, 16, 3) fp16 or None, all in the new numbering."""
+	for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32), (adj, 'adj', torch.int32),
+					 (raw, 'raw', torch.float32), (d_log_scale, 'd_log_scale', torch.float32),
+					 (c_log_scale, 'c_log_scale', torch.float32), (dA, 'dA', torch.float32), (cA, 'cA', torch.float32),
+					 (sh, 'sh', torch.float32)):
+		_check(t, n, dt)
+	n, m = points.size(0), adj.numel()
+	_require(sh.dim() == 3 and sh.size(0) == n and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+	dev = points.device
+	p32 = None
+	if perm is not None:
+		p32 = perm.to(torch.int32).contiguous()
+		_check(p32, 'perm', torch.int32)
+	f = dict(dtype=torch.float32, device=dev)
+	out = {'points': torch.empty(n, 4, **f), 'offsets': torch.empty(n + 1, dtype=torch.int32, device=dev),
+		   'nbr': torch.empty(m + n, dtype=torch.int32, device=dev), 'edge': torch.empty(m + n, 4, **f),
+		   'attr': torch.empty(n, 20, **f), 'sh32': torch.empty(n, 16, 3, **f),
+		   'sh16': torch.empty(n, 16, 3, dtype=torch.float16, device=dev) if sh_half else None}
+	wb = int(_lib.load().vgr_pack_work_size(n))
+	work = torch.empty(wb, dtype=torch.uint8, device=dev)
+	with torch.cuda.device(dev):
+		call('vgr_pack_foam', ptr(points), n, ptr(offsets), ptr(adj), m, ptr(raw), ptr(d_log_scale), ptr(c_log_scale),
+			 ptr(dA), ptr(cA), ptr(sh), ptr(p32), float(scale_floor), float(eps_density), ptr(out['points']),
+			 ptr(out['offsets']), ptr(out['nbr']), ptr(out['edge']), ptr(out['attr']), ptr(out['sh32']),
+			 ptr(out['sh16']), ptr(work), wb, stream_of(dev))
+	return out
+
+
+def morton_codes(points, bits=10):
+	"""(N,) int64 Z-order keys of points (N, 3) over their bounding box (vgr_morton_codes, render.py:168-176)."""
+	_check(points, 'points', torch.float32)
+	n = points.size(0)
+	code = torch.empty(n, dtype=torch.int64, device=points.device)
+	if n == 0:
+		return code
+	wb = int(_lib.load().vgr_morton_work_size(n))
+	work = torch.empty(wb, dtype=torch.uint8, device=points.device)
+	with torch.cuda.device(points.device):
+		call('vgr_morton_codes', ptr(points), n, int(bits), ptr(code), ptr(work), wb, stream_of(points.device))
+	return code
+
+
 _FIELD, _MARCH, _FOAM_INFER = _FieldExtension(), _MarchExtension(), _FoamInferExtension()
 
 

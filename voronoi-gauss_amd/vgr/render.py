@@ -165,15 +165,23 @@ def sh_basis(d, deg):
 	return b
 
 
-def morton_order(points, bits=10):
-	"""Permutation sorting the points along a Z-order curve of their bounding box (render.py:168-176)."""
+def morton_codes(points, bits=10):
+	"""Z-order keys of the points over their bounding box, as morton_order sorts them (render.py:168-176): on the
+	GPU one pass of vgr_morton_codes, on the host the same arithmetic in torch."""
+	if points.is_cuda:
+		return ext.morton_codes(points.float().contiguous(), bits)
 	lo, hi = points.amin(0), points.amax(0)
 	q = ((points - lo) / (hi - lo).clamp_min(1e-12) * (2 ** bits - 1)).long()
 	code = torch.zeros(len(points), dtype=torch.long, device=points.device)
 	for b in range(bits):
 		for a in range(3):
 			code |= ((q[:, a] >> b) & 1) << (3 * b + a)
-	return torch.argsort(code)
+	return code
+
+
+def morton_order(points, bits=10):
+	"""Permutation sorting the points along a Z-order curve of their bounding box (render.py:168-176)."""
+	return torch.argsort(morton_codes(points, bits))
 
 
 def cut_bits(r2, lam):
@@ -233,12 +241,25 @@ def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=Fa
 	(E)) with one float4 per edge = (p_j, half2(r2_j, lam_j)), r2 the squared distance beyond which
 	rho_j G_j < eps_density (inf when eps_density = 0) and lam the smallest eigenvalue of the colour conic, both
 	rounded to the safe side; attr (N, 20) = (density conic, min(raw, 30), colour conic, baked rgb); sh in fp32
-	or fp16; reorder renumbers the sites along a Z-order curve (perm: new -> old, inv: old -> new)."""
+	or fp16; reorder renumbers the sites along a Z-order curve (perm: new -> old, inv: old -> new). Built on the GPU
+	by vgr_pack_foam (the Z-order permutation by torch's sort); pack_foam_arrays is the same pack in torch."""
 	g = model.graph
 	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
 	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
-	return pack_foam_arrays(g.points, g.offsets, g.adj, model.raw, model.d_log_scale, model.c_log_scale, dA, cA,
-							model.sh(), scale_floor, eps_density, sh_half, reorder)
+	n = len(g.points)
+	perm = inv = None
+	if reorder:
+		perm = morton_order(g.points)
+		inv = torch.empty_like(perm)
+		inv[perm] = torch.arange(n, device=perm.device)
+	sh = model.sh().detach().float().contiguous()
+	out = ext.pack_foam(g.points, g.offsets, g.adj, model.raw.detach().contiguous(),
+						model.d_log_scale.detach().contiguous(), model.c_log_scale.detach().contiguous(),
+						dA.detach().contiguous(), cA.detach().contiguous(), sh, perm, scale_floor, eps_density, sh_half)
+	return {'points': out['points'], 'offsets': out['offsets'], 'nbr': out['nbr'], 'edge': out['edge'],
+			'attr': out['attr'], 'sh': out['sh16'] if sh_half else out['sh32'], 'sh32': out['sh32'], 'perm': perm,
+			'inv': inv, 'orig': (perm if reorder else torch.empty(0, device=g.points.device)).int().contiguous(),
+			'baked_center': None}
 
 
 @torch.no_grad()
