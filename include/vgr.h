@@ -223,6 +223,14 @@ int64_t vgr_pack_work_size(int64_t n_sites);
 int64_t vgr_morton_work_size(int64_t n);
 int vgr_morton_codes(const float* points, int64_t n, int32_t bits, int64_t* code, void* work, int64_t work_bytes,
                      void* stream);
+/*
+ * Per-view site colours for the baked colour mode: for every packed site i, max(SH_i(d_i) + 1/2, 0) with
+ * d_i = normalize(p_i - (cx, cy, cz)) (norm clamped at 1e-12), written into attr[i, 16..18]. Replaces the torch
+ * ops of the reference's baking step (render.py:228-235, run per camera before render_rays_foam_infer with
+ * colors='baked'). points4 f32 (N, 4) and sh32 f32 (N, 16, 3) are vgr_pack_foam's outputs; attr f32 (N, 20).
+ */
+int vgr_bake_colors(const float* points4, const float* sh32, int64_t n_sites, int64_t sh_deg, double cx, double cy,
+                    double cz, float* attr, void* stream);
 int vgr_pack_foam(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj, int64_t n_adj,
                   const float* raw, const float* d_log_scale, const float* c_log_scale, const float* dA,
                   const float* cA, const float* sh, const int32_t* perm, double scale_floor, double eps_density,

@@ -96,6 +96,31 @@ def test_native_morton_codes_match_torch(model, gpu, bits):
 	assert ext.morton_codes(torch.zeros(0, 3, device=gpu)).numel() == 0
 
 
+@pytest.mark.parametrize('deg', [3, 2, 1, 0])
+def test_native_bake_matches_float64(model, gpu, deg):
+	"""vgr_bake_colors (the baking step of render.py:228-235) on a packed, renumbered scene against the same colours in
+	float64 from the packed positions and SH rows; attr's other columns untouched; a camera centre on a site gives
+	that site the degree-0 colour, and degree 0 gives max(Y00 sh_0 + 1/2, 0) everywhere, whatever the view."""
+	sc, m = model
+	pk = render.pack_foam(m, reorder=True)
+	for on_site, center in ((False, torch.tensor(sc.cameras[0].eye, dtype=torch.float32, device=gpu)),
+							(True, pk['points'][7, :3].clone())):
+		attr = pk['attr'].clone()
+		ext.bake_colors(pk['points'], pk['sh32'], deg, center, attr)
+		assert torch.equal(attr[:, :16], pk['attr'][:, :16]) and torch.equal(attr[:, 19:], pk['attr'][:, 19:])
+		p, sh = pk['points'][:, :3].double(), pk['sh32'].double()
+		v = p - center.double()
+		dirs = v / v.norm(dim=1, keepdim=True).clamp_min(1e-12)
+		ref = (render.sh_basis(dirs, deg)[:, :, None] * sh).sum(1).add(0.5).clamp_min(0)
+		assert (attr[:, 16:19].double() - ref).abs().max() < 2e-6
+		y00 = (0.28209479177387814 * sh[:, 0] + 0.5).clamp_min(0)
+		if on_site:
+			assert (attr[7, 16:19].double() - y00[7]).abs().max() < 1e-6
+		if deg == 0:
+			assert (attr[:, 16:19].double() - y00).abs().max() < 1e-6
+	ext.bake_colors(pk['points'][:0], pk['sh32'][:0], deg, center, pk['attr'][:0])
+
+
 def test_native_pack_errors(gpu):
 	pts = torch.zeros(4, 3, device=gpu)
 	with pytest.raises(RuntimeError, match='float32|CUDA|sh must'):

@@ -235,8 +235,54 @@ __global__ void __launch_bounds__(kBlock)
     code[i] = key;
 }
 
+// Baked colour of site i for the view from c = (cx, cy, cz) (render.py:228-235): max(SH_i(d) + 1/2, 0) with
+// d = (p_i - c) / max(|p_i - c|, 1e-12), written to attr[20 i + 16 .. 18]. The basis is sh_basis's; the
+// coefficients of degree <= deg are summed in storage order, and only their float4 are read.
+__global__ void __launch_bounds__(kBlock)
+    bake_kernel(const float4* __restrict__ points4, const float4* __restrict__ sh32, int64_t n, int deg, float cx,
+                float cy, float cz, float* __restrict__ attr) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const float4 p = points4[i];
+    float dx = p.x - cx, dy = p.y - cy, dz = p.z - cz;
+    const float nrm = fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
+    dx /= nrm, dy /= nrm, dz /= nrm;
+    float b[16];
+    sh_basis(dx, dy, dz, deg, b);
+    const int nb = (deg + 1) * (deg + 1);
+    float c[3] = {0.f, 0.f, 0.f};
+    const float4* s = sh32 + 12 * i;
+#pragma unroll
+    for (int q = 0; q < 12; ++q) {
+        if (4 * q >= 3 * nb) break;
+        const float4 f = s[q];
+        const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = 4 * q + u;
+            if (j / 3 < nb) c[j % 3] += b[j / 3] * fv[u];
+        }
+    }
+    float* a = attr + 20 * i;
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) a[16 + ch] = fmaxf(c[ch] + 0.5f, 0.f);
+}
+
 }  // namespace
 }  // namespace vgr
+
+extern "C" int vgr_bake_colors(const float* points4, const float* sh32, int64_t n_sites, int64_t sh_deg,
+                               double cx, double cy, double cz, float* attr, void* stream) {
+    using namespace vgr;
+    VGR_REQUIRE(n_sites >= 0, "bake_colors: n_sites must be >= 0");
+    VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
+    if (n_sites == 0) return VGR_OK;
+    VGR_REQUIRE(points4 && sh32 && attr, "bake_colors: null pointer");
+    hipLaunchKernelGGL(bake_kernel, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, as_stream(stream),
+                       reinterpret_cast<const float4*>(points4), reinterpret_cast<const float4*>(sh32), n_sites,
+                       int(sh_deg), float(cx), float(cy), float(cz), attr);
+    return launch_status("bake_kernel");
+}
 
 extern "C" int64_t vgr_morton_work_size(int64_t n) {
     return n > 0 ? 4 * 6 * vgr::grid_for(n, vgr::kBlock) : 0;

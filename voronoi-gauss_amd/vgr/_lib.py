@@ -40,6 +40,7 @@ SIGNATURES = {
 	'vgr_pack_work_size': [_I64],
 	'vgr_morton_work_size': [_I64],
 	'vgr_morton_codes': [_P, _I64, _I32, _P, _P, _I64, _P],
+	'vgr_bake_colors': [_P, _P, _I64, _I64, _F64, _F64, _F64, _P, _P],
 	'vgr_pack_foam': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P,
 					  _I64, _P],
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
@@ -50,7 +51,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 _lib = None
 
 

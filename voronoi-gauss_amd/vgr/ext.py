@@ -342,6 +342,23 @@ def morton_codes(points, bits=10):
 	return code
 
 
+def bake_colors(points4, sh32, sh_deg, center, attr):
+	"""Write the baked colours max(SH_k(d_k) + 1/2, 0) of the view from center (3,) into attr[:, 16:19] in place
+	(vgr_bake_colors, render.py:228-235); points4 (N, 4), sh32 (N, 16, 3) and attr (N, 20) are packed records."""
+	_check(points4, 'points4', torch.float32)
+	_check(sh32, 'sh32', torch.float32)
+	_check(attr, 'attr', torch.float32)
+	n = points4.size(0)
+	_require(points4.dim() == 2 and points4.size(1) == 4, 'points4 must be (N, 4)')
+	_require(sh32.shape == (n, 16, 3) and attr.shape == (n, 20), 'sh32 must be (N, 16, 3) and attr (N, 20)')
+	_require(sh32.device == points4.device == attr.device, 'points4, sh32 and attr must share a device')
+	cx, cy, cz = (float(v) for v in torch.as_tensor(center, dtype=torch.float32).reshape(3).tolist())
+	with torch.cuda.device(points4.device):
+		call('vgr_bake_colors', ptr(points4), ptr(sh32), n, int(sh_deg), cx, cy, cz, ptr(attr),
+			 stream_of(points4.device))
+	return attr
+
+
 _FIELD, _MARCH, _FOAM_INFER = _FieldExtension(), _MarchExtension(), _FoamInferExtension()
 
 

@@ -265,7 +265,11 @@ def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=Fa
 @torch.no_grad()
 def bake_colors(model, pack, center):
 	"""Site colours max(SH_k(d_k) + 1/2, 0) for the view direction d_k from the camera center to site k
-	(render.py:228-235)."""
+	(render.py:228-235). Packed records on the GPU are baked by vgr_bake_colors; host packs by the torch ops."""
+	if pack['attr'].is_cuda:
+		ext.bake_colors(pack['points'], pack['sh32'], model.sh_deg, center, pack['attr'])
+		pack['baked_center'] = center
+		return
 	points = model.graph.points if pack['perm'] is None else model.graph.points[pack['perm']]
 	dirs = torch.nn.functional.normalize(points - center.view(1, 3), dim=-1)
 	rgb = (sh_basis(dirs, model.sh_deg)[:, :, None] * pack['sh32']).sum(1).add_(0.5).clamp_min_(0.0)
