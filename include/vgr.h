@@ -122,6 +122,23 @@ int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offse
                       int32_t* trace, int64_t trace_cap, void* work, int64_t work_bytes, void* stream);
 
 /*
+ * Fused uniform-step march (backward: re-marches every ray). Replaces march_backward() of csrc/march.cu:405-428
+ * (kernel :264-345, export :433), called by _March.backward (ext.py:162-169) when training through ext.march.
+ *   The field, rays and march parameters are the forward's; rgb f32 (B, 3) and T f32 (B) are the forward's outputs
+ *   and g_rgb f32 (B, 3), g_T f32 (B) their upstream gradients.
+ *   -> g_raw f32 (N), g_dA f32 (N, 6), g_cA f32 (N, 6), g_sh f32 (N, 16, 3), overwritten (zeroed first). The sums
+ *   use fp32 atomics, so they agree with a sequential sum to rounding, not bitwise.
+ * work: as for vgr_march_forward (vgr_march_work_size(N, sh_deg) bytes, 256-byte aligned).
+ */
+int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                       int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                       int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                       const float* mid_t, const float* far_t, int64_t n_rays, double dt, int64_t n_bg,
+                       double t_thresh, double w_thresh, const float* rgb, const float* T, const float* g_rgb,
+                       const float* g_T, float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work,
+                       int64_t work_bytes, void* stream);
+
+/*
  * Nearest site of every sorted ray sample o + z d by a greedy walk (strict <). Replaces walk() of
  * csrc/vgf.cu:438-456 (export :566), bound by Graph.walk (ext.py:54-58).
  *   z f32 (B, S) sorted per ray; start i32 (B) -> site i32 (B, S), steps i32 (B) (steps may be NULL)

@@ -22,6 +22,8 @@ _SIGS = {
 						   _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32], ctypes.c_double),
 	'oracle_march_forward': ([_P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _F32, _I32, _F32,
 							  _F32, _P, _P, _P, _P, _P, _I32, _I32], ctypes.c_double),
+	'oracle_march_backward': ([_P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64, _F32, _I32, _F32,
+							   _F32, _P, _P, _P, _P, _P, _P, _P, _P], None),
 	'oracle_walk': ([_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _I32], None),
 	'oracle_density': ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _F32, _P, _I32], None),
 	'oracle_color': ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _I32], None),
@@ -118,6 +120,22 @@ def march_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, ne
 									   float(dt), int(n_bg), t_thresh, w_thresh, _p(rgb), _p(T), _p(depth), _p(stats),
 									   _p(trace), int(trace_cap), int(n_threads))
 	return {'rgb': rgb, 'T': T, 'depth': depth, 'stats': stats, 'trace': trace, 'seconds': secs}
+
+
+def march_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg, rgb, T,
+				   g_rgb, g_T, t_thresh=1e-4, w_thresh=1e-4):
+	"""Gradients of the march's rgb and T: -> g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)."""
+	arrs = [_a(points, np.float32), _a(offsets, np.int32), _a(adj, np.int32), _a(raw, np.float32),
+			_a(dA, np.float32), _a(cA, np.float32), _a(sh, np.float32)]
+	ray_arrs = [_a(o, np.float32), _a(d, np.float32), _a(start, np.int32), _a(near, np.float32),
+				_a(mid, np.float32), _a(far, np.float32)]
+	n, B = len(arrs[0]), len(ray_arrs[0])
+	g = [np.zeros(n, np.float32), np.zeros((n, 6), np.float32), np.zeros((n, 6), np.float32),
+		 np.zeros((n, 16, 3), np.float32)]
+	up = [_a(rgb, np.float32), _a(T, np.float32), _a(g_rgb, np.float32), _a(g_T, np.float32)]
+	load().oracle_march_backward(*[_p(a) for a in arrs], int(sh_deg), *[_p(a) for a in ray_arrs], B, float(dt),
+								 int(n_bg), t_thresh, w_thresh, *[_p(a) for a in up], *[_p(a) for a in g])
+	return tuple(g)
 
 
 def walk(points, offsets, adj, o, d, z, start, n_threads=0):

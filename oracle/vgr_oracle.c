@@ -9,6 +9,7 @@
  *                                               kernel :286-361, cache :151-168, site_color :121-149)
  *   march_forward csrc/march.cu:134-262        (load_ray :134-141, sample_at :143-153, walk_to :157-180,
  *                                               density_at :182-192, color_at :195-219, kernel :221-262)
+ *   march_backward csrc/march.cu:264-345, 402-428
  *   walk          csrc/vgf.cu:51-79
  *   density       csrc/vgf.cu:98-119,152-177
  *   color         csrc/vgf.cu:202-282
@@ -533,6 +534,124 @@ double oracle_march_forward(const float* points, const int32_t* offsets, const i
 #else
     return 0.0;
 #endif
+}
+
+/* ==================================================================================== march_backward */
+
+/* gA_k += gm (v v^T) in the packed symmetric layout (xx, 2xy, 2xz, yy, 2yz, zz); march.cu:86-95. */
+static void add_conic_grad(float* gA, int k, float gm, const float v[3]) {
+    float* a = gA + 6 * (int64_t)k;
+    a[0] += gm * v[0] * v[0];
+    a[1] += 2.f * gm * v[0] * v[1];
+    a[2] += 2.f * gm * v[0] * v[2];
+    a[3] += gm * v[1] * v[1];
+    a[4] += 2.f * gm * v[1] * v[2];
+    a[5] += gm * v[2] * v[2];
+}
+
+/* One ray of the backward: the forward replayed sample by sample (same walk, density, colour and stopping rule),
+ * the upstream gradient of the density at each sample, d rgb / d sigma_k = delta_k (T_{k+1} C_k - (rgb - acc_k))
+ * and d T / d sigma_k = -delta_k T, scattered over the sample's neighbourhood into raw and the density conic; for
+ * coloured samples the gradient of C_k into the SH rows and the colour conics. march.cu:264-345 (the thresholds
+ * 1e-12 on the density term and 1e-7 on the normalised colour weight are the reference's). */
+static void march_ray_backward(const Field* F, float dt, int n_bg, float t_thresh, float w_thresh, const float o[3],
+                               const float d[3], int start, float near, float mid, float far, const float fg[3],
+                               float T_out, const float gR[3], float gT, float* g_raw, float* g_dA, float* g_cA,
+                               float* g_sh) {
+    const int n_in = mid > near ? (int)ceilf((mid - near) / dt) : 0;
+    const int n_total = n_in + n_bg;
+    const int nb = (F->sh_deg + 1) * (F->sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F->sh_deg, b);
+    const float gT_final = gT * T_out;
+    int cur = start, walk_steps = 0;
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f};
+    for (int k = 0; k < n_total; ++k) {
+        float t, delta, x[3];
+        sample_at(near, mid, far, n_in, dt, n_bg, k, &t, &delta);
+        for (int a = 0; a < 3; ++a) x[a] = o[a] + t * d[a];
+        cur = march_walk_to(F, cur, x, &walk_steps);
+        const float alpha = 1.f - expf(-march_density(F, cur, x) * delta);
+        const float w = T * alpha;
+        const float T_next = T * (1.f - alpha);
+        const int active = w > w_thresh;
+        float C[3] = {0.f, 0.f, 0.f}, mmin = K_INF, inv_a = 0.f;
+        const int e0 = F->offsets[cur], n = F->offsets[cur + 1] - e0 + 1;
+        if (active) {
+            /* the colour blend of march_color, keeping m_min and 1 / sum of the shifted weights */
+            for (int e = 0; e < n; ++e) {
+                const int q = neighbor(F, cur, e0, e);
+                const float* p = F->points + 3 * (int64_t)q;
+                const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+                mmin = fminf(mmin, conic_maha(F->cA, q, v));
+            }
+            float A = 0.f, cs[3] = {0.f, 0.f, 0.f};
+            for (int e = 0; e < n; ++e) {
+                const int q = neighbor(F, cur, e0, e);
+                const float* p = F->points + 3 * (int64_t)q;
+                const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+                const float a = expf(-0.5f * (conic_maha(F->cA, q, v) - mmin));
+                float c[3];
+                sh_eval(F->sh, q, b, nb, c);
+                A += a;
+                for (int ch = 0; ch < 3; ++ch) cs[ch] += a * fmaxf(c[ch], 0.f);
+            }
+            inv_a = 1.f / A;
+            for (int ch = 0; ch < 3; ++ch) C[ch] = cs[ch] * inv_a;
+            for (int ch = 0; ch < 3; ++ch) acc[ch] += w * C[ch];
+        }
+        float gsig = 0.f;
+        for (int ch = 0; ch < 3; ++ch) gsig += gR[ch] * (T_next * C[ch] - (fg[ch] - acc[ch]));
+        gsig = delta * (gsig - gT_final);
+        if (gsig != 0.f) {
+            for (int e = 0; e < n; ++e) {
+                const int q = neighbor(F, cur, e0, e);
+                const float* p = F->points + 3 * (int64_t)q;
+                const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+                const float gc = gsig * expf(fminf(F->raw[q], 30.f) - 0.5f * conic_maha(F->dA, q, v));
+                if (fabsf(gc) > 1e-12f) {
+                    g_raw[q] += gc;
+                    add_conic_grad(g_dA, q, -0.5f * gc, v);
+                }
+            }
+        }
+        if (active) {
+            const float gC[3] = {w * gR[0], w * gR[1], w * gR[2]};
+            const float gCC = gC[0] * C[0] + gC[1] * C[1] + gC[2] * C[2];
+            for (int e = 0; e < n; ++e) {
+                const int q = neighbor(F, cur, e0, e);
+                const float* p = F->points + 3 * (int64_t)q;
+                const float v[3] = {x[0] - p[0], x[1] - p[1], x[2] - p[2]};
+                const float a = expf(-0.5f * (conic_maha(F->cA, q, v) - mmin)) * inv_a;
+                if (a < 1e-7f) continue;
+                float c[3];
+                sh_eval(F->sh, q, b, nb, c);
+                float* gs = g_sh + 48 * (int64_t)q;
+                for (int ch = 0; ch < 3; ++ch) {
+                    const float dc = c[ch] > 0.f ? a * gC[ch] : 0.f;
+                    for (int j = 0; j < nb; ++j) gs[3 * j + ch] += b[j] * dc;
+                }
+                const float ga = gC[0] * fmaxf(c[0], 0.f) + gC[1] * fmaxf(c[1], 0.f) + gC[2] * fmaxf(c[2], 0.f);
+                add_conic_grad(g_cA, q, -0.5f * a * (ga - gCC), v);
+            }
+        }
+        T = T_next;
+        if (T < t_thresh) break;
+    }
+}
+
+/* Gradients of a march over rays 0..B-1 (sequential, so the sums are deterministic); g_* are accumulated into
+ * (the caller zeroes them). march.cu:264-345, host march_backward :402-428. */
+void oracle_march_backward(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                           const float* dA, const float* cA, const float* sh, int sh_deg, const float* o,
+                           const float* d, const int32_t* start, const float* near_t, const float* mid_t,
+                           const float* far_t, int64_t B, float dt, int n_bg, float t_thresh, float w_thresh,
+                           const float* rgb, const float* T, const float* g_rgb, const float* g_T, float* g_raw,
+                           float* g_dA, float* g_cA, float* g_sh) {
+    const Field F = {points, offsets, adj, raw, dA, cA, sh, sh_deg};
+    for (int64_t r = 0; r < B; ++r)
+        march_ray_backward(&F, dt, n_bg, t_thresh, w_thresh, o + 3 * r, d + 3 * r, start[r], near_t[r], mid_t[r],
+                           far_t[r], rgb + 3 * r, T[r], g_rgb + 3 * r, g_T[r], g_raw, g_dA, g_cA, g_sh);
 }
 
 /* ============================================================================ vgf forward operators */

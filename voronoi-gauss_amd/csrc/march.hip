@@ -381,6 +381,235 @@ __global__ void __launch_bounds__(kBlock, VGR_MARCH_WAVES)
     }
 }
 
+// ------------------------------------------------------------------------------------------------- backward
+//
+// The backward re-marches every ray (march.cu:264-345): the same batched neighbourhood passes resolve the same
+// samples at the same sites, a colour pass blends the coloured samples of each pass as the forward does, and then
+// the upstream gradient of each resolved sample's density, d rgb / d sigma = delta (T_next C - (rgb - acc)) and
+// d T / d sigma = -delta T (acc: the colour composited up to and including the sample), and of its colour, w dL/drgb,
+// are pushed to the neighbourhood. All samples of a pass share one neighbourhood, so one more pass over it sums every
+// sample's contribution per neighbour in registers and issues one set of fp32 atomics per neighbour and pass (1 for
+// raw, 6 + 6 for the conics, 3 (deg + 1)^2 for the SH row) where the reference issues one per sample and neighbour.
+// Per pair the reference's cut-offs hold: density terms with |g| <= 1e-12 and normalised colour weights below 1e-7
+// contribute nothing. The SH gradient of a neighbour is b_j gR_c sum_s a_s w_s over the samples whose weight passes
+// the cut-off, for the channels whose unclamped colour is positive (the colour depends only on the site and the ray).
+
+struct MarchGradIn {
+    const float* __restrict__ rgb;    // (B, 3) the forward's colour
+    const float* __restrict__ T;      // (B) the forward's final transmittance
+    const float* __restrict__ g_rgb;  // (B, 3)
+    const float* __restrict__ g_T;    // (B)
+};
+
+struct MarchGradOut {
+    float* __restrict__ g_raw;  // (N)
+    float* __restrict__ g_dA;   // (N, 6)
+    float* __restrict__ g_cA;   // (N, 6)
+    float* __restrict__ g_sh;   // (N, 16, 3)
+};
+
+constexpr float kMinColourWeight = 1e-7f;
+constexpr float kMinDensityGrad = 1e-12f;
+
+// g += s (v v^T) in the packed symmetric layout of the conics (xx, 2xy, 2xz, yy, 2yz, zz).
+__device__ __forceinline__ void add_outer(float (&g)[6], float s, const float (&v)[3]) {
+    g[0] += s * v[0] * v[0];
+    g[1] += 2.f * s * v[0] * v[1];
+    g[2] += 2.f * s * v[0] * v[2];
+    g[3] += s * v[1] * v[1];
+    g[4] += 2.f * s * v[1] * v[2];
+    g[5] += s * v[2] * v[2];
+}
+
+// The resolved samples of one pass: positions, density gradients, compositing weights, m_min, 1 / sum of shifted
+// colour weights and gR . C; bit j of `coloured` marks a sample with w > w_thresh.
+struct GradBatch {
+    float t[kBatch], gsig[kBatch], w[kBatch], mmin[kBatch], inv_a[kBatch], grc[kBatch];
+    int n;
+    unsigned coloured;
+};
+
+template <int NV>
+__device__ void grad_pass(const MarchField& F, const MarchGradOut& G, int i, const float (&o)[3], const float (&d)[3],
+                          const float (&b)[16], int nb, const float (&gR)[3], const GradBatch& S) {
+    const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float4* rp = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const SiteRec rc = {rp[0], rp[1], rp[2], rp[3]};
+        float c[3] = {0.f, 0.f, 0.f};
+        if (S.coloured) sh_eval_n<NV>(rp + kRec, b, nb, c);
+        const float gc3 = gR[0] * fmaxf(c[0], 0.f) + gR[1] * fmaxf(c[1], 0.f) + gR[2] * fmaxf(c[2], 0.f);
+        float graw = 0.f, aw = 0.f, gd[6], gc[6];
+#pragma unroll
+        for (int u = 0; u < 6; ++u) gd[u] = gc[u] = 0.f;
+        bool dens = false, col = false;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (j < S.n) {
+                float x[3], v[3];
+                point_at(o, d, S.t[j], x);
+                offset_to(rc.q0, x, v);
+                if (S.gsig[j] != 0.f) {
+                    const float g = S.gsig[j] * fexp(rc.q0.w - 0.5f * density_m(rc, v));
+                    if (fabsf(g) > kMinDensityGrad) graw += g, add_outer(gd, -0.5f * g, v), dens = true;
+                }
+                if ((S.coloured >> j) & 1u) {
+                    const float a = fexp(-0.5f * (color_m(rc.q2, rc.q3, v) - S.mmin[j])) * S.inv_a[j];
+                    if (a >= kMinColourWeight) {
+                        const float aw_j = a * S.w[j];
+                        aw += aw_j;
+                        add_outer(gc, -0.5f * aw_j * (gc3 - S.grc[j]), v);
+                        col = true;
+                    }
+                }
+            }
+        }
+        if (dens) {
+            unsafeAtomicAdd(G.g_raw + k, graw);
+            float* ga = G.g_dA + 6 * static_cast<int64_t>(k);
+#pragma unroll
+            for (int u = 0; u < 6; ++u) unsafeAtomicAdd(ga + u, gd[u]);
+        }
+        if (col) {
+            float* ga = G.g_cA + 6 * static_cast<int64_t>(k);
+#pragma unroll
+            for (int u = 0; u < 6; ++u) unsafeAtomicAdd(ga + u, gc[u]);
+            float* gs = G.g_sh + 48 * static_cast<int64_t>(k);
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) {
+                const float dc = c[ch] > 0.f ? gR[ch] * aw : 0.f;
+                if (dc != 0.f)
+                    for (int jj = 0; jj < nb; ++jj) unsafeAtomicAdd(gs + 3 * jj + ch, b[jj] * dc);
+            }
+        }
+    }
+}
+
+// Colour blend of the coloured samples of a pass (flush's sums): A_s and the unnormalised channel sums.
+template <int NV>
+__device__ void blend_sums(const MarchField& F, int i, const float (&o)[3], const float (&d)[3], const float (&b)[16],
+                           int nb, const GradBatch& S, float (&A)[kBatch], float (&cs)[kBatch][3]) {
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) A[s] = cs[s][0] = cs[s][1] = cs[s][2] = 0.f;
+    const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const float4 p = r[0], c0 = r[2], c1 = r[3];
+        float c[3];
+        sh_eval_n<NV>(r + kRec, b, nb, c);
+        c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
+#pragma unroll
+        for (int s = 0; s < kBatch; ++s) {
+            if (s < S.n && ((S.coloured >> s) & 1u)) {
+                float x[3], v[3];
+                point_at(o, d, S.t[s], x);
+                offset_to(p, x, v);
+                const float a = fexp(-0.5f * (color_m(c0, c1, v) - S.mmin[s]));
+                A[s] += a, cs[s][0] += a * c[0], cs[s][1] += a * c[1], cs[s][2] += a * c[2];
+            }
+        }
+    }
+}
+
+template <int NV>
+__device__ void march_ray_backward(const MarchField& F, const MarchParams& M, const MarchRays& R,
+                                   const MarchGradIn& GI, const MarchGradOut& G, int64_t r, int cur) {
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
+    const int n_in = mid > near ? static_cast<int>(ceilf((mid - near) / M.dt)) : 0;
+    const int n_total = n_in + M.n_bg;
+    const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    const float gR[3] = {GI.g_rgb[3 * r], GI.g_rgb[3 * r + 1], GI.g_rgb[3 * r + 2]};
+    const float fg[3] = {GI.rgb[3 * r], GI.rgb[3 * r + 1], GI.rgb[3 * r + 2]};
+    const float gT_final = GI.g_T[r] * GI.T[r];
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f};
+    int k = 0, moves = 0;
+    bool live = true;
+    while (live && k < n_total) {
+        GradBatch S;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            float unused;
+            sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), S.t[j], unused);
+        }
+        CellPass C;
+        cell_pass<block_vec4(NV)>(F, cur, o, d, S.t, C);
+        const bool force = moves >= kWalkCap;
+        int next = cur;
+        bool run = true;
+        float Tn[kBatch], delta[kBatch];
+        S.n = 0, S.coloured = 0u;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            S.w[j] = S.gsig[j] = S.inv_a[j] = S.grc[j] = Tn[j] = delta[j] = 0.f;
+            S.mmin[j] = C.mmin[j];
+            if (!run || k + j >= n_total) {
+                run = false;
+            } else if (C.best[j] == cur || (j == 0 && force)) {
+                float t;
+                sample_at(near, mid, far, n_in, M, k + j, t, delta[j]);
+                const float alpha = 1.f - fexp(-C.sigma[j] * delta[j]);
+                const float w = T * alpha;
+                ++S.n;
+                S.w[j] = w;
+                if (w > M.w_thresh) S.coloured |= 1u << j;
+                T *= 1.f - alpha;
+                Tn[j] = T;
+                if (T < M.t_thresh) run = live = false;
+            } else {
+                next = C.best[j], run = false;
+            }
+        }
+        float A[kBatch], cs[kBatch][3];
+        if (S.coloured) blend_sums<NV>(F, cur, o, d, b, nb, S, A, cs);
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (j < S.n) {
+                float Cj[3] = {0.f, 0.f, 0.f};
+                if ((S.coloured >> j) & 1u) {
+                    S.inv_a[j] = 1.f / A[j];
+#pragma unroll
+                    for (int a = 0; a < 3; ++a) Cj[a] = cs[j][a] * S.inv_a[j], acc[a] += S.w[j] * Cj[a];
+                    S.grc[j] = gR[0] * Cj[0] + gR[1] * Cj[1] + gR[2] * Cj[2];
+                }
+                float g = 0.f;
+#pragma unroll
+                for (int a = 0; a < 3; ++a) g += gR[a] * (Tn[j] * Cj[a] - (fg[a] - acc[a]));
+                S.gsig[j] = delta[j] * (g - gT_final);
+            }
+        }
+        if (S.n > 0) grad_pass<NV>(F, G, cur, o, d, b, nb, gR, S);
+        k += S.n;
+        moves = S.n > 0 ? 0 : moves;
+        if (live && k < n_total && next != cur) cur = next, ++moves;
+    }
+}
+
+__global__ void __launch_bounds__(kBlock)
+    march_backward_kernel(MarchField F, MarchParams M, MarchRays R, MarchGradIn GI, MarchGradOut G) {
+    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
+    if (r >= R.n) return;
+    const int cur = R.start[r];
+    if (cur < 0 || cur >= F.n_sites) return;  // not traced: no samples, no gradient
+    switch (F.sh_deg) {
+        case 0: march_ray_backward<sh_vec4_f32(0)>(F, M, R, GI, G, r, cur); break;
+        case 1: march_ray_backward<sh_vec4_f32(1)>(F, M, R, GI, G, r, cur); break;
+        case 2: march_ray_backward<sh_vec4_f32(2)>(F, M, R, GI, G, r, cur); break;
+        default: march_ray_backward<sh_vec4_f32(3)>(F, M, R, GI, G, r, cur); break;
+    }
+}
+
+// Grid-stride fill with zeros (a kernel, not a memset, so that a captured stream records no memset node).
+constexpr int64_t kZeroBlocks = 4096;
+__global__ void __launch_bounds__(256) zero_kernel(float* __restrict__ p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += kZeroBlocks * 256) p[i] = 0.f;
+}
+
 }  // namespace
 }  // namespace vgr
 
@@ -427,4 +656,46 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
         hipLaunchKernelGGL(march_forward_kernel<false>, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0,
                            as_stream(stream), F, M, R, O);
     return launch_status("march_forward_kernel");
+}
+
+extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                                  int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                                  int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                                  const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
+                                  double dt, int64_t n_bg, double t_thresh, double w_thresh, const float* rgb,
+                                  const float* T, const float* g_rgb, const float* g_T, float* g_raw, float* g_dA,
+                                  float* g_cA, float* g_sh, void* work, int64_t work_bytes, void* stream) {
+    using namespace vgr;
+    VGR_REQUIRE(n_rays >= 0, "march_backward: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
+    VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
+    VGR_REQUIRE(n_bg >= 0 && n_bg <= INT_MAX, "march_backward: n_bg must be >= 0");
+    VGR_REQUIRE(dt > 0.0, "march_backward: dt must be > 0");
+    VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "march_backward: n_sites must be in [1, 2^31)");
+    VGR_REQUIRE(n_adj >= 0 && n_adj <= INT_MAX, "march_backward: n_adj must be in [0, 2^31)");
+    VGR_REQUIRE(g_raw && g_dA && g_cA && g_sh, "march_backward: null gradient pointer");
+    const hipStream_t s = as_stream(stream);
+    // the gradients are overwritten: zeroed by a kernel (no memset node if the caller captures the stream)
+    float* const outs[4] = {g_raw, g_dA, g_cA, g_sh};
+    const int64_t sizes[4] = {n_sites, 6 * n_sites, 6 * n_sites, 48 * n_sites};
+    for (int u = 0; u < 4; ++u)
+        hipLaunchKernelGGL(zero_kernel, dim3(kZeroBlocks), dim3(256), 0, s, outs[u], sizes[u]);
+    if (n_rays == 0) return launch_status("march_backward zero");
+    VGR_REQUIRE(points && offsets && (adj || n_adj == 0) && raw && dA && cA && sh,
+                "march_backward: null field pointer");
+    VGR_REQUIRE(o && d && start && near_t && mid_t && far_t, "march_backward: null ray pointer");
+    VGR_REQUIRE(rgb && T && g_rgb && g_T, "march_backward: null forward output or upstream gradient pointer");
+    const int64_t need = vgr_march_work_size(n_sites, sh_deg);
+    VGR_REQUIRE(work && work_bytes >= need, "march_backward: work must hold %lld bytes", static_cast<long long>(need));
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "march_backward: work must be 256-byte aligned");
+    float4* rec = static_cast<float4*>(work);
+    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
+    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
+                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
+    const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
+    const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
+    const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
+    const MarchGradIn GI{rgb, T, g_rgb, g_T};
+    const MarchGradOut G{g_raw, g_dA, g_cA, g_sh};
+    hipLaunchKernelGGL(march_backward_kernel, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0, s, F, M, R, GI, G);
+    return launch_status("march_backward_kernel");
 }

@@ -25,6 +25,8 @@ SIGNATURES = {
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
+	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
+						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
 								_P],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
@@ -51,7 +53,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 _lib = None
 
 

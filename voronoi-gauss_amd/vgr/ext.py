@@ -3,13 +3,14 @@ hand-written gfx950 kernels of libvgr.so instead of JIT-built CUDA extensions.
 
 Same names, argument meaning and error behaviour as the reference:
   extension().walk / density_forward / color_forward / conic_forward       (csrc/vgf.cu:438-546)
-  march_extension().march_forward                                          (csrc/march.cu:383-403)
+  extension().density_backward / color_backward / conic_backward          (csrc/vgf.cu:121-148,179-198,284-424)
+  march_extension().march_forward / march_backward                         (csrc/march.cu:383-428)
   foam_infer_extension().foam_infer                                        (csrc/foam_infer.cu:376-435)
   Graph, density, color, conic, conic_reference, march                     (ext.py:46-182)
 Inputs are checked like the reference's TORCH_CHECKs (CUDA, contiguous, dtype, shapes) and a violation raises
 RuntimeError; outputs are allocated here with torch on the input's device and the kernels run asynchronously on
-torch's current stream. Training (the backward kernels and the autograd replay) is not part of this build: the
-autograd wrappers evaluate the forward pass and raise if a gradient is requested."""
+torch's current stream. density, color, conic and march are autograd Functions whose backward runs the gradient
+kernels; the training renderer foam.cu (forward with records, backward) is not part of this build."""
 
 import torch
 
@@ -213,6 +214,34 @@ class _MarchExtension:
 				 ptr(far), B, float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(depth),
 				 ptr(stats), ptr(trace), int(trace_cap), ptr(work), work_bytes, stream_of(dev))
 		return out
+
+	@staticmethod
+	def march_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
+					   t_thresh, w_thresh, rgb, T, g_rgb, g_T):
+		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (march.cu:405-428)."""
+		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
+						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
+						  (d, 'd', torch.float32), (start, 'start', torch.int32), (near, 'near', torch.float32),
+						  (mid, 'mid', torch.float32), (far, 'far', torch.float32), (rgb, 'rgb', torch.float32),
+						  (T, 'T', torch.float32), (g_rgb, 'g_rgb', torch.float32), (g_T, 'g_T', torch.float32)):
+			_check(t, n, dtp)
+		_require(sh.dim() == 3 and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+		_require(dA.size(1) == 6 and cA.size(1) == 6, 'conics must be (N, 6)')
+		B, dev = o.size(0), o.device
+		_require(rgb.shape == g_rgb.shape == (B, 3) and T.shape == g_T.shape == (B,),
+				 'rgb, g_rgb must be (B, 3) and T, g_T (B,)')
+		n = points.numel() // 3
+		g = [torch.empty(n, device=dev), torch.empty(n, 6, device=dev), torch.empty(n, 6, device=dev),
+			 torch.empty(n, 16, 3, device=dev)]
+		work_bytes = int(_lib.load().vgr_march_work_size(n, int(sh_deg)))
+		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
+		with torch.cuda.device(dev):
+			call('vgr_march_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
+				 ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid), ptr(far), B,
+				 float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(g_rgb), ptr(g_T),
+				 *[ptr(x) for x in g], ptr(work), work_bytes, stream_of(dev))
+		return g
 
 
 # ============================================================================ foam_infer.cu
@@ -498,23 +527,27 @@ def conic_reference(log_scale, quat, floor=0.0):
 	return torch.stack([A[:, 0, 0], A[:, 0, 1], A[:, 0, 2], A[:, 1, 1], A[:, 1, 2], A[:, 2, 2]], -1).contiguous()
 
 
-class _ForwardOnly(torch.autograd.Function):
-	"""Wraps a forward result so that parameters requiring gradients keep a graph edge whose backward raises: the
-	march's backward (csrc/march.cu:264-345) is not part of this build."""
+class _March(torch.autograd.Function):
+	"""The march with its backward (vgr_march_backward re-marches every ray; ext.py:150-169)."""
 
 	@staticmethod
-	def forward(ctx, out, *params):
-		return out.clone()
+	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg):
+		rgb, T, depth, stats = march_extension().march_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
+															   sh, cfg[0], *rays, *cfg[1:])
+		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, *rays)
+		ctx.graph, ctx.cfg = graph, cfg
+		ctx.mark_non_differentiable(depth, stats)
+		return rgb, T, depth, stats
 
 	@staticmethod
-	def backward(ctx, *grads):
-		raise RuntimeError('backward of the uniform march is not part of this build (march.cu forward only)')
-
-
-def _forward_only(out, params):
-	if torch.is_grad_enabled() and any(isinstance(p, torch.Tensor) and p.requires_grad for p in params):
-		return _ForwardOnly.apply(out, *params)
-	return out
+	def backward(ctx, g_rgb, g_T, _g_depth, _g_stats):
+		raw, dA, cA, sh, rgb, T, *rays = ctx.saved_tensors
+		g, cfg = ctx.graph, ctx.cfg
+		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
+		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
+		grads = march_extension().march_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays,
+												 *cfg[1:], rgb, T, g_rgb, g_T)
+		return (*grads, None, None, None)
 
 
 def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg, t_thresh=1e-4, w_thresh=1e-4):
@@ -522,8 +555,9 @@ def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
 	depth (B,), per-ray stats (B, 3) int: samples marched, samples with color, walk steps (ext.py:172-182)."""
 	rays = tuple(t.float().contiguous() for t in (o, d)) + (start.int().contiguous(),) + \
 		tuple(t.float().contiguous() for t in (near, mid, far))
-	params = [p.contiguous() for p in (raw, dA, cA, sh)]
-	rgb, T, depth, stats = march_extension().march_forward(graph.points, graph.offsets, graph.adj,
-														   *[p.detach() for p in params], int(sh_deg), *rays,
-														   float(dt), int(n_bg), float(t_thresh), float(w_thresh))
-	return _forward_only(rgb, params), _forward_only(T, params), depth, stats
+	params = [p.float().contiguous() for p in (raw, dA, cA, sh)]
+	cfg = (int(sh_deg), float(dt), int(n_bg), float(t_thresh), float(w_thresh))
+	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
+		return march_extension().march_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
+											   cfg[0], *rays, *cfg[1:])
+	return _March.apply(*params, graph, rays, cfg)
