@@ -14,7 +14,8 @@ Other rows of the path, each as one JSON line of the same form (not the headline
   --workload pack     pack_foam with Z-order renumbering on config 3 (the step before the kernel)
   --workload grad     the backward of the field operators on the frame of --workload field
   --workload traverse the cell traversal alone (foam_infer stage 0) on config 3 in both layouts: one ray per lane
-                      (foam_infer) against 16 lanes per ray testing a cell's faces in parallel
+                      (foam_infer) against a group of lanes per ray testing a cell's faces in parallel (--lanes)
+  --workload march-grad  a training step of the uniform march on config 5: forward + backward of --batch rays
   --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
                       one 1920x1080 frame at 64 stratified samples per ray (render_rays' first round)
 """
@@ -126,7 +127,7 @@ def main():
 	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
 	ap.add_argument('--workload', default='foam',
-					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse'],
+					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse', 'march-grad'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
 	args = ap.parse_args()
@@ -149,6 +150,8 @@ def main():
 		return bench_pack(args)
 	if args.workload == 'traverse':
 		return bench_traverse(args)
+	if args.workload == 'march-grad':
+		return bench_march_grad(args)
 	if args.workload == 'grad':
 		return bench_grad(args)
 	bench_foam(args)
@@ -336,6 +339,102 @@ def emit(metric, value, unit, args, ms, config, roofline, cpu, dtype='f32'):
 		   'vs_baseline': None, 'dtype': dtype, 'data': 'synthetic', 'config': config, 'roofline': roofline,
 		   'cpu_baseline': cpu}
 	print(json.dumps(res), flush=True)
+
+
+def bench_march_grad(args):
+	"""A training step of the uniform march (render_rays_uniform under autograd, train.py:114,132) on config 5:
+	--batch rays (train.py's default 4096) drawn at random from the config-5 ray batch, dt = 1/512 and 64 disparity
+	steps (train.py:35-36); march_forward, then march_backward with random upstream gradients of rgb and T. value =
+	rays per second through forward + backward. A second leg times 16 x the batch, since 4,096 rays (64 waves of one
+	ray per lane) occupy a fraction of the 1,024 SIMDs. CPU baseline: the C oracle's backward (one thread) on a
+	bounded subset of the batch.
+
+	Algorithmic bytes of the backward launch (E = mean self-inclusive neighbourhood, SHB = 12 (deg + 1)^2): the
+	forward's (rays 56 B; per walk step 8 + 16 E; per sample 8 + 44 E; per coloured sample E (24 + SHB)) again for
+	the re-march, plus the gradient pass: per sample E (16 + 28) record reads and E 28 B of raw and density-conic
+	gradient, per coloured sample E (SHB + 24 + SHB) SH reads and colour-conic and SH gradient."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, grid, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	sc = scenes.make_scene(5, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	o_np, d_np = sc.ray_batch
+	dt, n_bg = 1 / 512, 64
+	floor = 0.5 * dt
+	dA = ext.conic(model.d_log_scale, model.d_quat, floor).contiguous()
+	cA = ext.conic(model.c_log_scale, model.c_quat, floor).contiguous()
+	sh = model.sh().contiguous()
+	me = ext.march_extension()
+	g = model.graph
+	sites = g.points
+	locator = grid.SiteGrid(sites)
+	stream = torch.cuda.current_stream(dev)
+	E = 1.0 + len(sc.adj) / sc.n_sites
+	SHB = 12 * (sc.sh_deg + 1) ** 2
+	rng = np.random.default_rng(0)
+	legs = {}
+	for B in (args.batch, 16 * args.batch):
+		pick = rng.choice(len(o_np), B, replace=False)
+		o, d = torch.from_numpy(o_np[pick]).to(dev), torch.from_numpy(d_np[pick]).to(dev)
+		start = locator.nearest(o)
+		near, mid, far = render.ray_bounds(o, d, 0.02, sc.far_radius)
+		rays = (o, d, start, near, mid, far)
+		fwd_args = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, dt, n_bg, 1e-4, 1e-4)
+		gen = torch.Generator(device=dev).manual_seed(0)
+		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
+		f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args), args.steps, args.warmup, stream)
+		rgb, T, _, stats = out
+		b_ms, grads, _ = time_steps(lambda: me.march_backward(*fwd_args, rgb, T, g_rgb, g_T), args.steps,
+									args.warmup, stream)
+		st = stats.double()
+		fwd_bytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
+						  st[:, 1].sum() * E * (24 + SHB))
+		bwd_bytes = fwd_bytes + float(st[:, 0].sum() * E * (44 + 28) + st[:, 1].sum() * E * (2 * SHB + 24))
+		legs[B] = dict(fwd=float(np.mean(f_ms)), bwd=float(np.mean(b_ms)), bytes=bwd_bytes, rays=rays, rgb=rgb, T=T,
+					   g_rgb=g_rgb, g_T=g_T, samples=float(st[:, 0].mean()), coloured=float(st[:, 1].mean()))
+		L = legs[B]
+		log(f'{B} rays: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms ({bwd_bytes / L["bwd"] / 1e6:.0f} GB/s '
+			f'algorithmic); samples/ray {L["samples"]:.1f}, coloured {L["coloured"]:.1f}')
+	L = legs[args.batch]
+	ms = L['fwd'] + L['bwd']
+	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
+	cpu = None
+	if args.cpu_seconds > 0:
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		host = [x.cpu().numpy() for x in (g.points, g.offsets, g.adj, model.raw, dA, cA, sh)]
+		rays = [x.cpu().numpy() for x in L['rays']]
+		up = [x.cpu().numpy() for x in (L['rgb'], L['T'], L['g_rgb'], L['g_T'])]
+		B = args.batch
+		t1 = time.perf_counter()
+		probe = np.arange(0, B, max(1, B // 16))
+		oracle.march_backward(*host, sc.sh_deg, *[r[probe] for r in rays], dt, n_bg, *[u[probe] for u in up])
+		rate = len(probe) / max(time.perf_counter() - t1, 1e-6)
+		sel = np.arange(0, B, max(1, int(B / (rate * args.cpu_seconds))))
+		t1 = time.perf_counter()
+		oracle.march_backward(*host, sc.sh_deg, *[r[sel] for r in rays], dt, n_bg, *[u[sel] for u in up])
+		secs = time.perf_counter() - t1
+		cpu = {'value': round(len(sel) / secs / 1e3, 4), 'unit': 'Krays/s (backward only)', 'cores': 1,
+			   'kind': 'port', 'sample': f'every {B // len(sel)}th ray of the batch ({len(sel)} rays), C oracle '
+										 f'march_backward, one thread'}
+	big = legs[16 * args.batch]
+	emit('Mrays/s through march forward + backward (training batch)', mrays_per_s(args.batch, ms), 'Mrays/s', args, ms,
+		 {'workload': f'config 5 uniform march training step: {args.batch} random rays of the config-5 batch, dt = '
+					  f'1/512, 64 bg steps, march_forward + march_backward', 'sites': sc.n_sites,
+		  'rays_per_step': args.batch, 'forward_ms': round(L['fwd'], 4), 'backward_ms': round(L['bwd'], 4),
+		  'samples_per_ray': round(L['samples'], 2), 'coloured_per_ray': round(L['coloured'], 2),
+		  f'rays_{16 * args.batch}': {'forward_ms': round(big['fwd'], 3), 'backward_ms': round(big['bwd'], 3),
+									  'Mrays_per_s': round(mrays_per_s(16 * args.batch, big['fwd'] + big['bwd']), 3)}},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
+		  'frac': round(achieved / 8000.0, 4), 'traffic': None, 'kernel': 'march_backward_kernel',
+		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
+
+
+def mrays_per_s(B, ms):
+	return B / (ms * 1e-3) / 1e6
 
 
 def bench_locate(args):

@@ -128,8 +128,10 @@ int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offse
  *   and g_rgb f32 (B, 3), g_T f32 (B) their upstream gradients.
  *   -> g_raw f32 (N), g_dA f32 (N, 6), g_cA f32 (N, 6), g_sh f32 (N, 16, 3), overwritten (zeroed first). The sums
  *   use fp32 atomics, so they agree with a sequential sum to rounding, not bitwise.
- * work: as for vgr_march_forward (vgr_march_work_size(N, sh_deg) bytes, 256-byte aligned).
+ * work: device scratch of vgr_march_backward_work_size(N, sh_deg) bytes (the forward's site blocks plus a 256-byte
+ * gradient block per site), 256-byte aligned.
  */
+int64_t vgr_march_backward_work_size(int64_t n_sites, int64_t sh_deg);
 int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                        int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
                        int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,

@@ -48,6 +48,26 @@ def test_march_backward_matches_oracle(gpu, sh_deg, t_thresh, w_thresh):
 	assert (got[3][:, (sh_deg + 1) ** 2:] == 0).all()
 
 
+def test_march_backward_wave_atomics_match_oracle(gpu):
+	"""16,384 rays, where the launch shares each row of atomics across the wave: against the oracle, and against the
+	per-lane atomics of the same rays in two launches of 8,192 (whose gradients add)."""
+	B = 16384
+	f, rays, dA, cA, fx, field, rt, rgb, Tt = case(gpu, 3, 1e-4, 1e-4, B=B)
+	rng = np.random.default_rng(8)
+	g_rgb = T(rng.normal(size=(B, 3)).astype(np.float32), gpu)
+	g_T = T(rng.normal(size=B).astype(np.float32), gpu)
+	got = fx.march_backward(*field, 3, *rt, DT, NBG, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T)
+	ref = oracle.march_backward(f.points, f.offsets, f.adj, f.raw, dA, cA, f.sh, 3, *rays, DT, NBG, rgb.cpu().numpy(),
+								Tt.cpu().numpy(), g_rgb.cpu().numpy(), g_T.cpu().numpy())
+	for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref):
+		assert rel(a.cpu().numpy(), r) < 2e-5, name
+	halves = [fx.march_backward(*field, 3, *[x[s].contiguous() for x in rt], DT, NBG, 1e-4, 1e-4, rgb[s].contiguous(),
+								Tt[s].contiguous(), g_rgb[s].contiguous(), g_T[s].contiguous())
+			  for s in (slice(0, B // 2), slice(B // 2, None))]
+	for name, a, h0, h1 in zip(('raw', 'dA', 'cA', 'sh'), got, *halves):
+		assert rel((h0 + h1).cpu().numpy(), a.cpu().numpy()) < 1e-5, name
+
+
 def test_march_autograd_matches_oracle(gpu):
 	"""ext.march with gradients on, as training calls it (ext.py:150-182): loss = <rgb, g_rgb> + <T, g_T>."""
 	f, rays, dA, cA, fx, field, rt, rgb0, T0 = case(gpu, 3, 1e-4, 1e-4)

@@ -25,6 +25,7 @@ SIGNATURES = {
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
+	'vgr_march_backward_work_size': [_I64, _I64],
 	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
@@ -53,7 +54,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 _lib = None
 
 
@@ -71,6 +72,7 @@ def load():
 		lib.vgr_last_error.restype = ctypes.c_char_p
 		lib.vgr_grid_work_size.restype = ctypes.c_int64
 		lib.vgr_march_work_size.restype = ctypes.c_int64
+		lib.vgr_march_backward_work_size.restype = ctypes.c_int64
 		lib.vgr_field_work_size.restype = ctypes.c_int64
 		lib.vgr_color_backward_work_size.restype = ctypes.c_int64
 		lib.vgr_density_backward_work_size.restype = ctypes.c_int64

@@ -234,7 +234,7 @@ class _MarchExtension:
 		n = points.numel() // 3
 		g = [torch.empty(n, device=dev), torch.empty(n, 6, device=dev), torch.empty(n, 6, device=dev),
 			 torch.empty(n, 16, 3, device=dev)]
-		work_bytes = int(_lib.load().vgr_march_work_size(n, int(sh_deg)))
+		work_bytes = int(_lib.load().vgr_march_backward_work_size(n, int(sh_deg)))
 		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
 			call('vgr_march_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
