@@ -385,20 +385,25 @@ def bench_march_grad(args):
 		fwd_args = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, dt, n_bg, 1e-4, 1e-4)
 		gen = torch.Generator(device=dev).manual_seed(0)
 		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
-		f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args), args.steps, args.warmup, stream)
-		rgb, T, _, stats = out
-		b_ms, grads, _ = time_steps(lambda: me.march_backward(*fwd_args, rgb, T, g_rgb, g_T), args.steps,
-									args.warmup, stream)
-		st = stats.double()
-		fwd_bytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
-						  st[:, 1].sum() * E * (24 + SHB))
-		bwd_bytes = fwd_bytes + float(st[:, 0].sum() * E * (44 + 28) + st[:, 1].sum() * E * (2 * SHB + 24))
-		legs[B] = dict(fwd=float(np.mean(f_ms)), bwd=float(np.mean(b_ms)), bytes=bwd_bytes, rays=rays, rgb=rgb, T=T,
-					   g_rgb=g_rgb, g_T=g_T, samples=float(st[:, 0].mean()), coloured=float(st[:, 1].mean()))
-		L = legs[B]
-		log(f'{B} rays: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms ({bwd_bytes / L["bwd"] / 1e6:.0f} GB/s '
-			f'algorithmic); samples/ray {L["samples"]:.1f}, coloured {L["coloured"]:.1f}')
-	L = legs[args.batch]
+		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 16384 rays
+			f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args, lanes=lanes), args.steps, args.warmup,
+									  stream)
+			rgb, T, _, stats = out
+			b_ms, grads, _ = time_steps(lambda: me.march_backward(*fwd_args, rgb, T, g_rgb, g_T, lanes=lanes),
+										args.steps, args.warmup, stream)
+			st = stats.double()
+			fwd_bytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
+							  st[:, 1].sum() * E * (24 + SHB))
+			bwd_bytes = fwd_bytes + float(st[:, 0].sum() * E * (44 + 28) + st[:, 1].sum() * E * (2 * SHB + 24))
+			legs[B, lanes] = dict(fwd=float(np.mean(f_ms)), bwd=float(np.mean(b_ms)), bytes=bwd_bytes, rays=rays,
+								  rgb=rgb, T=T, g_rgb=g_rgb, g_T=g_T, samples=float(st[:, 0].mean()),
+								  coloured=float(st[:, 1].mean()))
+			L = legs[B, lanes]
+			log(f'{B} rays, {lanes} lane(s) per ray: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms '
+				f'({bwd_bytes / L["bwd"] / 1e6:.0f} GB/s algorithmic); samples/ray {L["samples"]:.1f}, coloured '
+				f'{L["coloured"]:.1f}')
+	auto = 16 if args.batch < 16384 else 1
+	L = legs[args.batch, auto]
 	ms = L['fwd'] + L['bwd']
 	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
 	cpu = None
@@ -420,14 +425,15 @@ def bench_march_grad(args):
 		cpu = {'value': round(len(sel) / secs / 1e3, 4), 'unit': 'Krays/s (backward only)', 'cores': 1,
 			   'kind': 'port', 'sample': f'every {B // len(sel)}th ray of the batch ({len(sel)} rays), C oracle '
 										 f'march_backward, one thread'}
-	big = legs[16 * args.batch]
+	layouts = {f'{B} rays, {lanes} lanes/ray': {'forward_ms': round(v['fwd'], 3), 'backward_ms': round(v['bwd'], 3),
+												'Mrays_per_s': round(mrays_per_s(B, v['fwd'] + v['bwd']), 3)}
+			   for (B, lanes), v in legs.items()}
 	emit('Mrays/s through march forward + backward (training batch)', mrays_per_s(args.batch, ms), 'Mrays/s', args, ms,
 		 {'workload': f'config 5 uniform march training step: {args.batch} random rays of the config-5 batch, dt = '
 					  f'1/512, 64 bg steps, march_forward + march_backward', 'sites': sc.n_sites,
-		  'rays_per_step': args.batch, 'forward_ms': round(L['fwd'], 4), 'backward_ms': round(L['bwd'], 4),
-		  'samples_per_ray': round(L['samples'], 2), 'coloured_per_ray': round(L['coloured'], 2),
-		  f'rays_{16 * args.batch}': {'forward_ms': round(big['fwd'], 3), 'backward_ms': round(big['bwd'], 3),
-									  'Mrays_per_s': round(mrays_per_s(16 * args.batch, big['fwd'] + big['bwd']), 3)}},
+		  'rays_per_step': args.batch, 'lanes_per_ray': auto, 'forward_ms': round(L['fwd'], 4),
+		  'backward_ms': round(L['bwd'], 4), 'samples_per_ray': round(L['samples'], 2),
+		  'coloured_per_ray': round(L['coloured'], 2), 'layouts': layouts},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
 		  'frac': round(achieved / 8000.0, 4), 'traffic': None, 'kernel': 'march_backward_kernel',
 		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)

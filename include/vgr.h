@@ -122,12 +122,28 @@ int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offse
                       int32_t* trace, int64_t trace_cap, void* work, int64_t work_bytes, void* stream);
 
 /*
+ * vgr_march_forward with the ray layout chosen by the caller: lanes_per_ray 1 (one ray per lane), 16 (a group of
+ * 16 lanes per ray, one neighbour per lane: for small batches, whose launches are bound by each ray's serial chain
+ * of loads) or 0 (by batch size: 16 below 16384 rays, else 1, which is what vgr_march_forward does). The layouts
+ * visit the same sites; their sums differ in the order of addition. Same reference function as vgr_march_forward.
+ */
+int vgr_march_forward_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                            int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                            int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                            const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays, double dt,
+                            int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T, float* depth,
+                            int32_t* stats, int32_t* trace, int64_t trace_cap, int64_t lanes_per_ray, void* work,
+                            int64_t work_bytes, void* stream);
+
+/*
  * Fused uniform-step march (backward: re-marches every ray). Replaces march_backward() of csrc/march.cu:405-428
  * (kernel :264-345, export :433), called by _March.backward (ext.py:162-169) when training through ext.march.
  *   The field, rays and march parameters are the forward's; rgb f32 (B, 3) and T f32 (B) are the forward's outputs
  *   and g_rgb f32 (B, 3), g_T f32 (B) their upstream gradients.
  *   -> g_raw f32 (N), g_dA f32 (N, 6), g_cA f32 (N, 6), g_sh f32 (N, 16, 3), overwritten (zeroed first). The sums
  *   use fp32 atomics, so they agree with a sequential sum to rounding, not bitwise.
+ * lanes_per_ray: the forward's layout (0, 1 or 16 as for vgr_march_forward_lanes); it must be the one that produced
+ * rgb and T, since the backward replays that forward's sums.
  * work: device scratch of vgr_march_backward_work_size(N, sh_deg) bytes (the forward's site blocks plus a 256-byte
  * gradient block per site), 256-byte aligned.
  */
@@ -137,8 +153,8 @@ int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offs
                        int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
                        const float* mid_t, const float* far_t, int64_t n_rays, double dt, int64_t n_bg,
                        double t_thresh, double w_thresh, const float* rgb, const float* T, const float* g_rgb,
-                       const float* g_T, float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work,
-                       int64_t work_bytes, void* stream);
+                       const float* g_T, float* g_raw, float* g_dA, float* g_cA, float* g_sh, int64_t lanes_per_ray,
+                       void* work, int64_t work_bytes, void* stream);
 
 /*
  * Nearest site of every sorted ray sample o + z d by a greedy walk (strict <). Replaces walk() of

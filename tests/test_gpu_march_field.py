@@ -16,23 +16,24 @@ def T(a, dev):
 	return torch.as_tensor(np.ascontiguousarray(a), device=dev)
 
 
-def gpu_march(dev, f, dA, cA, rays, dt, n_bg, t_thresh, w_thresh, trace_cap=0, sh=None, sh_deg=3):
+def gpu_march(dev, f, dA, cA, rays, dt, n_bg, t_thresh, w_thresh, trace_cap=0, sh=None, sh_deg=3, lanes=0):
 	o, d, start, near, mid, far = rays
 	out = ext.march_extension().march_forward(
 		T(f.points, dev), T(f.offsets, dev), T(f.adj, dev), T(f.raw, dev), T(dA, dev), T(cA, dev),
 		T(f.sh if sh is None else sh, dev), sh_deg, T(o, dev), T(d, dev), T(start, dev), T(near, dev), T(mid, dev),
-		T(far, dev), dt, n_bg, t_thresh, w_thresh, trace_cap=trace_cap)
+		T(far, dev), dt, n_bg, t_thresh, w_thresh, trace_cap=trace_cap, lanes=lanes)
 	torch.cuda.synchronize()
 	return [x.cpu().numpy() for x in out]
 
 
+@pytest.mark.parametrize('lanes', [1, 16])
 @pytest.mark.parametrize('thresholds', [(0.0, -1.0), (1e-4, 1e-4)])
-def test_march_vs_oracle(gpu, thresholds):
-	"""test_march.py:33-55 setup (300 sites, B=64 -> 256, dt=0.05, n_bg=8, floor 0.01)."""
+def test_march_vs_oracle(gpu, thresholds, lanes):
+	"""test_march.py:33-55 setup (300 sites, B=64 -> 256, dt=0.05, n_bg=8, floor 0.01), in both ray layouts."""
 	f = Field(seed=1, n=300)
 	rays = f.rays(B=256, seed=1)
 	dA, cA = f.conics(0.01)
-	rgb, Tt, depth, stats, trace = gpu_march(gpu, f, dA, cA, rays, 0.05, 8, *thresholds, trace_cap=256)
+	rgb, Tt, depth, stats, trace = gpu_march(gpu, f, dA, cA, rays, 0.05, 8, *thresholds, trace_cap=256, lanes=lanes)
 	r = oracle.march_forward(f.points, f.offsets, f.adj, f.raw, dA, cA, f.sh, 3, *rays, 0.05, 8, *thresholds,
 							 trace_cap=256)
 	np.testing.assert_allclose(rgb, r['rgb'], atol=1e-4)
@@ -58,6 +59,25 @@ def test_march_default_step_config1(gpu):
 							 mid.cpu().numpy(), far.cpu().numpy(), 1 / 512, 64)
 	np.testing.assert_allclose(out['rgb'].cpu().numpy(), r['rgb'] + r['T'][:, None] * 0.5, atol=1e-4)
 	np.testing.assert_allclose(out['acc'].cpu().numpy(), 1 - r['T'], atol=1e-4)
+
+
+@pytest.mark.parametrize('sh_deg', [3, 1])
+def test_march_layouts_agree(gpu, sh_deg):
+	"""One ray per lane and 16 lanes per ray on the same rays (default thresholds, 1/64 steps): the same sites in
+	the same order, the same counts, colours within 1e-5 (the sums are added in another order)."""
+	f = Field(seed=4, n=400, sh_deg=sh_deg)
+	rays = f.rays(B=512, seed=4)
+	dA, cA = f.conics(0.01)
+	a = gpu_march(gpu, f, dA, cA, rays, 1 / 64, 16, 1e-4, 1e-4, trace_cap=512, sh_deg=sh_deg, lanes=1)
+	b = gpu_march(gpu, f, dA, cA, rays, 1 / 64, 16, 1e-4, 1e-4, trace_cap=512, sh_deg=sh_deg, lanes=16)
+	assert a[3][:, 0].max() < 512
+	np.testing.assert_array_equal(a[4], b[4])
+	np.testing.assert_array_equal(a[3], b[3])
+	np.testing.assert_allclose(a[0], b[0], atol=1e-5)
+	np.testing.assert_allclose(a[1], b[1], atol=1e-5)
+	np.testing.assert_allclose(a[2], b[2], atol=1e-4)
+	with pytest.raises(RuntimeError, match='lanes_per_ray'):
+		gpu_march(gpu, f, dA, cA, rays, 1 / 64, 16, 1e-4, 1e-4, lanes=8)
 
 
 def test_march_errors(gpu):

@@ -21,26 +21,29 @@ def T(a, dev):
 	return torch.as_tensor(np.ascontiguousarray(a), device=dev)
 
 
-def case(dev, sh_deg, t_thresh, w_thresh, B=192, seed=5):
+def case(dev, sh_deg, t_thresh, w_thresh, B=192, seed=5, lanes=0):
 	f = Field(seed=seed, n=300, sh_deg=sh_deg)
 	rays = f.rays(B=B, seed=seed)
 	dA, cA = f.conics(0.01)
 	fx = ext.march_extension()
 	field = [T(a, dev) for a in (f.points, f.offsets, f.adj, f.raw, dA, cA, f.sh)]
 	rt = [T(a, dev) for a in rays]
-	rgb, Tt, _, _ = fx.march_forward(*field, sh_deg, *rt, DT, NBG, t_thresh, w_thresh)
+	rgb, Tt, _, _ = fx.march_forward(*field, sh_deg, *rt, DT, NBG, t_thresh, w_thresh, lanes=lanes)
 	return f, rays, dA, cA, fx, field, rt, rgb, Tt
 
 
+@pytest.mark.parametrize('lanes', [1, 16])
 @pytest.mark.parametrize('t_thresh,w_thresh', [(0.0, -1.0), (1e-4, 1e-4)])
 @pytest.mark.parametrize('sh_deg', [3, 2, 0])
-def test_march_backward_matches_oracle(gpu, sh_deg, t_thresh, w_thresh):
-	f, rays, dA, cA, fx, field, rt, rgb, Tt = case(gpu, sh_deg, t_thresh, w_thresh)
+def test_march_backward_matches_oracle(gpu, sh_deg, t_thresh, w_thresh, lanes):
+	"""Both ray layouts (one ray per lane; 16 lanes per ray, one neighbour per lane), each replaying its own forward."""
+	f, rays, dA, cA, fx, field, rt, rgb, Tt = case(gpu, sh_deg, t_thresh, w_thresh, lanes=lanes)
 	rng = np.random.default_rng(3)
 	g_rgb = rng.normal(size=(len(rays[0]), 3)).astype(np.float32)
 	g_T = rng.normal(size=len(rays[0])).astype(np.float32)
 	g_rgb[:7] = 0  # rays without an upstream colour gradient still pass dL/dT
-	got = fx.march_backward(*field, sh_deg, *rt, DT, NBG, t_thresh, w_thresh, rgb, Tt, T(g_rgb, gpu), T(g_T, gpu))
+	got = fx.march_backward(*field, sh_deg, *rt, DT, NBG, t_thresh, w_thresh, rgb, Tt, T(g_rgb, gpu), T(g_T, gpu),
+							lanes=lanes)
 	ref = oracle.march_backward(f.points, f.offsets, f.adj, f.raw, dA, cA, f.sh, sh_deg, *rays, DT, NBG,
 								rgb.cpu().numpy(), Tt.cpu().numpy(), g_rgb, g_T, t_thresh, w_thresh)
 	for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref):
@@ -52,17 +55,17 @@ def test_march_backward_wave_atomics_match_oracle(gpu):
 	"""16,384 rays, where the launch shares each row of atomics across the wave: against the oracle, and against the
 	per-lane atomics of the same rays in two launches of 8,192 (whose gradients add)."""
 	B = 16384
-	f, rays, dA, cA, fx, field, rt, rgb, Tt = case(gpu, 3, 1e-4, 1e-4, B=B)
+	f, rays, dA, cA, fx, field, rt, rgb, Tt = case(gpu, 3, 1e-4, 1e-4, B=B, lanes=1)
 	rng = np.random.default_rng(8)
 	g_rgb = T(rng.normal(size=(B, 3)).astype(np.float32), gpu)
 	g_T = T(rng.normal(size=B).astype(np.float32), gpu)
-	got = fx.march_backward(*field, 3, *rt, DT, NBG, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T)
+	got = fx.march_backward(*field, 3, *rt, DT, NBG, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T, lanes=1)
 	ref = oracle.march_backward(f.points, f.offsets, f.adj, f.raw, dA, cA, f.sh, 3, *rays, DT, NBG, rgb.cpu().numpy(),
 								Tt.cpu().numpy(), g_rgb.cpu().numpy(), g_T.cpu().numpy())
 	for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref):
 		assert rel(a.cpu().numpy(), r) < 2e-5, name
 	halves = [fx.march_backward(*field, 3, *[x[s].contiguous() for x in rt], DT, NBG, 1e-4, 1e-4, rgb[s].contiguous(),
-								Tt[s].contiguous(), g_rgb[s].contiguous(), g_T[s].contiguous())
+								Tt[s].contiguous(), g_rgb[s].contiguous(), g_T[s].contiguous(), lanes=1)
 			  for s in (slice(0, B // 2), slice(B // 2, None))]
 	for name, a, h0, h1 in zip(('raw', 'dA', 'cA', 'sh'), got, *halves):
 		assert rel((h0 + h1).cpu().numpy(), a.cpu().numpy()) < 1e-5, name

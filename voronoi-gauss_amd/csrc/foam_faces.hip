@@ -53,13 +53,8 @@ __device__ __forceinline__ void keep_min(const FacesScene& S, float u, int j, fl
 }
 
 template <int CTRL>
-__device__ __forceinline__ int row_perm(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-
-template <int CTRL>
 __device__ __forceinline__ void reduce_step(const FacesScene& S, float& t, int& k) {
-    const float u = __int_as_float(row_perm<CTRL>(__float_as_int(t)));
+    const float u = row_perm<CTRL>(t);
     const int j = row_perm<CTRL>(k);
     keep_min(S, u, j, t, k);
 }
@@ -68,10 +63,10 @@ __device__ __forceinline__ void reduce_step(const FacesScene& S, float& t, int& 
 template <int G>
 __device__ __forceinline__ void group_min(const FacesScene& S, float& t, int& k) {
     static_assert(G == 4 || G == 8 || G == 16, "group width");
-    reduce_step<0xB1>(S, t, k);                  // quad_perm [1, 0, 3, 2]: lane ^ 1
-    reduce_step<0x4E>(S, t, k);                  // quad_perm [2, 3, 0, 1]: lane ^ 2
-    if constexpr (G >= 8) reduce_step<0x141>(S, t, k);   // row_half_mirror: i <-> 7 - i within 8
-    if constexpr (G >= 16) reduce_step<0x140>(S, t, k);  // row_mirror: i <-> 15 - i within 16
+    reduce_step<kXor1>(S, t, k);
+    reduce_step<kXor2>(S, t, k);
+    if constexpr (G >= 8) reduce_step<kHalfMirror>(S, t, k);
+    if constexpr (G >= 16) reduce_step<kMirror>(S, t, k);
 }
 
 template <int G, bool TRACE>

@@ -568,17 +568,6 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
 // (a few ulps). Per lane this layout runs the same face and field arithmetic as one ray per lane, but 64 / G rays
 // per wave keep more independent loads in flight per wave, and a wave's loads of one cell are contiguous.
 
-template <int CTRL>
-__device__ __forceinline__ int row_perm(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float row_perm(float v) {
-    return __int_as_float(row_perm<CTRL>(__float_as_int(v)));
-}
-
-constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141;  // DPP: quad_perm [1,0,3,2], [2,3,0,1]; row_half_mirror
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 

@@ -716,6 +716,377 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
+// -------------------------------------------------------------------------------------- group layout (small batches)
+//
+// A training batch of a few thousand rays fills a fraction of the GPU with one ray per lane (4,096 rays are 64
+// waves for 1,024 SIMDs), and each ray's samples form a serial chain, so such a launch lasts as long as its slowest
+// ray's chain of dependent loads. With kGroup = 16 lanes per ray (4 rays per wave), lane g takes neighbours g,
+// g + 16, ... of every neighbourhood, so one round of loads covers a whole neighbourhood (mean 16.5) and the chain
+// per sample shrinks from a neighbourhood's length of loads to about one. Per sample: one round at the walk's site
+// evaluates the walk's argmin, the density and the colour minimum; the walk moves and repeats the round until its
+// site wins or the walk cap is reached (march.cu:157-180); one more round blends a coloured sample's colour (and in
+// the backward, one pushes its gradients). Reductions are DPP butterflies inside the 16-lane row: the lexicographic
+// (distance, index) minimum, sums and the minimum. Their pairwise operations are commutative, so all lanes of a
+// group hold the same bits and composite in step. Sites and walks are those of a sequential scan; the sums differ
+// from it by their order of addition (a few ulps).
+
+constexpr int kGroup = 16;
+
+template <int CTRL>
+__device__ __forceinline__ void argmin_step(float& d, int& k) {
+    const float d2 = row_perm<CTRL>(d);
+    const int k2 = row_perm<CTRL>(k);
+    if (d2 < d || (d2 == d && k2 < k)) d = d2, k = k2;
+}
+
+__device__ __forceinline__ void row_argmin(float& d, int& k) {
+    argmin_step<kXor1>(d, k);
+    argmin_step<kXor2>(d, k);
+    argmin_step<kHalfMirror>(d, k);
+    argmin_step<kMirror>(d, k);
+}
+
+__device__ __forceinline__ float row_sum(float v) {
+    v = v + row_perm<kXor1>(v);
+    v = v + row_perm<kXor2>(v);
+    v = v + row_perm<kHalfMirror>(v);
+    return v + row_perm<kMirror>(v);
+}
+
+__device__ __forceinline__ float row_min(float v) {
+    v = fminf(v, row_perm<kXor1>(v));
+    v = fminf(v, row_perm<kXor2>(v));
+    v = fminf(v, row_perm<kHalfMirror>(v));
+    return fminf(v, row_perm<kMirror>(v));
+}
+
+struct GroupRound {
+    float d, sigma, mmin;
+    int k;
+};
+
+// Walk test, density and colour minimum of point x over the neighbourhood of site i, reduced over the group.
+template <int BLK>
+__device__ __forceinline__ void group_round(const MarchField& F, int i, const float (&x)[3], int g, GroupRound& Q) {
+    const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
+    float bd = kInf, s = 0.f, mm = kInf;
+    int bk = INT_MAX;
+    for (int e = g; e < n; e += kGroup) {
+        const int k = neighbor(F, i, e0, e);
+        const SiteRec rc = site_rec<BLK>(F, k);
+        float v[3];
+        offset_to(rc.q0, x, v);
+        const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+        if (dk < bd || (dk == bd && k < bk)) bd = dk, bk = k;
+        s += fexp(rc.q0.w - 0.5f * density_m(rc, v));
+        mm = fminf(mm, color_m(rc.q2, rc.q3, v));
+    }
+    row_argmin(bd, bk);
+    Q.d = bd, Q.k = bk, Q.sigma = row_sum(s), Q.mmin = row_min(mm);
+}
+
+// The neighbourhood of the group's current cell, as the lanes hold it: lane g's slots are neighbours g and g + 16
+// (k = -1 past the end) with their unclamped colours 1/2 + SH_k(d) . b, which depend only on the site and the ray,
+// evaluated once per cell visit at its first coloured sample. Neighbours beyond the two slots (cells of more than 32
+// neighbours) are read directly at every sample.
+constexpr int kSlots = 2;
+
+struct GroupCell {
+    int cell, e0, n;
+    int k[kSlots];
+    float c[kSlots][3];
+    bool col_ok;
+};
+
+__device__ __forceinline__ void enter_cell(const MarchField& F, int cell, int g, GroupCell& C) {
+    C.cell = cell, C.e0 = F.offsets[cell], C.n = F.offsets[cell + 1] - C.e0 + 1, C.col_ok = false;
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) {
+        const int e = g + kGroup * s;
+        C.k[s] = e < C.n ? neighbor(F, cell, C.e0, e) : -1;
+    }
+}
+
+template <int NV>
+__device__ __forceinline__ void cell_colours(const MarchField& F, const float (&b)[16], int nb, GroupCell& C) {
+    if (C.col_ok) return;
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s)
+        if (C.k[s] >= 0) sh_eval_n<NV>(F.rec + block_vec4(NV) * static_cast<int64_t>(C.k[s]) + kRec, b, nb, C.c[s]);
+    C.col_ok = true;
+}
+
+// Normalised colour blend at x over the cell's neighbourhood (weights exp(-(m_k - m_min) / 2)): 1 / sum of weights
+// and the colour.
+template <int NV>
+__device__ __forceinline__ void group_colour(const MarchField& F, GroupCell& Cc, const float (&x)[3],
+                                             const float (&b)[16], int nb, float mmin, int g, float& inv_a,
+                                             float (&C)[3]) {
+    cell_colours<NV>(F, b, nb, Cc);
+    float A = 0.f, cs[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) {
+        if (Cc.k[s] >= 0) {
+            const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(Cc.k[s]);
+            const float4 p = r[0], c0 = r[2], c1 = r[3];
+            float v[3];
+            offset_to(p, x, v);
+            const float a = fexp(-0.5f * (color_m(c0, c1, v) - mmin));
+            A += a;
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) cs[ch] += a * fmaxf(Cc.c[s][ch], 0.f);
+        }
+    }
+    for (int e = g + kGroup * kSlots; e < Cc.n; e += kGroup) {
+        const int k = neighbor(F, Cc.cell, Cc.e0, e);
+        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const float4 p = r[0], c0 = r[2], c1 = r[3];
+        float c[3], v[3];
+        sh_eval_n<NV>(r + kRec, b, nb, c);
+        offset_to(p, x, v);
+        const float a = fexp(-0.5f * (color_m(c0, c1, v) - mmin));
+        A += a;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) cs[ch] += a * fmaxf(c[ch], 0.f);
+    }
+    inv_a = 1.f / row_sum(A);
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) C[ch] = row_sum(cs[ch]) * inv_a;
+}
+
+// Per ray: the sample loop of march_ray with one sample per round.
+template <int NV, bool TRACE>
+__device__ void march_ray_group(const MarchField& F, const MarchParams& M, const MarchRays& R, const MarchOut& O,
+                                int64_t r, int cur, int g) {
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
+    const int n_in = mid > near ? static_cast<int>(ceilf((mid - near) / M.dt)) : 0;
+    const int n_total = n_in + M.n_bg;
+    const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    int n_samples = 0, n_color = 0, walk_steps = 0, moves = 0;
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    GroupCell Cc;
+    Cc.cell = -1;
+    for (int k = 0; k < n_total;) {
+        float t, delta, x[3];
+        sample_at(near, mid, far, n_in, M, k, t, delta);
+        point_at(o, d, t, x);
+        GroupRound Q;
+        group_round<block_vec4(NV)>(F, cur, x, g, Q);
+        if (Q.k != cur && moves < kWalkCap) {
+            cur = Q.k, ++walk_steps, ++moves;
+            continue;
+        }
+        moves = 0;
+        if (TRACE && g == 0 && n_samples < O.trace_cap) O.trace[r * O.trace_cap + n_samples] = cur;
+        const float alpha = 1.f - fexp(-Q.sigma * delta);
+        const float w = T * alpha;
+        ++n_samples;
+        if (w > M.w_thresh) {
+            if (Cc.cell != cur) enter_cell(F, cur, g, Cc);
+            float inv_a, C[3];
+            group_colour<NV>(F, Cc, x, b, nb, Q.mmin, g, inv_a, C);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += w * C[a];
+            dep += w * t;
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        ++k;
+        if (T < M.t_thresh) break;
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
+        O.T[r] = T;
+        O.depth[r] = dep;
+        O.stats[3 * r] = n_samples, O.stats[3 * r + 1] = n_color, O.stats[3 * r + 2] = walk_steps;
+    }
+}
+
+template <bool TRACE>
+__global__ void __launch_bounds__(kBlock) march_group_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
+    const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
+    const int g = threadIdx.x % kGroup;
+    if (r >= R.n) return;
+    const int cur = R.start[r];
+    if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground
+        if (g == 0) {
+            O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+            O.T[r] = 1.f, O.depth[r] = 0.f;
+            O.stats[3 * r] = O.stats[3 * r + 1] = O.stats[3 * r + 2] = 0;
+        }
+        return;
+    }
+    switch (F.sh_deg) {
+        case 0: march_ray_group<sh_vec4_f32(0), TRACE>(F, M, R, O, r, cur, g); break;
+        case 1: march_ray_group<sh_vec4_f32(1), TRACE>(F, M, R, O, r, cur, g); break;
+        case 2: march_ray_group<sh_vec4_f32(2), TRACE>(F, M, R, O, r, cur, g); break;
+        default: march_ray_group<sh_vec4_f32(3), TRACE>(F, M, R, O, r, cur, g); break;
+    }
+}
+
+// A slot's gradient sums over the samples of one cell visit: raw, the density conic, the colour conic and
+// sum_s a_s w_s (the SH gradient is b_j gR_c times it, for the channels whose unclamped colour is positive).
+struct SlotGrad {
+    float raw, dA[6], cA[6], aw;
+    bool dens, col;
+};
+
+__device__ __forceinline__ void clear_slot(SlotGrad& A) {
+    A.raw = A.aw = 0.f;
+#pragma unroll
+    for (int u = 0; u < 6; ++u) A.dA[u] = A.cA[u] = 0.f;
+    A.dens = A.col = false;
+}
+
+// One sample's contribution to neighbour k (record rc) at x, with the neighbour's unclamped colour c.
+__device__ __forceinline__ void sample_grad(const SiteRec& rc, const float (&x)[3], const float (&c)[3],
+                                            const float (&gR)[3], float gsig, bool coloured, float w, float mmin,
+                                            float inv_a, float grc, SlotGrad& A) {
+    float v[3];
+    offset_to(rc.q0, x, v);
+    if (gsig != 0.f) {
+        const float gd = gsig * fexp(rc.q0.w - 0.5f * density_m(rc, v));
+        if (fabsf(gd) > kMinDensityGrad) A.raw += gd, add_outer(A.dA, -0.5f * gd, v), A.dens = true;
+    }
+    if (coloured) {
+        const float a = fexp(-0.5f * (color_m(rc.q2, rc.q3, v) - mmin)) * inv_a;
+        if (a >= kMinColourWeight) {
+            const float aw = a * w;
+            const float gc3 = gR[0] * fmaxf(c[0], 0.f) + gR[1] * fmaxf(c[1], 0.f) + gR[2] * fmaxf(c[2], 0.f);
+            A.aw += aw;
+            add_outer(A.cA, -0.5f * aw * (gc3 - grc), v);
+            A.col = true;
+        }
+    }
+}
+
+__device__ __forceinline__ void flush_slot(const MarchGradOut& G, int k, const float (&c)[3], const float (&b)[16],
+                                           int nb, const float (&gR)[3], const SlotGrad& A) {
+    float* gb = G.block + kGradBlock * static_cast<int64_t>(k);
+    if (A.dens) {
+        unsafeAtomicAdd(gb, A.raw);
+#pragma unroll
+        for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 1 + u, A.dA[u]);
+    }
+    if (A.col) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 7 + u, A.cA[u]);
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+            const float dc = c[ch] > 0.f ? gR[ch] * A.aw : 0.f;
+            if (dc != 0.f)
+                for (int jj = 0; jj < nb; ++jj) unsafeAtomicAdd(gb + kGradSh + 3 * jj + ch, b[jj] * dc);
+        }
+    }
+}
+
+// The backward of march_ray_group: the same rounds replay the same samples bit for bit. Each lane sums its slots'
+// gradients over the samples of a cell visit in registers and adds them with atomics when the ray leaves the cell
+// (or ends), so a visit of several samples costs one set of atomics per neighbour; neighbours beyond the slots add
+// theirs per sample. The formulas are those of march_ray_backward.
+template <int NV>
+__device__ void march_ray_group_backward(const MarchField& F, const MarchParams& M, const MarchRays& R,
+                                         const MarchGradIn& GI, const MarchGradOut& G, int64_t r, int cur, int g) {
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
+    const int n_in = mid > near ? static_cast<int>(ceilf((mid - near) / M.dt)) : 0;
+    const int n_total = n_in + M.n_bg;
+    const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    const float gR[3] = {GI.g_rgb[3 * r], GI.g_rgb[3 * r + 1], GI.g_rgb[3 * r + 2]};
+    const float fg[3] = {GI.rgb[3 * r], GI.rgb[3 * r + 1], GI.rgb[3 * r + 2]};
+    const float gT_final = GI.g_T[r] * GI.T[r];
+    int moves = 0;
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f};
+    GroupCell Cc;
+    Cc.cell = -1;
+    SlotGrad S[kSlots];
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) clear_slot(S[s]);
+    auto flush = [&]() {
+        if (Cc.cell < 0) return;
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            if (Cc.k[s] >= 0) flush_slot(G, Cc.k[s], Cc.c[s], b, nb, gR, S[s]);
+            clear_slot(S[s]);
+        }
+    };
+    for (int k = 0; k < n_total;) {
+        float t, delta, x[3];
+        sample_at(near, mid, far, n_in, M, k, t, delta);
+        point_at(o, d, t, x);
+        GroupRound Q;
+        group_round<block_vec4(NV)>(F, cur, x, g, Q);
+        if (Q.k != cur && moves < kWalkCap) {
+            cur = Q.k, ++moves;
+            continue;
+        }
+        moves = 0;
+        if (Cc.cell != cur) flush(), enter_cell(F, cur, g, Cc);
+        const float alpha = 1.f - fexp(-Q.sigma * delta);
+        const float w = T * alpha;
+        const float T_next = T * (1.f - alpha);
+        const bool coloured = w > M.w_thresh;
+        float inv_a = 0.f, C[3] = {0.f, 0.f, 0.f}, grc = 0.f;
+        if (coloured) {
+            group_colour<NV>(F, Cc, x, b, nb, Q.mmin, g, inv_a, C);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += w * C[a];
+            grc = gR[0] * C[0] + gR[1] * C[1] + gR[2] * C[2];
+        }
+        float gs = 0.f;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) gs += gR[a] * (T_next * C[a] - (fg[a] - acc[a]));
+        const float gsig = delta * (gs - gT_final);
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            if (Cc.k[s] >= 0) {
+                const SiteRec rc = site_rec<block_vec4(NV)>(F, Cc.k[s]);
+                const float c[3] = {Cc.col_ok ? Cc.c[s][0] : 0.f, Cc.col_ok ? Cc.c[s][1] : 0.f,
+                                    Cc.col_ok ? Cc.c[s][2] : 0.f};
+                sample_grad(rc, x, c, gR, gsig, coloured, w, Q.mmin, inv_a, grc, S[s]);
+            }
+        }
+        for (int e = g + kGroup * kSlots; e < Cc.n; e += kGroup) {
+            const int kk = neighbor(F, cur, Cc.e0, e);
+            const float4* rp = F.rec + block_vec4(NV) * static_cast<int64_t>(kk);
+            const SiteRec rc = {rp[0], rp[1], rp[2], rp[3]};
+            float c[3] = {0.f, 0.f, 0.f};
+            if (coloured) sh_eval_n<NV>(rp + kRec, b, nb, c);
+            SlotGrad A;
+            clear_slot(A);
+            sample_grad(rc, x, c, gR, gsig, coloured, w, Q.mmin, inv_a, grc, A);
+            flush_slot(G, kk, c, b, nb, gR, A);
+        }
+        T = T_next;
+        ++k;
+        if (T < M.t_thresh) break;
+    }
+    flush();
+}
+
+__global__ void __launch_bounds__(kBlock)
+    march_group_backward_kernel(MarchField F, MarchParams M, MarchRays R, MarchGradIn GI, MarchGradOut G) {
+    const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
+    const int g = threadIdx.x % kGroup;
+    if (r >= R.n) return;
+    const int cur = R.start[r];
+    if (cur < 0 || cur >= F.n_sites) return;
+    switch (F.sh_deg) {
+        case 0: march_ray_group_backward<sh_vec4_f32(0)>(F, M, R, GI, G, r, cur, g); break;
+        case 1: march_ray_group_backward<sh_vec4_f32(1)>(F, M, R, GI, G, r, cur, g); break;
+        case 2: march_ray_group_backward<sh_vec4_f32(2)>(F, M, R, GI, G, r, cur, g); break;
+        default: march_ray_group_backward<sh_vec4_f32(3)>(F, M, R, GI, G, r, cur, g); break;
+    }
+}
+
 // Grid-stride fill with zeros (a kernel, not a memset, so that a captured stream records no memset node).
 constexpr int64_t kZeroBlocks = 4096;
 __global__ void __launch_bounds__(256) zero_kernel(float* __restrict__ p, int64_t n) {
@@ -736,14 +1107,28 @@ extern "C" int64_t vgr_march_backward_work_size(int64_t n_sites, int64_t sh_deg)
     return fwd > 0 ? fwd + n_sites * static_cast<int64_t>(sizeof(float)) * vgr::kGradBlock : 0;
 }
 
-extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
-                                 int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
-                                 int64_t sh_deg, const float* o, const float* d, const int32_t* start,
-                                 const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
-                                 double dt, int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T,
-                                 float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* work,
-                                 int64_t work_bytes, void* stream) {
+namespace vgr {
+namespace {
+// Launches of fewer rays take the 16-lane group layout: below about one wave per CU in one ray per lane, the launch is
+// bound by its rays' serial chains of loads, which the group shortens.
+constexpr int64_t kGroupRays = 16384;
+
+int64_t march_lanes(int64_t lanes, int64_t n_rays) { return lanes != 0 ? lanes : n_rays < kGroupRays ? kGroup : 1; }
+}  // namespace
+}  // namespace vgr
+
+extern "C" int vgr_march_forward_lanes(const float* points, int64_t n_sites, const int32_t* offsets,
+                                       const int32_t* adj, int64_t n_adj, const float* raw, const float* dA,
+                                       const float* cA, const float* sh, int64_t sh_deg, const float* o,
+                                       const float* d, const int32_t* start, const float* near_t,
+                                       const float* mid_t, const float* far_t, int64_t n_rays, double dt,
+                                       int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T,
+                                       float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                                       int64_t lanes_per_ray, void* work, int64_t work_bytes, void* stream) {
     using namespace vgr;
+    VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 1 || lanes_per_ray == kGroup,
+                "march_forward: lanes_per_ray must be 0 (by batch size), 1 or 16 (got %lld)",
+                static_cast<long long>(lanes_per_ray));
     VGR_REQUIRE(n_rays >= 0, "march_forward: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
     VGR_REQUIRE(n_bg >= 0 && n_bg <= INT_MAX, "march_forward: n_bg must be >= 0");
@@ -766,6 +1151,14 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
     const MarchOut O{rgb, T, depth, stats, trace, trace_cap};
+    if (march_lanes(lanes_per_ray, n_rays) == kGroup) {
+        const dim3 grid(grid_for(n_rays * kGroup, kBlock));
+        if (trace != nullptr)
+            hipLaunchKernelGGL(march_group_kernel<true>, grid, dim3(kBlock), 0, as_stream(stream), F, M, R, O);
+        else
+            hipLaunchKernelGGL(march_group_kernel<false>, grid, dim3(kBlock), 0, as_stream(stream), F, M, R, O);
+        return launch_status("march_group_kernel");
+    }
     if (trace != nullptr)
         hipLaunchKernelGGL(march_forward_kernel<true>, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0,
                            as_stream(stream), F, M, R, O);
@@ -775,14 +1168,30 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
     return launch_status("march_forward_kernel");
 }
 
+extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                                 int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                                 int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                                 const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
+                                 double dt, int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T,
+                                 float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap, void* work,
+                                 int64_t work_bytes, void* stream) {
+    return vgr_march_forward_lanes(points, n_sites, offsets, adj, n_adj, raw, dA, cA, sh, sh_deg, o, d, start, near_t,
+                                   mid_t, far_t, n_rays, dt, n_bg, t_thresh, w_thresh, rgb, T, depth, stats, trace,
+                                   trace_cap, 0, work, work_bytes, stream);
+}
+
 extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                                   int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
                                   int64_t sh_deg, const float* o, const float* d, const int32_t* start,
                                   const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
                                   double dt, int64_t n_bg, double t_thresh, double w_thresh, const float* rgb,
                                   const float* T, const float* g_rgb, const float* g_T, float* g_raw, float* g_dA,
-                                  float* g_cA, float* g_sh, void* work, int64_t work_bytes, void* stream) {
+                                  float* g_cA, float* g_sh, int64_t lanes_per_ray, void* work, int64_t work_bytes,
+                                  void* stream) {
     using namespace vgr;
+    VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 1 || lanes_per_ray == kGroup,
+                "march_backward: lanes_per_ray must be 0 (by batch size), 1 or 16 (got %lld)",
+                static_cast<long long>(lanes_per_ray));
     VGR_REQUIRE(n_rays >= 0, "march_backward: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
     VGR_REQUIRE(n_bg >= 0 && n_bg <= INT_MAX, "march_backward: n_bg must be >= 0");
@@ -820,7 +1229,10 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
     // wave-shared atomics once the launch holds at least one wave per CU (16384 rays); per-lane atomics below, where
     // the launch is bound by the latency of its few waves (config 5: 4096 rays 85 against 158 ms, 65536 rays 456
     // against 193 ms)
-    if (n_rays >= kCoopRays)
+    if (march_lanes(lanes_per_ray, n_rays) == kGroup)
+        hipLaunchKernelGGL(march_group_backward_kernel, dim3(grid_for(n_rays * kGroup, kBlock)), dim3(kBlock), 0, s,
+                           F, M, R, GI, G);
+    else if (n_rays >= kCoopRays)
         hipLaunchKernelGGL(march_backward_kernel<true>, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0, s, F, M, R,
                            GI, G);
     else

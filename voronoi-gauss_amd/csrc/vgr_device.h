@@ -35,6 +35,21 @@ __device__ __forceinline__ float maha(float xx, float xy, float xz, float yy, fl
     return xx * vx * vx + yy * vy * vy + zz * vz * vz + 2.f * (xy * vx * vy + xz * vx * vz + yz * vy * vz);
 }
 
+// DPP row permutations for reductions inside groups of 2, 4, 8 or 16 consecutive lanes: quad_perm [1,0,3,2] and
+// [2,3,0,1] (xor 1, xor 2), row_half_mirror (i <-> 7 - i within 8 lanes) and row_mirror (i <-> 15 - i within 16).
+// A butterfly over them with a commutative operation leaves the same bits in every lane of the group.
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int row_perm(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float row_perm(float v) {
+    return __int_as_float(row_perm<CTRL>(__float_as_int(v)));
+}
+
 // Real spherical-harmonics basis up to degree 3 (3DGS constants and signs), zero beyond `deg`.
 __device__ inline void sh_basis(float x, float y, float z, int deg, float (&b)[16]) {
     b[0] = 0.28209479177387814f;

@@ -26,8 +26,10 @@ SIGNATURES = {
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
 	'vgr_march_backward_work_size': [_I64, _I64],
+	'vgr_march_forward_lanes': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64,
+								_I64, _F64, _F64, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
 	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
-						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
 								_P],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
@@ -54,7 +56,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 _lib = None
 
 

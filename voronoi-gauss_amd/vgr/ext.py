@@ -186,8 +186,9 @@ def _field_work(points, m, records):
 class _MarchExtension:
 	@staticmethod
 	def march_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
-					  t_thresh, w_thresh, trace_cap=0):
-		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0)."""
+					  t_thresh, w_thresh, trace_cap=0, lanes=0):
+		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0).
+		lanes: 1 ray per lane (1), 16 lanes per ray (16) or by batch size (0)."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -209,16 +210,17 @@ class _MarchExtension:
 		work_bytes = int(_lib.load().vgr_march_work_size(points.numel() // 3, int(sh_deg)))
 		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
-			call('vgr_march_forward', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
+			call('vgr_march_forward_lanes', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(dA), ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid),
 				 ptr(far), B, float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(depth),
-				 ptr(stats), ptr(trace), int(trace_cap), ptr(work), work_bytes, stream_of(dev))
+				 ptr(stats), ptr(trace), int(trace_cap), int(lanes), ptr(work), work_bytes, stream_of(dev))
 		return out
 
 	@staticmethod
 	def march_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
-					   t_thresh, w_thresh, rgb, T, g_rgb, g_T):
-		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (march.cu:405-428)."""
+					   t_thresh, w_thresh, rgb, T, g_rgb, g_T, lanes=0):
+		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (march.cu:405-428). lanes: the layout of the
+		forward that produced rgb and T."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -240,7 +242,7 @@ class _MarchExtension:
 			call('vgr_march_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
 				 ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid), ptr(far), B,
 				 float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(g_rgb), ptr(g_T),
-				 *[ptr(x) for x in g], ptr(work), work_bytes, stream_of(dev))
+				 *[ptr(x) for x in g], int(lanes), ptr(work), work_bytes, stream_of(dev))
 		return g
 
 
