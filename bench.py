@@ -121,9 +121,9 @@ def main():
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
 	ap.add_argument('--batch', type=int, default=4096, help='grad workload: random rays per training step')
-	ap.add_argument('--lanes-per-ray', type=int, default=None, choices=[1, 2, 4, 8],
-					help='foam workload: ray layout (1: one ray per lane, 2 / 4 / 8: lanes per ray; default: the '
-						 'library default)')
+	ap.add_argument('--lanes-per-ray', type=int, default=None, choices=[1, 2, 4, 8, 16],
+					help='foam workload: ray layout (1: one ray per lane, 2 / 4 / 8: lanes per ray); march workload: '
+						 '1 or 16; default: the library default')
 	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
 	ap.add_argument('--workload', default='foam',
@@ -435,7 +435,8 @@ def bench_march_grad(args):
 		  'backward_ms': round(L['bwd'], 4), 'samples_per_ray': round(L['samples'], 2),
 		  'coloured_per_ray': round(L['coloured'], 2), 'layouts': layouts},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
-		  'frac': round(achieved / 8000.0, 4), 'traffic': None, 'kernel': 'march_backward_kernel',
+		  'frac': round(achieved / 8000.0, 4), 'traffic': None,
+		  'kernel': 'march_group_backward_kernel' if auto == 16 else 'march_backward_kernel',
 		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
 
 
@@ -527,7 +528,9 @@ def bench_march(args):
 									   sc.sh_deg, o[sel], d[sel], start[sel], near[sel], mid[sel], far[sel], dt, n_bg,
 									   1e-4, 1e-4)
 	stream = torch.cuda.current_stream(dev)
-	launch_ms, out, wall = time_steps(lambda: me.march_forward(*args_of()), args.steps, args.warmup, stream)
+	lanes = args.lanes_per_ray or 0
+	launch_ms, out, wall = time_steps(lambda: me.march_forward(*args_of(), lanes=lanes), args.steps, args.warmup,
+									  stream)
 	ms = float(np.mean(launch_ms))
 	rgb, T, depth, stats = out
 	st = stats.double()
@@ -580,7 +583,8 @@ def bench_march(args):
 					  f'disparity steps, starts from the GPU grid', 'sites': sc.n_sites, 'rays': B,
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
-		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4)},
+		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
+		  'lanes_per_ray': lanes or (16 if B < 16384 else 1)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
 		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)
