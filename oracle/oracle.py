@@ -24,6 +24,10 @@ _SIGS = {
 							  _F32, _P, _P, _P, _P, _P, _I32, _I32], ctypes.c_double),
 	'oracle_march_backward': ([_P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64, _F32, _I32, _F32,
 							   _F32, _P, _P, _P, _P, _P, _P, _P, _P], None),
+	'oracle_foam_forward': ([_P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _F32, _F32, _P, _P, _P, _P,
+							 _P, _I32], None),
+	'oracle_foam_backward': ([_P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _F32, _F32, _P, _P, _P,
+							  _P, _P, _P, _P, _P], None),
 	'oracle_walk': ([_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _I32], None),
 	'oracle_density': ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _F32, _P, _I32], None),
 	'oracle_color': ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _I32], None),
@@ -135,6 +139,39 @@ def march_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, n
 	up = [_a(rgb, np.float32), _a(T, np.float32), _a(g_rgb, np.float32), _a(g_T, np.float32)]
 	load().oracle_march_backward(*[_p(a) for a in arrs], int(sh_deg), *[_p(a) for a in ray_arrs], B, float(dt),
 								 int(n_bg), t_thresh, w_thresh, *[_p(a) for a in up], *[_p(a) for a in g])
+	return tuple(g)
+
+
+def _foam_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far):
+	return ([_a(points, np.float32), _a(offsets, np.int32), _a(adj, np.int32), _a(raw, np.float32),
+			 _a(dA, np.float32), _a(cA, np.float32), _a(sh, np.float32)],
+			[_a(o, np.float32), _a(d, np.float32), _a(start, np.int32), _a(near, np.float32), _a(far, np.float32)])
+
+
+def foam_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh=1e-4,
+				 w_thresh=1e-4, record_cap=0):
+	"""foam.cu training forward -> dict rgb, T, depth, stats (B, 3) [samples, coloured segments, walk steps], rec
+	(B, K, 8) or None."""
+	arrs, rays = _foam_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
+	B = len(rays[0])
+	rgb, T, depth = np.zeros((B, 3), np.float32), np.zeros(B, np.float32), np.zeros(B, np.float32)
+	stats = np.zeros((B, 3), np.int32)
+	rec = np.zeros((B, record_cap, 8), np.float32) if record_cap > 0 else None
+	load().oracle_foam_forward(*[_p(x) for x in arrs], int(sh_deg), *[_p(x) for x in rays], B, t_thresh, w_thresh,
+							   _p(rgb), _p(T), _p(depth), _p(stats), _p(rec), int(record_cap))
+	return {'rgb': rgb, 'T': T, 'depth': depth, 'stats': stats, 'rec': rec}
+
+
+def foam_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, rgb, T, g_rgb, g_T,
+				  t_thresh=1e-4, w_thresh=1e-4):
+	"""foam.cu training backward -> g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)."""
+	arrs, rays = _foam_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
+	n, B = len(arrs[0]), len(rays[0])
+	g = [np.zeros(n, np.float32), np.zeros((n, 6), np.float32), np.zeros((n, 6), np.float32),
+		 np.zeros((n, 16, 3), np.float32)]
+	up = [_a(rgb, np.float32), _a(T, np.float32), _a(g_rgb, np.float32), _a(g_T, np.float32)]
+	load().oracle_foam_backward(*[_p(x) for x in arrs], int(sh_deg), *[_p(x) for x in rays], B, t_thresh, w_thresh,
+								*[_p(x) for x in up], *[_p(x) for x in g])
 	return tuple(g)
 
 

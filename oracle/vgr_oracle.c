@@ -10,6 +10,7 @@
  *   march_forward csrc/march.cu:134-262        (load_ray :134-141, sample_at :143-153, walk_to :157-180,
  *                                               density_at :182-192, color_at :195-219, kernel :221-262)
  *   march_backward csrc/march.cu:264-345, 402-428
+ *   training renderer (foam.cu) forward and backward   csrc/foam.cu:160-469
  *   walk          csrc/vgf.cu:51-79
  *   density       csrc/vgf.cu:98-119,152-177
  *   color         csrc/vgf.cu:202-282
@@ -652,6 +653,248 @@ void oracle_march_backward(const float* points, const int32_t* offsets, const in
     for (int64_t r = 0; r < B; ++r)
         march_ray_backward(&F, dt, n_bg, t_thresh, w_thresh, o + 3 * r, d + 3 * r, start[r], near_t[r], mid_t[r],
                            far_t[r], rgb + 3 * r, T[r], g_rgb + 3 * r, g_T[r], g_raw, g_dA, g_cA, g_sh);
+}
+
+/* ================================================================ foam (training renderer) forward/backward */
+
+/* A sample of the training renderer: foam.cu:272-286 (the record is t, site, sigma, C, m_min, 1 / A or 0). */
+typedef struct {
+    float t, x[3], sigma, C[3], mmin, inv_a;
+    int site, has_c;
+} TSample;
+
+/* Exit of cell i: smallest bisector parameter ahead of the ray, ties to the smaller neighbour index;
+ * foam.cu:183-206. */
+static void train_exit_face(const Field* F, int i, const float o[3], const float d[3], float* t_exit, int* next) {
+    const float* pi = F->points + 3 * (int64_t)i;
+    float bt = K_INF;
+    int bk = INT_MAX;
+    for (int e = F->offsets[i]; e < F->offsets[i + 1]; ++e) {
+        const int j = F->adj[e];
+        const float* pj = F->points + 3 * (int64_t)j;
+        float n[3], m[3];
+        for (int a = 0; a < 3; ++a) {
+            n[a] = pj[a] - pi[a];
+            m[a] = 0.5f * (pj[a] + pi[a]) - o[a];
+        }
+        const float dn = n[0] * d[0] + n[1] * d[1] + n[2] * d[2];
+        if (dn > 0.f) {
+            const float t = (m[0] * n[0] + m[1] * n[1] + m[2] * n[2]) / dn;
+            if (t < bt || (t == bt && j < bk)) { bt = t; bk = j; }
+        }
+    }
+    *t_exit = bt;
+    *next = bk;
+}
+
+/* make_sample: foam.cu:245-253. */
+static void train_make(const Field* F, const float o[3], const float d[3], float t, int site, TSample* P) {
+    P->t = t;
+    for (int a = 0; a < 3; ++a) P->x[a] = o[a] + t * d[a];
+    P->site = site;
+    P->sigma = march_density(F, site, P->x);
+    P->has_c = 0;
+    P->inv_a = 0.f;
+    P->mmin = 0.f;
+    P->C[0] = P->C[1] = P->C[2] = 0.f;
+}
+
+/* color_at with m_min and 1 / A kept: foam.cu:217-243. */
+static void train_color(const Field* F, TSample* P, const float b[16]) {
+    const int i = P->site, e0 = F->offsets[i], n = F->offsets[i + 1] - e0 + 1;
+    const int nb = (F->sh_deg + 1) * (F->sh_deg + 1);
+    float mmin = K_INF;
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)k;
+        const float v[3] = {P->x[0] - p[0], P->x[1] - p[1], P->x[2] - p[2]};
+        mmin = fminf(mmin, conic_maha(F->cA, k, v));
+    }
+    float A = 0.f, cs[3] = {0.f, 0.f, 0.f};
+    for (int e = 0; e < n; ++e) {
+        const int k = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)k;
+        const float v[3] = {P->x[0] - p[0], P->x[1] - p[1], P->x[2] - p[2]};
+        const float a = expf(-0.5f * (conic_maha(F->cA, k, v) - mmin));
+        float c[3];
+        sh_eval(F->sh, k, b, nb, c);
+        A += a;
+        for (int ch = 0; ch < 3; ++ch) cs[ch] += a * fmaxf(c[ch], 0.f);
+    }
+    P->mmin = mmin;
+    P->inv_a = 1.f / A;
+    for (int ch = 0; ch < 3; ++ch) P->C[ch] = cs[ch] * P->inv_a;
+    P->has_c = 1;
+}
+
+static void train_store(float* rec, int K, int s, const TSample* P) {
+    if (rec == NULL || s >= K) return;
+    float* q = rec + 8 * (int64_t)s;
+    int32_t site = P->site;
+    q[0] = P->t;
+    memcpy(q + 1, &site, 4);
+    q[2] = P->sigma;
+    q[3] = P->C[0]; q[4] = P->C[1]; q[5] = P->C[2];
+    q[6] = P->mmin;
+    q[7] = P->has_c ? P->inv_a : 0.f;
+}
+
+/* Training forward of one ray: x(near) in the walked cell, then every exit crossing, up to x(far), trapezoid
+ * compositing, colours only for segments of weight > w_thresh; foam.cu:345-393. */
+static void train_ray(const Field* F, float t_thresh, float w_thresh, const float o[3], const float d[3], int start,
+                     float near, float far, float rgb[3], float* T_out, float* depth, int32_t stats[3], float* rec,
+                     int K) {
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F->sh_deg, b);
+    int walk_steps = 0, n_samples = 1, n_color = 0;
+    float x0[3];
+    for (int a = 0; a < 3; ++a) x0[a] = o[a] + near * d[a];
+    int cur = march_walk_to(F, start, x0, &walk_steps);
+    TSample P, Q;
+    train_make(F, o, d, near, cur, &P);
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    for (int it = 0; it < K_MAX_CELLS; ++it) {
+        float te;
+        int nx;
+        train_exit_face(F, cur, o, d, &te, &nx);
+        const int last = nx == INT_MAX || te >= far;
+        train_make(F, o, d, last ? far : fmaxf(te, P.t), last ? cur : nx, &Q);
+        ++n_samples;
+        const float delta = Q.t - P.t;
+        const float alpha = 1.f - expf(-0.5f * (P.sigma + Q.sigma) * delta);
+        const float w = T * alpha;
+        if (w > w_thresh) {
+            if (!P.has_c) train_color(F, &P, b);
+            train_color(F, &Q, b);
+            for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (P.C[a] + Q.C[a]);
+            dep += w * 0.5f * (P.t + Q.t);
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        train_store(rec, K, n_samples - 2, &P);
+        P = Q;
+        cur = Q.site;
+        if (last || T < t_thresh) break;
+    }
+    train_store(rec, K, n_samples - 1, &P);
+    for (int a = 0; a < 3; ++a) rgb[a] = acc[a];
+    *T_out = T;
+    *depth = dep;
+    stats[0] = n_samples; stats[1] = n_color; stats[2] = walk_steps;
+}
+
+void oracle_foam_forward(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                         const float* dA, const float* cA, const float* sh, int sh_deg, const float* o,
+                         const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t B,
+                         float t_thresh, float w_thresh, float* rgb, float* T, float* depth, int32_t* stats,
+                         float* rec, int K) {
+    const Field F = {points, offsets, adj, raw, dA, cA, sh, sh_deg};
+    for (int64_t r = 0; r < B; ++r)
+        train_ray(&F, t_thresh, w_thresh, o + 3 * r, d + 3 * r, start[r], near_t[r], far_t[r], rgb + 3 * r, T + r,
+                 depth + r, stats + 3 * r, rec != NULL ? rec + 8 * (int64_t)K * r : NULL, K);
+}
+
+/* A sample's gradients: gs = dL/dsigma, gC = dL/dC; foam.cu:303-343. */
+static void train_scatter(const Field* F, const TSample* P, float gs, const float gC[3], const float b[16],
+                         float* g_raw, float* g_dA, float* g_cA, float* g_sh) {
+    const int i = P->site, e0 = F->offsets[i], n = F->offsets[i + 1] - e0 + 1;
+    if (gs != 0.f) {
+        for (int e = 0; e < n; ++e) {
+            const int q = neighbor(F, i, e0, e);
+            const float* p = F->points + 3 * (int64_t)q;
+            const float v[3] = {P->x[0] - p[0], P->x[1] - p[1], P->x[2] - p[2]};
+            const float gc = gs * expf(fminf(F->raw[q], 30.f) - 0.5f * conic_maha(F->dA, q, v));
+            if (fabsf(gc) > 1e-12f) {
+                g_raw[q] += gc;
+                add_conic_grad(g_dA, q, -0.5f * gc, v);
+            }
+        }
+    }
+    if (!P->has_c || (gC[0] == 0.f && gC[1] == 0.f && gC[2] == 0.f)) return;
+    const int nb = (F->sh_deg + 1) * (F->sh_deg + 1);
+    const float gCC = gC[0] * P->C[0] + gC[1] * P->C[1] + gC[2] * P->C[2];
+    for (int e = 0; e < n; ++e) {
+        const int q = neighbor(F, i, e0, e);
+        const float* p = F->points + 3 * (int64_t)q;
+        const float v[3] = {P->x[0] - p[0], P->x[1] - p[1], P->x[2] - p[2]};
+        const float a = expf(-0.5f * (conic_maha(F->cA, q, v) - P->mmin)) * P->inv_a;
+        if (a < 1e-7f) continue;
+        float c[3];
+        sh_eval(F->sh, q, b, nb, c);
+        float* gsh = g_sh + 48 * (int64_t)q;
+        for (int ch = 0; ch < 3; ++ch) {
+            const float dc = c[ch] > 0.f ? a * gC[ch] : 0.f;
+            for (int j = 0; j < nb; ++j) gsh[3 * j + ch] += b[j] * dc;
+        }
+        const float ga = gC[0] * fmaxf(c[0], 0.f) + gC[1] * fmaxf(c[1], 0.f) + gC[2] * fmaxf(c[2], 0.f);
+        const float gm = -0.5f * a * (ga - gCC);
+        if (gm != 0.f) add_conic_grad(g_cA, q, gm, v);
+    }
+}
+
+/* Training backward of one ray, re-tracing it (the reference's replay of recorded samples gives the same values):
+ * each sample collects half of the segment gradients on both sides; foam.cu:395-469. */
+static void train_ray_backward(const Field* F, float t_thresh, float w_thresh, const float o[3], const float d[3],
+                              int start, float near, float far, const float fg[3], float T_out, const float gR[3],
+                              float gT, float* g_raw, float* g_dA, float* g_cA, float* g_sh) {
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F->sh_deg, b);
+    const float gT_final = gT * T_out;
+    int walk_steps = 0;
+    float x0[3];
+    for (int a = 0; a < 3; ++a) x0[a] = o[a] + near * d[a];
+    int cur = march_walk_to(F, start, x0, &walk_steps);
+    TSample P, Q;
+    train_make(F, o, d, near, cur, &P);
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, gs_pending = 0.f, gC_pending[3] = {0.f, 0.f, 0.f};
+    for (int it = 0; it < K_MAX_CELLS; ++it) {
+        float te;
+        int nx;
+        train_exit_face(F, cur, o, d, &te, &nx);
+        const int last = nx == INT_MAX || te >= far;
+        train_make(F, o, d, last ? far : fmaxf(te, P.t), last ? cur : nx, &Q);
+        const float delta = Q.t - P.t;
+        const float alpha = 1.f - expf(-0.5f * (P.sigma + Q.sigma) * delta);
+        const float w = T * alpha;
+        const float T_next = T * (1.f - alpha);
+        const int active = w > w_thresh;
+        float c[3] = {0.f, 0.f, 0.f};
+        if (active) {
+            if (!P.has_c) train_color(F, &P, b);
+            if (!Q.has_c) train_color(F, &Q, b);
+            for (int a = 0; a < 3; ++a) {
+                c[a] = 0.5f * (P.C[a] + Q.C[a]);
+                acc[a] += w * c[a];
+            }
+        }
+        float g_sbar = 0.f;
+        for (int a = 0; a < 3; ++a) g_sbar += gR[a] * (T_next * c[a] - (fg[a] - acc[a]));
+        g_sbar = delta * (g_sbar - gT_final);
+        float gc_half[3], gC_P[3];
+        for (int a = 0; a < 3; ++a) {
+            gc_half[a] = active ? 0.5f * w * gR[a] : 0.f;
+            gC_P[a] = gC_pending[a] + gc_half[a];
+        }
+        train_scatter(F, &P, gs_pending + 0.5f * g_sbar, gC_P, b, g_raw, g_dA, g_cA, g_sh);
+        gs_pending = 0.5f * g_sbar;
+        for (int a = 0; a < 3; ++a) gC_pending[a] = gc_half[a];
+        T = T_next;
+        P = Q;
+        cur = Q.site;
+        if (last || T < t_thresh) break;
+    }
+    train_scatter(F, &P, gs_pending, gC_pending, b, g_raw, g_dA, g_cA, g_sh);
+}
+
+void oracle_foam_backward(const float* points, const int32_t* offsets, const int32_t* adj, const float* raw,
+                          const float* dA, const float* cA, const float* sh, int sh_deg, const float* o,
+                          const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t B,
+                          float t_thresh, float w_thresh, const float* rgb, const float* T, const float* g_rgb,
+                          const float* g_T, float* g_raw, float* g_dA, float* g_cA, float* g_sh) {
+    const Field F = {points, offsets, adj, raw, dA, cA, sh, sh_deg};
+    for (int64_t r = 0; r < B; ++r)
+        train_ray_backward(&F, t_thresh, w_thresh, o + 3 * r, d + 3 * r, start[r], near_t[r], far_t[r], rgb + 3 * r,
+                          T[r], g_rgb + 3 * r, g_T[r], g_raw, g_dA, g_cA, g_sh);
 }
 
 /* ============================================================================ vgf forward operators */
