@@ -157,6 +157,34 @@ int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offs
                        void* work, int64_t work_bytes, void* stream);
 
 /*
+ * The training renderer: rendering at the ray's crossings of the Voronoi faces with a record of every sample, and
+ * its backward. Replaces foam_forward() / foam_backward() of csrc/foam.cu:471-531 (kernels :345-469, exports
+ * :533-536), bound by ext.foam (ext.py:185-216), the renderer train.py uses by default (render_rays_foam).
+ * Both run 16 lanes per ray (one neighbour per lane), the layout for training batches.
+ *   Field and rays as for vgr_march_forward (no mid_t). foam_forward -> rgb f32 (B, 3), T f32 (B), depth f32 (B),
+ *   stats i32 (B, 3) = samples, coloured segments, walk steps; rec f32 (B, record_cap, 8) = per sample (t, site
+ *   bits, sigma, C rgb, m_min, 1 / sum of colour weights or 0) for the first record_cap samples (record_cap 0: no
+ *   records, rec may be NULL).
+ *   foam_backward takes the forward's rgb, T, rec and stats (records replayed for rays whose samples fit, the others
+ *   re-traced with the same arithmetic) and the upstream gradients g_rgb (B, 3), g_T (B) -> g_raw (N), g_dA (N, 6),
+ *   g_cA (N, 6), g_sh (N, 16, 3), overwritten. Sums use fp32 atomics (equal to a sequential sum to rounding).
+ * work: vgr_foam_work_size(N, sh_deg) bytes, 256-byte aligned, for both.
+ */
+int64_t vgr_foam_work_size(int64_t n_sites, int64_t sh_deg);
+int vgr_foam_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj, int64_t n_adj,
+                     const float* raw, const float* dA, const float* cA, const float* sh, int64_t sh_deg,
+                     const float* o, const float* d, const int32_t* start, const float* near_t, const float* far_t,
+                     int64_t n_rays, double t_thresh, double w_thresh, float* rgb, float* T, float* depth,
+                     int32_t* stats, float* rec, int64_t record_cap, void* work, int64_t work_bytes, void* stream);
+int vgr_foam_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                      int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                      int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                      const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, const float* rgb,
+                      const float* T, const float* g_rgb, const float* g_T, const float* rec, int64_t record_cap,
+                      const int32_t* stats, float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work,
+                      int64_t work_bytes, void* stream);
+
+/*
  * Nearest site of every sorted ray sample o + z d by a greedy walk (strict <). Replaces walk() of
  * csrc/vgf.cu:438-456 (export :566), bound by Graph.walk (ext.py:54-58).
  *   z f32 (B, S) sorted per ray; start i32 (B) -> site i32 (B, S), steps i32 (B) (steps may be NULL)

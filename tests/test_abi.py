@@ -26,7 +26,7 @@ def test_header_declares_the_entry_points():
 	names = declared()
 	for n in ('vgr_foam_infer', 'vgr_foam_infer_traced', 'vgr_foam_infer_lanes', 'vgr_foam_traverse_faces',
 			  'vgr_march_forward', 'vgr_march_work_size', 'vgr_march_backward', 'vgr_march_backward_work_size',
-			  'vgr_march_forward_lanes',
+			  'vgr_march_forward_lanes', 'vgr_foam_work_size', 'vgr_foam_forward', 'vgr_foam_backward',
 			  'vgr_walk', 'vgr_density_forward', 'vgr_color_forward', 'vgr_field_work_size', 'vgr_conic_forward', 'vgr_density_backward', 'vgr_density_backward_work_size',
 			  'vgr_color_backward', 'vgr_color_backward_work_size', 'vgr_conic_backward', 'vgr_pack_work_size',
 			  'vgr_pack_foam', 'vgr_morton_work_size', 'vgr_morton_codes', 'vgr_bake_colors', 'vgr_grid_work_size',

@@ -1087,6 +1087,335 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
+// ---------------------------------------------------------------------- training renderer (foam.cu), 16 lanes per ray
+//
+// The samples of foam.cu:1-17: x(near) in the cell the walk reaches, then every crossing of a Voronoi face (the
+// nearest bisector plane ahead of the ray, ties to the smaller neighbour index), then x(far); trapezoid compositing
+// of consecutive samples, colours only for segments of weight > w_thresh. Same group layout and site blocks as the
+// 16-lane march. A crossing sample's site is the cell the ray enters, whose neighbourhood is also the one that gives
+// that cell's exit, so one round over it evaluates the sample's density and colour minimum and the cell's exit
+// candidates together: one round per sample, plus one colour round for a sample of a coloured segment. The forward
+// can record every sample (t, site, sigma, C, m_min, 1 / A or 0: foam.cu:272-286) for the backward, which replays
+// the records or re-traces rays that did not fit with the same rounds (same bits).
+
+constexpr int kTrainRecord = 8;
+
+struct TrainSample {
+    float t, sigma, mmin, inv_a, C[3];
+    int site;
+    bool has_c;
+};
+
+// Density and colour minimum at x over the neighbourhood of i, and the exit of cell i along the ray (smallest
+// bisector parameter ahead, ties to the smaller index; INT_MAX when none), reduced over the group.
+template <int BLK>
+__device__ __forceinline__ void train_round(const MarchField& F, int i, const float (&o)[3], const float (&d)[3],
+                                            float t, int g, TrainSample& S, float& t_exit, int& next) {
+    float x[3];
+    point_at(o, d, t, x);
+    const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
+    const float4 pi = F.rec[BLK * static_cast<int64_t>(i)];
+    float s = 0.f, mm = kInf, bt = kInf;
+    int bk = INT_MAX;
+    for (int e = g; e < n; e += kGroup) {
+        const int k = neighbor(F, i, e0, e);
+        const SiteRec rc = site_rec<BLK>(F, k);
+        float v[3];
+        offset_to(rc.q0, x, v);
+        s += fexp(rc.q0.w - 0.5f * density_m(rc, v));
+        mm = fminf(mm, color_m(rc.q2, rc.q3, v));
+        if (e > 0) {
+            const float nn[3] = {rc.q0.x - pi.x, rc.q0.y - pi.y, rc.q0.z - pi.z};
+            const float m[3] = {0.5f * (rc.q0.x + pi.x) - o[0], 0.5f * (rc.q0.y + pi.y) - o[1],
+                                0.5f * (rc.q0.z + pi.z) - o[2]};
+            const float dn = nn[0] * d[0] + nn[1] * d[1] + nn[2] * d[2];
+            if (dn > 0.f) {
+                const float tj = (m[0] * nn[0] + m[1] * nn[1] + m[2] * nn[2]) / dn;
+                if (tj < bt || (tj == bt && k < bk)) bt = tj, bk = k;
+            }
+        }
+    }
+    row_argmin(bt, bk);
+    S.t = t, S.site = i, S.sigma = row_sum(s), S.mmin = row_min(mm), S.has_c = false, S.inv_a = 0.f;
+    S.C[0] = S.C[1] = S.C[2] = 0.f;
+    t_exit = bt, next = bk;
+}
+
+// Normalised colour blend of sample S (weights exp(-(m_k - m_min) / 2) over its site's neighbourhood).
+template <int NV>
+__device__ __forceinline__ void train_colour(const MarchField& F, const float (&o)[3], const float (&d)[3],
+                                             const float (&b)[16], int nb, int g, TrainSample& S) {
+    float x[3];
+    point_at(o, d, S.t, x);
+    const int e0 = F.offsets[S.site], n = F.offsets[S.site + 1] - e0 + 1;
+    float A = 0.f, cs[3] = {0.f, 0.f, 0.f};
+    for (int e = g; e < n; e += kGroup) {
+        const int k = neighbor(F, S.site, e0, e);
+        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const float4 p = r[0], c0 = r[2], c1 = r[3];
+        float c[3], v[3];
+        sh_eval_n<NV>(r + kRec, b, nb, c);
+        offset_to(p, x, v);
+        const float a = fexp(-0.5f * (color_m(c0, c1, v) - S.mmin));
+        A += a;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) cs[ch] += a * fmaxf(c[ch], 0.f);
+    }
+    S.inv_a = 1.f / row_sum(A);
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) S.C[ch] = row_sum(cs[ch]) * S.inv_a;
+    S.has_c = true;
+}
+
+// Greedy walk of the group from `cur` to the site nearest x(t) (march.cu / foam.cu walk_to).
+template <int BLK>
+__device__ __forceinline__ int train_walk(const MarchField& F, int cur, const float (&o)[3], const float (&d)[3],
+                                          float t, int g, int& steps) {
+    float x[3];
+    point_at(o, d, t, x);
+    for (int it = 0; it < kWalkCap; ++it) {
+        GroupRound Q;
+        group_round<BLK>(F, cur, x, g, Q);
+        if (Q.k == cur) break;
+        cur = Q.k, ++steps;
+    }
+    return cur;
+}
+
+__device__ __forceinline__ void train_store(float* __restrict__ rec, int64_t r, int K, int s, const TrainSample& S,
+                                            int g) {
+    if (rec == nullptr || s >= K || g >= kTrainRecord) return;
+    const float v = g == 0 ? S.t
+                  : g == 1 ? __int_as_float(S.site)
+                  : g == 2 ? S.sigma
+                  : g == 3 ? S.C[0]
+                  : g == 4 ? S.C[1]
+                  : g == 5 ? S.C[2]
+                  : g == 6 ? S.mmin
+                           : (S.has_c ? S.inv_a : 0.f);
+    rec[(r * K + s) * kTrainRecord + g] = v;
+}
+
+__device__ __forceinline__ void train_load(const float* __restrict__ rec, int64_t r, int K, int s, TrainSample& S) {
+    const float* p = rec + (r * K + s) * kTrainRecord;
+    S.t = p[0], S.site = __float_as_int(p[1]), S.sigma = p[2];
+    S.C[0] = p[3], S.C[1] = p[4], S.C[2] = p[5];
+    S.mmin = p[6], S.inv_a = p[7], S.has_c = p[7] > 0.f;
+}
+
+struct TrainRays {
+    const float* __restrict__ o;
+    const float* __restrict__ d;
+    const int* __restrict__ start;
+    const float* __restrict__ t_near;
+    const float* __restrict__ t_far;
+    int64_t n;
+};
+
+template <int NV>
+__device__ void train_ray(const MarchField& F, const MarchParams& M, const TrainRays& R, const MarchOut& O,
+                          float* __restrict__ rec, int K, int64_t r, int g) {
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float near = R.t_near[r], far = R.t_far[r];
+    const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    int walk_steps = 0, n_samples = 1, n_color = 0;
+    int cur = train_walk<block_vec4(NV)>(F, R.start[r], o, d, near, g, walk_steps);
+    TrainSample P, Q;
+    float te, te2;
+    int nx, nx2;
+    train_round<block_vec4(NV)>(F, cur, o, d, near, g, P, te, nx);
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
+    for (int it = 0; it < kMaxCells; ++it) {
+        const bool last = nx == INT_MAX || te >= far;
+        train_round<block_vec4(NV)>(F, last ? cur : nx, o, d, last ? far : fmaxf(te, P.t), g, Q, te2, nx2);
+        ++n_samples;
+        const float delta = Q.t - P.t;
+        const float alpha = 1.f - fexp(-0.5f * (P.sigma + Q.sigma) * delta);
+        const float w = T * alpha;
+        if (w > M.w_thresh) {
+            if (!P.has_c) train_colour<NV>(F, o, d, b, nb, g, P);
+            train_colour<NV>(F, o, d, b, nb, g, Q);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) acc[a] += w * 0.5f * (P.C[a] + Q.C[a]);
+            dep += w * 0.5f * (P.t + Q.t);
+            ++n_color;
+        }
+        T *= 1.f - alpha;
+        train_store(rec, r, K, n_samples - 2, P, g);
+        P = Q;
+        cur = Q.site, te = te2, nx = nx2;
+        if (last || T < M.t_thresh) break;
+    }
+    train_store(rec, r, K, n_samples - 1, P, g);
+    if (g == 0) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
+        O.T[r] = T;
+        O.depth[r] = dep;
+        O.stats[3 * r] = n_samples, O.stats[3 * r + 1] = n_color, O.stats[3 * r + 2] = walk_steps;
+    }
+}
+
+__global__ void __launch_bounds__(kBlock)
+    train_forward_kernel(MarchField F, MarchParams M, TrainRays R, MarchOut O, float* __restrict__ rec, int K) {
+    const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
+    const int g = threadIdx.x % kGroup;
+    if (r >= R.n) return;
+    const int cur = R.start[r];
+    if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground, no samples
+        if (g == 0) {
+            O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
+            O.T[r] = 1.f, O.depth[r] = 0.f;
+            O.stats[3 * r] = O.stats[3 * r + 1] = O.stats[3 * r + 2] = 0;
+        }
+        return;
+    }
+    switch (F.sh_deg) {
+        case 0: train_ray<sh_vec4_f32(0)>(F, M, R, O, rec, K, r, g); break;
+        case 1: train_ray<sh_vec4_f32(1)>(F, M, R, O, rec, K, r, g); break;
+        case 2: train_ray<sh_vec4_f32(2)>(F, M, R, O, rec, K, r, g); break;
+        default: train_ray<sh_vec4_f32(3)>(F, M, R, O, rec, K, r, g); break;
+    }
+}
+
+// A sample's gradients (gs = dL/dsigma, gC = dL/dC) over its site's neighbourhood, each lane adding its neighbours'
+// with atomics into their gradient blocks; foam.cu:303-343.
+template <int NV>
+__device__ void train_scatter(const MarchField& F, const MarchGradOut& G, const float (&o)[3], const float (&d)[3],
+                              const float (&b)[16], int nb, const TrainSample& S, float gs, const float (&gC)[3],
+                              int g) {
+    const bool colour = S.has_c && (gC[0] != 0.f || gC[1] != 0.f || gC[2] != 0.f);
+    if (gs == 0.f && !colour) return;
+    float x[3];
+    point_at(o, d, S.t, x);
+    const float gCC = gC[0] * S.C[0] + gC[1] * S.C[1] + gC[2] * S.C[2];
+    const int e0 = F.offsets[S.site], n = F.offsets[S.site + 1] - e0 + 1;
+    for (int e = g; e < n; e += kGroup) {
+        const int k = neighbor(F, S.site, e0, e);
+        const float4* rp = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const SiteRec rc = {rp[0], rp[1], rp[2], rp[3]};
+        float v[3];
+        offset_to(rc.q0, x, v);
+        float* gb = G.block + kGradBlock * static_cast<int64_t>(k);
+        if (gs != 0.f) {
+            const float gd = gs * fexp(rc.q0.w - 0.5f * density_m(rc, v));
+            if (fabsf(gd) > kMinDensityGrad) {
+                float gA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                add_outer(gA, -0.5f * gd, v);
+                unsafeAtomicAdd(gb, gd);
+#pragma unroll
+                for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 1 + u, gA[u]);
+            }
+        }
+        if (colour) {
+            const float a = fexp(-0.5f * (color_m(rc.q2, rc.q3, v) - S.mmin)) * S.inv_a;
+            if (a >= kMinColourWeight) {
+                float c[3];
+                sh_eval_n<NV>(rp + kRec, b, nb, c);
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) {
+                    const float dc = c[ch] > 0.f ? a * gC[ch] : 0.f;
+                    if (dc != 0.f)
+                        for (int jj = 0; jj < nb; ++jj) unsafeAtomicAdd(gb + kGradSh + 3 * jj + ch, b[jj] * dc);
+                }
+                const float ga = gC[0] * fmaxf(c[0], 0.f) + gC[1] * fmaxf(c[1], 0.f) + gC[2] * fmaxf(c[2], 0.f);
+                const float gm = -0.5f * a * (ga - gCC);
+                if (gm != 0.f) {
+                    float gA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                    add_outer(gA, gm, v);
+#pragma unroll
+                    for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 7 + u, gA[u]);
+                }
+            }
+        }
+    }
+}
+
+// foam.cu:395-469: every sample collects half of the gradients of the segments on both sides.
+template <int NV>
+__device__ void train_ray_backward(const MarchField& F, const MarchParams& M, const TrainRays& R,
+                                   const MarchGradIn& GI, const MarchGradOut& G, const float* __restrict__ rec, int K,
+                                   const int* __restrict__ stats, int64_t r, int g) {
+    const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
+    const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
+    const float near = R.t_near[r], far = R.t_far[r];
+    const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
+    float b[16];
+    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+    const float gR[3] = {GI.g_rgb[3 * r], GI.g_rgb[3 * r + 1], GI.g_rgb[3 * r + 2]};
+    const float fg[3] = {GI.rgb[3 * r], GI.rgb[3 * r + 1], GI.rgb[3 * r + 2]};
+    const float gT_final = GI.g_T[r] * GI.T[r];
+    const int n_stored = rec != nullptr && stats[3 * r] <= K ? stats[3 * r] : 0;
+    TrainSample P, Q;
+    float te = 0.f, te2 = 0.f;
+    int nx = INT_MAX, nx2 = INT_MAX, cur = 0;
+    if (n_stored > 0) {
+        train_load(rec, r, K, 0, P);
+    } else {
+        int steps = 0;
+        cur = train_walk<block_vec4(NV)>(F, R.start[r], o, d, near, g, steps);
+        train_round<block_vec4(NV)>(F, cur, o, d, near, g, P, te, nx);
+    }
+    float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, gs_pending = 0.f, gC_pending[3] = {0.f, 0.f, 0.f};
+    for (int it = 0; it < kMaxCells; ++it) {
+        bool last;
+        if (n_stored > 0) {
+            if (it + 1 >= n_stored) break;
+            train_load(rec, r, K, it + 1, Q);
+            last = it + 2 >= n_stored;
+        } else {
+            last = nx == INT_MAX || te >= far;
+            train_round<block_vec4(NV)>(F, last ? cur : nx, o, d, last ? far : fmaxf(te, P.t), g, Q, te2, nx2);
+        }
+        const float delta = Q.t - P.t;
+        const float alpha = 1.f - fexp(-0.5f * (P.sigma + Q.sigma) * delta);
+        const float w = T * alpha;
+        const float T_next = T * (1.f - alpha);
+        const bool active = w > M.w_thresh;
+        float c[3] = {0.f, 0.f, 0.f};
+        if (active) {
+            if (!P.has_c) train_colour<NV>(F, o, d, b, nb, g, P);
+            if (!Q.has_c) train_colour<NV>(F, o, d, b, nb, g, Q);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) c[a] = 0.5f * (P.C[a] + Q.C[a]), acc[a] += w * c[a];
+        }
+        float g_sbar = 0.f;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) g_sbar += gR[a] * (T_next * c[a] - (fg[a] - acc[a]));
+        g_sbar = delta * (g_sbar - gT_final);
+        float gc_half[3], gC_P[3];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) gc_half[a] = active ? 0.5f * w * gR[a] : 0.f, gC_P[a] = gC_pending[a] + gc_half[a];
+        train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending + 0.5f * g_sbar, gC_P, g);
+        gs_pending = 0.5f * g_sbar;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) gC_pending[a] = gc_half[a];
+        T = T_next;
+        P = Q;
+        cur = Q.site, te = te2, nx = nx2;
+        if (last || T < M.t_thresh) break;
+    }
+    train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending, gC_pending, g);
+}
+
+__global__ void __launch_bounds__(kBlock)
+    train_backward_kernel(MarchField F, MarchParams M, TrainRays R, MarchGradIn GI, MarchGradOut G,
+                          const float* __restrict__ rec, int K, const int* __restrict__ stats) {
+    const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
+    const int g = threadIdx.x % kGroup;
+    if (r >= R.n) return;
+    if (R.start[r] < 0 || R.start[r] >= F.n_sites) return;  // not traced: no gradient
+    switch (F.sh_deg) {
+        case 0: train_ray_backward<sh_vec4_f32(0)>(F, M, R, GI, G, rec, K, stats, r, g); break;
+        case 1: train_ray_backward<sh_vec4_f32(1)>(F, M, R, GI, G, rec, K, stats, r, g); break;
+        case 2: train_ray_backward<sh_vec4_f32(2)>(F, M, R, GI, G, rec, K, stats, r, g); break;
+        default: train_ray_backward<sh_vec4_f32(3)>(F, M, R, GI, G, rec, K, stats, r, g); break;
+    }
+}
+
 // Grid-stride fill with zeros (a kernel, not a memset, so that a captured stream records no memset node).
 constexpr int64_t kZeroBlocks = 4096;
 __global__ void __launch_bounds__(256) zero_kernel(float* __restrict__ p, int64_t n) {
@@ -1241,4 +1570,99 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
     hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(61 * n_sites, 256)), dim3(256), 0, s, block, n_sites, g_raw,
                        g_dA, g_cA, g_sh);
     return launch_status("march_backward_kernel");
+}
+
+extern "C" int64_t vgr_foam_work_size(int64_t n_sites, int64_t sh_deg) {
+    return vgr_march_backward_work_size(n_sites, sh_deg);
+}
+
+namespace vgr {
+namespace {
+int train_check(int64_t n_sites, int64_t n_adj, int64_t sh_deg, int64_t n_rays, int64_t record_cap, const void* work,
+                int64_t work_bytes, const char* who) {
+    VGR_REQUIRE(n_rays >= 0, "%s: n_rays must be >= 0 (got %lld)", who, static_cast<long long>(n_rays));
+    VGR_REQUIRE(sh_deg >= 0 && sh_deg <= 3, "sh_deg must be in [0, 3] (got %lld)", static_cast<long long>(sh_deg));
+    VGR_REQUIRE(record_cap >= 0 && record_cap <= INT_MAX, "%s: record_cap must be in [0, 2^31)", who);
+    VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "%s: n_sites must be in [1, 2^31)", who);
+    VGR_REQUIRE(n_adj >= 0 && n_adj <= INT_MAX, "%s: n_adj must be in [0, 2^31)", who);
+    const int64_t need = vgr_foam_work_size(n_sites, sh_deg);
+    VGR_REQUIRE(work && work_bytes >= need, "%s: work must hold %lld bytes", who, static_cast<long long>(need));
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "%s: work must be 256-byte aligned", who);
+    return VGR_OK;
+}
+}  // namespace
+}  // namespace vgr
+
+extern "C" int vgr_foam_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                                int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                                int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                                const float* near_t, const float* far_t, int64_t n_rays, double t_thresh,
+                                double w_thresh, float* rgb, float* T, float* depth, int32_t* stats, float* rec,
+                                int64_t record_cap, void* work, int64_t work_bytes, void* stream) {
+    using namespace vgr;
+    if (n_rays == 0) {
+        VGR_REQUIRE(record_cap >= 0, "foam_forward: record_cap must be >= 0");
+        return VGR_OK;
+    }
+    const int st = train_check(n_sites, n_adj, sh_deg, n_rays, record_cap, work, work_bytes, "foam_forward");
+    if (st != VGR_OK) return st;
+    VGR_REQUIRE(points && offsets && (adj || n_adj == 0) && raw && dA && cA && sh, "foam_forward: null field pointer");
+    VGR_REQUIRE(o && d && start && near_t && far_t, "foam_forward: null ray pointer");
+    VGR_REQUIRE(rgb && T && depth && stats, "foam_forward: null output pointer");
+    VGR_REQUIRE(record_cap == 0 || rec, "foam_forward: record_cap > 0 needs rec");
+    const hipStream_t s = as_stream(stream);
+    float4* recb = static_cast<float4*>(work);
+    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
+    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
+                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
+    const MarchField F{recb, offsets, adj, int(sh_deg), int(n_sites)};
+    const MarchParams M{1.f, 0, float(t_thresh), float(w_thresh)};
+    const TrainRays R{o, d, start, near_t, far_t, n_rays};
+    const MarchOut O{rgb, T, depth, stats, nullptr, 0};
+    hipLaunchKernelGGL(train_forward_kernel, dim3(grid_for(n_rays * kGroup, kBlock)), dim3(kBlock), 0, s, F, M, R, O,
+                       record_cap > 0 ? rec : nullptr, int(record_cap));
+    return launch_status("train_forward_kernel");
+}
+
+extern "C" int vgr_foam_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
+                                 int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
+                                 int64_t sh_deg, const float* o, const float* d, const int32_t* start,
+                                 const float* near_t, const float* far_t, int64_t n_rays, double t_thresh,
+                                 double w_thresh, const float* rgb, const float* T, const float* g_rgb,
+                                 const float* g_T, const float* rec, int64_t record_cap, const int32_t* stats,
+                                 float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work, int64_t work_bytes,
+                                 void* stream) {
+    using namespace vgr;
+    VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_backward: n_sites must be in [1, 2^31)");
+    VGR_REQUIRE(g_raw && g_dA && g_cA && g_sh, "foam_backward: null gradient pointer");
+    const hipStream_t s = as_stream(stream);
+    if (n_rays == 0) {
+        float* const outs[4] = {g_raw, g_dA, g_cA, g_sh};
+        const int64_t sizes[4] = {n_sites, 6 * n_sites, 6 * n_sites, 48 * n_sites};
+        for (int u = 0; u < 4; ++u)
+            hipLaunchKernelGGL(zero_kernel, dim3(kZeroBlocks), dim3(256), 0, s, outs[u], sizes[u]);
+        return launch_status("foam_backward zero");
+    }
+    const int st = train_check(n_sites, n_adj, sh_deg, n_rays, record_cap, work, work_bytes, "foam_backward");
+    if (st != VGR_OK) return st;
+    VGR_REQUIRE(points && offsets && (adj || n_adj == 0) && raw && dA && cA && sh, "foam_backward: null field pointer");
+    VGR_REQUIRE(o && d && start && near_t && far_t, "foam_backward: null ray pointer");
+    VGR_REQUIRE(rgb && T && g_rgb && g_T, "foam_backward: null forward output or upstream gradient pointer");
+    VGR_REQUIRE(record_cap == 0 || (rec && stats), "foam_backward: records need rec and the forward's stats");
+    float4* recb = static_cast<float4*>(work);
+    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
+    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
+                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
+    float* block = reinterpret_cast<float*>(static_cast<char*>(work) + vgr_march_work_size(n_sites, sh_deg));
+    hipLaunchKernelGGL(zero_kernel, dim3(kZeroBlocks), dim3(256), 0, s, block, kGradBlock * n_sites);
+    const MarchField F{recb, offsets, adj, int(sh_deg), int(n_sites)};
+    const MarchParams M{1.f, 0, float(t_thresh), float(w_thresh)};
+    const TrainRays R{o, d, start, near_t, far_t, n_rays};
+    const MarchGradIn GI{rgb, T, g_rgb, g_T};
+    const MarchGradOut G{block};
+    hipLaunchKernelGGL(train_backward_kernel, dim3(grid_for(n_rays * kGroup, kBlock)), dim3(kBlock), 0, s, F, M, R,
+                       GI, G, record_cap > 0 ? rec : nullptr, int(record_cap), stats);
+    hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(61 * n_sites, 256)), dim3(256), 0, s, block, n_sites, g_raw,
+                       g_dA, g_cA, g_sh);
+    return launch_status("train_backward_kernel");
 }

@@ -26,6 +26,11 @@ SIGNATURES = {
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
 	'vgr_march_backward_work_size': [_I64, _I64],
+	'vgr_foam_work_size': [_I64, _I64],
+	'vgr_foam_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64, _P, _P,
+						 _P, _P, _P, _I64, _P, _I64, _P],
+	'vgr_foam_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64, _P, _P,
+						  _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_march_forward_lanes': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64,
 								_I64, _F64, _F64, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
 	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
@@ -56,7 +61,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 _lib = None
 
 
@@ -75,6 +80,7 @@ def load():
 		lib.vgr_grid_work_size.restype = ctypes.c_int64
 		lib.vgr_march_work_size.restype = ctypes.c_int64
 		lib.vgr_march_backward_work_size.restype = ctypes.c_int64
+		lib.vgr_foam_work_size.restype = ctypes.c_int64
 		lib.vgr_field_work_size.restype = ctypes.c_int64
 		lib.vgr_color_backward_work_size.restype = ctypes.c_int64
 		lib.vgr_density_backward_work_size.restype = ctypes.c_int64

@@ -390,13 +390,86 @@ def bake_colors(points4, sh32, sh_deg, center, attr):
 	return attr
 
 
-_FIELD, _MARCH, _FOAM_INFER = _FieldExtension(), _MarchExtension(), _FoamInferExtension()
+# ============================================================================ foam.cu (training renderer)
+
+class _FoamExtension:
+	@staticmethod
+	def _check_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far):
+		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
+						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
+						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
+						  (d, 'd', torch.float32), (start, 'start', torch.int32), (near, 'near', torch.float32),
+						  (far, 'far', torch.float32)):
+			_check(t, n, dtp)
+		_require(sh.dim() == 3 and sh.size(1) == 16 and sh.size(2) == 3, 'sh must be (N, 16, 3)')
+		_require(dA.size(1) == 6 and cA.size(1) == 6, 'conics must be (N, 6)')
+
+	@staticmethod
+	def foam_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
+					 record_cap):
+		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32, rec (B or 0, record_cap, 8)]
+		(foam.cu:471-497)."""
+		_FoamExtension._check_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
+		B, dev, n = o.size(0), o.device, points.numel() // 3
+		K = int(record_cap)
+		_require(K >= 0, 'record_cap must be >= 0')
+		rgb = torch.empty(B, 3, device=dev)
+		T = torch.empty(B, device=dev)
+		depth = torch.empty(B, device=dev)
+		stats = torch.empty(B, 3, dtype=torch.int32, device=dev)
+		rec = torch.empty(B if K > 0 else 0, K, 8, device=dev)
+		if B == 0:
+			return [rgb, T, depth, stats, rec]
+		wb = int(_lib.load().vgr_foam_work_size(n, int(sh_deg)))
+		work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
+		with torch.cuda.device(dev):
+			call('vgr_foam_forward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA), ptr(cA),
+				 ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B, float(t_thresh),
+				 float(w_thresh), ptr(rgb), ptr(T), ptr(depth), ptr(stats), ptr(rec) if K > 0 else None, K,
+				 ptr(work), wb, stream_of(dev))
+		return [rgb, T, depth, stats, rec]
+
+	@staticmethod
+	def foam_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
+					  rgb, T, g_rgb, g_T, rec, stats):
+		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (foam.cu:499-531). rec (B, K, 8) with the
+		forward's stats, or an empty rec to re-trace every ray."""
+		_FoamExtension._check_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
+		for t, nm in ((rgb, 'rgb'), (T, 'T'), (g_rgb, 'g_rgb'), (g_T, 'g_T'), (rec, 'rec')):
+			_check(t, nm, torch.float32)
+		_check(stats, 'stats', torch.int32)
+		B, dev, n = o.size(0), o.device, points.numel() // 3
+		_require(rgb.shape == g_rgb.shape == (B, 3) and T.shape == g_T.shape == (B,),
+				 'rgb, g_rgb must be (B, 3) and T, g_T (B,)')
+		replay = rec.numel() > 0
+		_require(not replay or (rec.dim() == 3 and rec.size(0) == B and rec.size(2) == 8), 'rec must be (B, K, 8)')
+		_require(not replay or stats.shape == (B, 3), 'stats must be (B, 3)')
+		K = rec.size(1) if replay else 0
+		g = [torch.empty(n, device=dev), torch.empty(n, 6, device=dev), torch.empty(n, 6, device=dev),
+			 torch.empty(n, 16, 3, device=dev)]
+		wb = int(_lib.load().vgr_foam_work_size(n, int(sh_deg)))
+		work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
+		with torch.cuda.device(dev):
+			call('vgr_foam_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
+				 ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B, float(t_thresh),
+				 float(w_thresh), ptr(rgb), ptr(T), ptr(g_rgb), ptr(g_T), ptr(rec) if replay else None, K,
+				 ptr(stats) if replay else None, *[ptr(x) for x in g], ptr(work), wb, stream_of(dev))
+		return g
+
+
+_FIELD, _MARCH, _FOAM_INFER, _FOAM = _FieldExtension(), _MarchExtension(), _FoamInferExtension(), _FoamExtension()
 
 
 def extension():
 	"""vgf.cu forward operators (reference: ext.py:30-31)."""
 	_lib.load()
 	return _FIELD
+
+
+def foam_extension():
+	"""foam.cu, the training renderer (reference: ext.py:38-39)."""
+	_lib.load()
+	return _FOAM
 
 
 def march_extension():
@@ -409,11 +482,6 @@ def foam_infer_extension():
 	"""foam_infer.cu (reference: ext.py:42-43)."""
 	_lib.load()
 	return _FOAM_INFER
-
-
-def foam_extension():
-	"""The training foam kernel (csrc/foam.cu, forward with records + backward) is not part of this build."""
-	raise NotImplementedError('the training renderer (foam.cu) is out of scope: use foam_infer_extension()')
 
 
 class Graph:
@@ -563,3 +631,41 @@ def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
 		return march_extension().march_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
 											   cfg[0], *rays, *cfg[1:])
 	return _March.apply(*params, graph, rays, cfg)
+
+
+class _Foam(torch.autograd.Function):
+	"""The training renderer with its backward (ext.py:185-206)."""
+
+	@staticmethod
+	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg, record_cap):
+		rgb, T, depth, stats, rec = foam_extension().foam_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
+																  sh, cfg[0], *rays, *cfg[1:], record_cap)
+		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, rec, stats, *rays)
+		ctx.graph, ctx.cfg = graph, cfg
+		ctx.mark_non_differentiable(depth, stats)
+		return rgb, T, depth, stats
+
+	@staticmethod
+	def backward(ctx, g_rgb, g_T, _g_depth, _g_stats):
+		raw, dA, cA, sh, rgb, T, rec, stats, *rays = ctx.saved_tensors
+		g, cfg = ctx.graph, ctx.cfg
+		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
+		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
+		grads = foam_extension().foam_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays, *cfg[1:],
+											   rgb, T, g_rgb, g_T, rec, stats)
+		return (*grads, None, None, None, None)
+
+
+def foam(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, record_cap=256):
+	"""Rendering at the interaction points of the rays with the Voronoi faces -> foreground rgb (B, 3), final
+	transmittance (B,), depth (B,), per-ray stats (B, 3) int: samples, segments with colour, walk steps to x(near).
+	With gradients, up to record_cap samples per ray are kept for the backward pass (0: re-trace every ray)
+	(ext.py:209-216)."""
+	rays = tuple(t.float().contiguous() for t in (o, d)) + (start.int().contiguous(),) + \
+		tuple(t.float().contiguous() for t in (near, far))
+	cfg = (int(sh_deg), float(t_thresh), float(w_thresh))
+	params = [p.float().contiguous() for p in (raw, dA, cA, sh)]
+	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
+		return foam_extension().foam_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
+											 cfg[0], *rays, *cfg[1:], 0)[:4]
+	return _Foam.apply(*params, graph, rays, cfg, int(record_cap))
