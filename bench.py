@@ -16,6 +16,8 @@ Other rows of the path, each as one JSON line of the same form (not the headline
   --workload traverse the cell traversal alone (foam_infer stage 0) on config 3 in both layouts: one ray per lane
                       (foam_infer) against a group of lanes per ray testing a cell's faces in parallel (--lanes)
   --workload march-grad  a training step of the uniform march on config 5: forward + backward of --batch rays
+  --workload foam-grad   a training step of the training renderer (foam.cu) on config 3: forward with records +
+                         backward of --batch rays
   --workload field    the NeRF-path operators (walk, density_forward, color_forward, conic_forward) on config 3,
                       one 1920x1080 frame at 64 stratified samples per ray (render_rays' first round)
 """
@@ -127,7 +129,8 @@ def main():
 	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
 	ap.add_argument('--workload', default='foam',
-					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse', 'march-grad'],
+					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse', 'march-grad',
+							 'foam-grad'],
 					help='foam: the headline (foam_infer, config 3); march / locate (config 5), field (config 3): '
 						 'the other rows')
 	args = ap.parse_args()
@@ -152,6 +155,8 @@ def main():
 		return bench_traverse(args)
 	if args.workload == 'march-grad':
 		return bench_march_grad(args)
+	if args.workload == 'foam-grad':
+		return bench_foam_grad(args)
 	if args.workload == 'grad':
 		return bench_grad(args)
 	bench_foam(args)
@@ -339,6 +344,109 @@ def emit(metric, value, unit, args, ms, config, roofline, cpu, dtype='f32'):
 		   'vs_baseline': None, 'dtype': dtype, 'data': 'synthetic', 'config': config, 'roofline': roofline,
 		   'cpu_baseline': cpu}
 	print(json.dumps(res), flush=True)
+
+
+def training_rays(sc, points, B, dev, seed=0):
+	"""B rays drawn uniformly over the pixels of the scene's cameras (scene.random_rays, train.py:132), with the
+	start site of each camera's eye -> o, d, start (device tensors)."""
+	import numpy as np
+	import torch
+
+	from vgr.sites import nearest_sites
+	rng = np.random.default_rng(seed)
+	cams = rng.integers(0, len(sc.cameras), B)
+	o_l, d_l, e_l = [], [], []
+	for c in range(len(sc.cameras)):
+		n_c = int((cams == c).sum())
+		o_c, d_c = sc.cameras[c].rays()
+		pick = rng.choice(len(o_c), n_c, replace=False)
+		o_l.append(o_c[pick]), d_l.append(d_c[pick]), e_l.append(np.repeat(sc.cameras[c].eye[None], n_c, 0))
+	o = torch.from_numpy(np.concatenate(o_l)).to(dev)
+	d = torch.from_numpy(np.concatenate(d_l)).to(dev)
+	pts = torch.from_numpy(np.concatenate(e_l).astype(np.float32)).to(dev)
+	return o, d, nearest_sites(points, pts)
+
+
+def bench_foam_grad(args):
+	"""A training step of the training renderer (render_rays_foam under autograd, train.py's default renderer,
+	train.py:117,132) on config 3: --batch rays (train.py's default 4096) drawn over the pixels of the 4 cameras;
+	vgr_foam_forward recording up to 256 samples per ray (ext.foam's default), then vgr_foam_backward replaying the
+	records with random upstream gradients. value = rays per second through forward + backward; a second leg times
+	16 x the batch. CPU baseline: the C oracle's backward (one thread, re-tracing) on a bounded subset.
+
+	Algorithmic bytes of the backward launch (E = mean self-inclusive neighbourhood, SHB = 12 (deg + 1)^2): per
+	sample the record 32 B and one scatter round E (16 + 28 + 28) (point, raw and density conic read, gradients
+	written); per coloured sample E (SHB + 24 + SHB) more (SH read, colour-conic and SH gradient)."""
+	import numpy as np
+	import torch
+
+	from vgr import ext, render, scenes
+	from vgr.model import VoronoiGaussField
+	dev = torch.device('cuda:0')
+	sc = scenes.make_scene(3, scale=args.scale, log=log)
+	model = VoronoiGaussField.from_scene(sc, dev)
+	g = model.graph
+	dA = ext.conic(model.d_log_scale, model.d_quat, 0.0).contiguous()
+	cA = ext.conic(model.c_log_scale, model.c_quat, 0.0).contiguous()
+	sh = model.sh().contiguous()
+	fx = ext.foam_extension()
+	stream = torch.cuda.current_stream(dev)
+	E = 1.0 + len(sc.adj) / sc.n_sites
+	SHB = 12 * (sc.sh_deg + 1) ** 2
+	legs = {}
+	for B in (args.batch, 16 * args.batch):
+		o, d, start = training_rays(sc, g.points, B, dev)
+		near, _, far = render.ray_bounds(o, d, 0.02, sc.far_radius)
+		rays = (o, d, start, near, far)
+		fwd = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, 1e-4, 1e-4)
+		gen = torch.Generator(device=dev).manual_seed(0)
+		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
+		f_ms, out, _ = time_steps(lambda: fx.foam_forward(*fwd, 256), args.steps, args.warmup, stream)
+		rgb, T, _, stats, rec = out
+		b_ms, _, _ = time_steps(lambda: fx.foam_backward(*fwd, rgb, T, g_rgb, g_T, rec, stats), args.steps,
+								args.warmup, stream)
+		st = stats.double()
+		bwd_bytes = float(st[:, 0].sum() * (32 + E * 72) + st[:, 1].sum() * 2 * E * (2 * SHB + 24))
+		legs[B] = dict(fwd=float(np.mean(f_ms)), bwd=float(np.mean(b_ms)), bytes=bwd_bytes, rays=rays, rgb=rgb, T=T,
+					   g_rgb=g_rgb, g_T=g_T, samples=float(st[:, 0].mean()), coloured=float(st[:, 1].mean()),
+					   fits=float((stats[:, 0] <= 256).double().mean()))
+		L = legs[B]
+		log(f'{B} rays: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms; samples/ray {L["samples"]:.1f}, '
+			f'coloured segments {L["coloured"]:.1f}, rays within the records {100 * L["fits"]:.1f} %')
+	L = legs[args.batch]
+	ms = L['fwd'] + L['bwd']
+	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
+	cpu = None
+	if args.cpu_seconds > 0:
+		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+		import oracle
+		host = [x.cpu().numpy() for x in (g.points, g.offsets, g.adj, model.raw, dA, cA, sh)]
+		rays = [x.cpu().numpy() for x in L['rays']]
+		up = [x.cpu().numpy() for x in (L['rgb'], L['T'], L['g_rgb'], L['g_T'])]
+		B = args.batch
+		probe = np.arange(0, B, max(1, B // 16))
+		t1 = time.perf_counter()
+		oracle.foam_backward(*host, sc.sh_deg, *[r[probe] for r in rays], *[u[probe] for u in up])
+		rate = len(probe) / max(time.perf_counter() - t1, 1e-6)
+		sel = np.arange(0, B, max(1, int(B / (rate * args.cpu_seconds))))
+		t1 = time.perf_counter()
+		oracle.foam_backward(*host, sc.sh_deg, *[r[sel] for r in rays], *[u[sel] for u in up])
+		secs = time.perf_counter() - t1
+		cpu = {'value': round(len(sel) / secs / 1e3, 4), 'unit': 'Krays/s (backward only)', 'cores': 1,
+			   'kind': 'port', 'sample': f'every {B // len(sel)}th ray of the batch ({len(sel)} rays), C oracle '
+										 f'foam_backward (re-tracing), one thread'}
+	big = legs[16 * args.batch]
+	emit('Mrays/s through foam forward + backward (training batch)', mrays_per_s(args.batch, ms), 'Mrays/s', args, ms,
+		 {'workload': f'config 3 training step of the training renderer: {args.batch} random rays over the 4 '
+					  f'cameras, foam_forward (256 records per ray) + foam_backward', 'sites': sc.n_sites,
+		  'rays_per_step': args.batch, 'forward_ms': round(L['fwd'], 4), 'backward_ms': round(L['bwd'], 4),
+		  'samples_per_ray': round(L['samples'], 2), 'coloured_segments_per_ray': round(L['coloured'], 2),
+		  'rays_within_records': round(L['fits'], 4),
+		  f'rays_{16 * args.batch}': {'forward_ms': round(big['fwd'], 3), 'backward_ms': round(big['bwd'], 3),
+									  'Mrays_per_s': round(mrays_per_s(16 * args.batch, big['fwd'] + big['bwd']), 3)}},
+		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
+		  'frac': round(achieved / 8000.0, 4), 'traffic': None, 'kernel': 'train_backward_kernel',
+		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
 
 
 def bench_march_grad(args):

@@ -539,6 +539,30 @@ constexpr int64_t kCoopRays = 16384;
 // their LDS slot; then the wave adds the rows one at a time, lane t of the wave adding float t of the row's 64-float
 // block. A row is one atomic instruction touching two cache lines instead of up to 61 instructions touching 64 lines
 // each. With many waves in flight the vector memory pipeline's line rate bounds the per-lane form, and this one wins.
+// Adds the rows the lanes of `rows` published in their LDS slots, one row at a time: float t of the 64-float
+// gradient block of the row's site k gets slot value t (t < 13) or b_j dc_c (t = 16 + 3 j + c), the wave's active
+// lanes taking t = rank, rank + n_act, ... (one atomic instruction per row, two cache lines).
+__device__ __forceinline__ void add_rows(const MarchGradOut& G, const float* __restrict__ slots, uint64_t rows, int k,
+                                         int nb, int rank, int n_act) {
+    while (rows != 0) {
+        const int L = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<unsigned long long>(rows)) - 1);
+        rows &= rows - 1;
+        const int kL = __builtin_amdgcn_readlane(k, L);
+        const float* s = slots + kSlot * L;
+        float* gb = G.block + kGradBlock * static_cast<int64_t>(kL);
+        for (int t = rank; t < kGradBlock; t += n_act) {
+            float v = 0.f;
+            if (t < 13) {
+                v = s[t];
+            } else if (t >= kGradSh) {
+                const int q = t - kGradSh, j = q / 3;
+                if (j < nb) v = s[16 + j] * s[13 + q % 3];
+            }
+            if (v != 0.f) unsafeAtomicAdd(gb + t, v);
+        }
+    }
+}
+
 template <int NV>
 __device__ void grad_pass_wave(const MarchField& F, const MarchGradOut& G, int i, bool has, const float (&o)[3],
                                const float (&d)[3], const float (&b)[16], int nb, const float (&gR)[3],
@@ -567,24 +591,7 @@ __device__ void grad_pass_wave(const MarchField& F, const MarchGradOut& G, int i
             }
         }
         __builtin_amdgcn_wave_barrier();
-        uint64_t rows = __ballot(row);
-        while (rows != 0) {
-            const int L = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<unsigned long long>(rows)) - 1);
-            rows &= rows - 1;
-            const int kL = __builtin_amdgcn_readlane(k, L);
-            const float* s = slots + kSlot * L;
-            float* gb = G.block + kGradBlock * static_cast<int64_t>(kL);
-            for (int t = rank; t < kGradBlock; t += n_act) {
-                float v = 0.f;
-                if (t < 13) {
-                    v = s[t];
-                } else if (t >= kGradSh) {
-                    const int q = t - kGradSh, j = q / 3;
-                    if (j < nb) v = s[16 + j] * s[13 + q % 3];
-                }
-                if (v != 0.f) unsafeAtomicAdd(gb + t, v);
-            }
-        }
+        add_rows(G, slots, __ballot(row), k, nb, rank, n_act);
         __builtin_amdgcn_wave_barrier();
     }
 }
@@ -1281,56 +1288,66 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
-// A sample's gradients (gs = dL/dsigma, gC = dL/dC) over its site's neighbourhood, each lane adding its neighbours'
-// with atomics into their gradient blocks; foam.cu:303-343.
+// A sample's gradients (gs = dL/dsigma, gC = dL/dC) over its site's neighbourhood (foam.cu:303-343). Each lane
+// computes its neighbours' contributions and publishes them in its LDS slot; the wave adds the rows with add_rows
+// (scattered fp32 atomics, one per lane and float, ran this kernel at ~16 G atomics/s, where a row is one atomic
+// instruction on two lines). The neighbour rounds run in step across the wave: every active lane takes part in
+// every round, lanes of rays with fewer neighbours (or nothing to add) idle.
 template <int NV>
 __device__ void train_scatter(const MarchField& F, const MarchGradOut& G, const float (&o)[3], const float (&d)[3],
                               const float (&b)[16], int nb, const TrainSample& S, float gs, const float (&gC)[3],
-                              int g) {
+                              int g, float* __restrict__ slots) {
     const bool colour = S.has_c && (gC[0] != 0.f || gC[1] != 0.f || gC[2] != 0.f);
-    if (gs == 0.f && !colour) return;
+    int e0 = 0, n = 0;
+    if (gs != 0.f || colour) e0 = F.offsets[S.site], n = F.offsets[S.site + 1] - e0 + 1;
     float x[3];
     point_at(o, d, S.t, x);
     const float gCC = gC[0] * S.C[0] + gC[1] * S.C[1] + gC[2] * S.C[2];
-    const int e0 = F.offsets[S.site], n = F.offsets[S.site + 1] - e0 + 1;
-    for (int e = g; e < n; e += kGroup) {
-        const int k = neighbor(F, S.site, e0, e);
-        const float4* rp = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
-        const SiteRec rc = {rp[0], rp[1], rp[2], rp[3]};
-        float v[3];
-        offset_to(rc.q0, x, v);
-        float* gb = G.block + kGradBlock * static_cast<int64_t>(k);
-        if (gs != 0.f) {
-            const float gd = gs * fexp(rc.q0.w - 0.5f * density_m(rc, v));
-            if (fabsf(gd) > kMinDensityGrad) {
-                float gA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                add_outer(gA, -0.5f * gd, v);
-                unsafeAtomicAdd(gb, gd);
-#pragma unroll
-                for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 1 + u, gA[u]);
+    const int lane = threadIdx.x & 63;
+    float* mine = slots + kSlot * lane;
+    const uint64_t act = __ballot(1);
+    const int n_act = __popcll(act);
+    const int rank = __popcll(act & ((uint64_t(1) << lane) - 1));
+    for (int base = 0; __ballot(base < n) != 0; base += kGroup) {
+        const int e = base + g;
+        int k = 0;
+        bool row = false;
+        if (e < n) {
+            k = neighbor(F, S.site, e0, e);
+            const float4* rp = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+            const SiteRec rc = {rp[0], rp[1], rp[2], rp[3]};
+            float v[3];
+            offset_to(rc.q0, x, v);
+            float graw = 0.f, gdA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, gcA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            float dc[3] = {0.f, 0.f, 0.f};
+            if (gs != 0.f) {
+                const float gd = gs * fexp(rc.q0.w - 0.5f * density_m(rc, v));
+                if (fabsf(gd) > kMinDensityGrad) graw = gd, add_outer(gdA, -0.5f * gd, v), row = true;
             }
-        }
-        if (colour) {
-            const float a = fexp(-0.5f * (color_m(rc.q2, rc.q3, v) - S.mmin)) * S.inv_a;
-            if (a >= kMinColourWeight) {
-                float c[3];
-                sh_eval_n<NV>(rp + kRec, b, nb, c);
+            if (colour) {
+                const float a = fexp(-0.5f * (color_m(rc.q2, rc.q3, v) - S.mmin)) * S.inv_a;
+                if (a >= kMinColourWeight) {
+                    float c[3];
+                    sh_eval_n<NV>(rp + kRec, b, nb, c);
 #pragma unroll
-                for (int ch = 0; ch < 3; ++ch) {
-                    const float dc = c[ch] > 0.f ? a * gC[ch] : 0.f;
-                    if (dc != 0.f)
-                        for (int jj = 0; jj < nb; ++jj) unsafeAtomicAdd(gb + kGradSh + 3 * jj + ch, b[jj] * dc);
-                }
-                const float ga = gC[0] * fmaxf(c[0], 0.f) + gC[1] * fmaxf(c[1], 0.f) + gC[2] * fmaxf(c[2], 0.f);
-                const float gm = -0.5f * a * (ga - gCC);
-                if (gm != 0.f) {
-                    float gA[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                    add_outer(gA, gm, v);
-#pragma unroll
-                    for (int u = 0; u < 6; ++u) unsafeAtomicAdd(gb + 7 + u, gA[u]);
+                    for (int ch = 0; ch < 3; ++ch) dc[ch] = c[ch] > 0.f ? a * gC[ch] : 0.f;
+                    const float ga = gC[0] * fmaxf(c[0], 0.f) + gC[1] * fmaxf(c[1], 0.f) + gC[2] * fmaxf(c[2], 0.f);
+                    const float gm = -0.5f * a * (ga - gCC);
+                    if (gm != 0.f) add_outer(gcA, gm, v);
+                    row = true;
                 }
             }
+            if (row) {
+                mine[0] = graw;
+#pragma unroll
+                for (int u = 0; u < 6; ++u) mine[1 + u] = gdA[u], mine[7 + u] = gcA[u];
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) mine[13 + ch] = dc[ch];
+            }
         }
+        __builtin_amdgcn_wave_barrier();
+        add_rows(G, slots, __ballot(row), k, nb, rank, n_act);
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1338,7 +1355,7 @@ __device__ void train_scatter(const MarchField& F, const MarchGradOut& G, const 
 template <int NV>
 __device__ void train_ray_backward(const MarchField& F, const MarchParams& M, const TrainRays& R,
                                    const MarchGradIn& GI, const MarchGradOut& G, const float* __restrict__ rec, int K,
-                                   const int* __restrict__ stats, int64_t r, int g) {
+                                   const int* __restrict__ stats, int64_t r, int g, float* __restrict__ slots) {
     const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
     const float near = R.t_near[r], far = R.t_far[r];
@@ -1348,6 +1365,8 @@ __device__ void train_ray_backward(const MarchField& F, const MarchParams& M, co
     const float gR[3] = {GI.g_rgb[3 * r], GI.g_rgb[3 * r + 1], GI.g_rgb[3 * r + 2]};
     const float fg[3] = {GI.rgb[3 * r], GI.rgb[3 * r + 1], GI.rgb[3 * r + 2]};
     const float gT_final = GI.g_T[r] * GI.T[r];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) slots[kSlot * (threadIdx.x & 63) + 16 + j] = b[j];
     const int n_stored = rec != nullptr && stats[3 * r] <= K ? stats[3 * r] : 0;
     TrainSample P, Q;
     float te = 0.f, te2 = 0.f;
@@ -1389,7 +1408,7 @@ __device__ void train_ray_backward(const MarchField& F, const MarchParams& M, co
         float gc_half[3], gC_P[3];
 #pragma unroll
         for (int a = 0; a < 3; ++a) gc_half[a] = active ? 0.5f * w * gR[a] : 0.f, gC_P[a] = gC_pending[a] + gc_half[a];
-        train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending + 0.5f * g_sbar, gC_P, g);
+        train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending + 0.5f * g_sbar, gC_P, g, slots);
         gs_pending = 0.5f * g_sbar;
 #pragma unroll
         for (int a = 0; a < 3; ++a) gC_pending[a] = gc_half[a];
@@ -1398,21 +1417,23 @@ __device__ void train_ray_backward(const MarchField& F, const MarchParams& M, co
         cur = Q.site, te = te2, nx = nx2;
         if (last || T < M.t_thresh) break;
     }
-    train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending, gC_pending, g);
+    train_scatter<NV>(F, G, o, d, b, nb, P, gs_pending, gC_pending, g, slots);
 }
 
 __global__ void __launch_bounds__(kBlock)
     train_backward_kernel(MarchField F, MarchParams M, TrainRays R, MarchGradIn GI, MarchGradOut G,
                           const float* __restrict__ rec, int K, const int* __restrict__ stats) {
+    static_assert(kBlock == 64, "the gradient slots are per wave: one wave per workgroup");
+    __shared__ float slots[kSlot * 64];
     const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
     const int g = threadIdx.x % kGroup;
     if (r >= R.n) return;
     if (R.start[r] < 0 || R.start[r] >= F.n_sites) return;  // not traced: no gradient
     switch (F.sh_deg) {
-        case 0: train_ray_backward<sh_vec4_f32(0)>(F, M, R, GI, G, rec, K, stats, r, g); break;
-        case 1: train_ray_backward<sh_vec4_f32(1)>(F, M, R, GI, G, rec, K, stats, r, g); break;
-        case 2: train_ray_backward<sh_vec4_f32(2)>(F, M, R, GI, G, rec, K, stats, r, g); break;
-        default: train_ray_backward<sh_vec4_f32(3)>(F, M, R, GI, G, rec, K, stats, r, g); break;
+        case 0: train_ray_backward<sh_vec4_f32(0)>(F, M, R, GI, G, rec, K, stats, r, g, slots); break;
+        case 1: train_ray_backward<sh_vec4_f32(1)>(F, M, R, GI, G, rec, K, stats, r, g, slots); break;
+        case 2: train_ray_backward<sh_vec4_f32(2)>(F, M, R, GI, G, rec, K, stats, r, g, slots); break;
+        default: train_ray_backward<sh_vec4_f32(3)>(F, M, R, GI, G, rec, K, stats, r, g, slots); break;
     }
 }
 
