@@ -493,7 +493,7 @@ def bench_march_grad(args):
 		fwd_args = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, dt, n_bg, 1e-4, 1e-4)
 		gen = torch.Generator(device=dev).manual_seed(0)
 		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
-		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 16384 rays
+		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 262144 rays
 			f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args, lanes=lanes), args.steps, args.warmup,
 									  stream)
 			rgb, T, _, stats = out
@@ -510,7 +510,7 @@ def bench_march_grad(args):
 			log(f'{B} rays, {lanes} lane(s) per ray: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms '
 				f'({bwd_bytes / L["bwd"] / 1e6:.0f} GB/s algorithmic); samples/ray {L["samples"]:.1f}, coloured '
 				f'{L["coloured"]:.1f}')
-	auto = 16 if args.batch < 16384 else 1
+	auto = 16 if args.batch < 262144 else 1
 	L = legs[args.batch, auto]
 	ms = L['fwd'] + L['bwd']
 	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
@@ -692,7 +692,7 @@ def bench_march(args):
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
-		  'lanes_per_ray': lanes or (16 if B < 16384 else 1)},
+		  'lanes_per_ray': lanes or (16 if B < 262144 else 1)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
 		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)

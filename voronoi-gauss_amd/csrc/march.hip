@@ -998,7 +998,8 @@ __device__ __forceinline__ void flush_slot(const MarchGradOut& G, int k, const f
 // theirs per sample. The formulas are those of march_ray_backward.
 template <int NV>
 __device__ void march_ray_group_backward(const MarchField& F, const MarchParams& M, const MarchRays& R,
-                                         const MarchGradIn& GI, const MarchGradOut& G, int64_t r, int cur, int g) {
+                                         const MarchGradIn& GI, const MarchGradOut& G, int64_t r, int cur, int g,
+                                         float* __restrict__ slots) {
     const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
     const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
@@ -1010,6 +1011,8 @@ __device__ void march_ray_group_backward(const MarchField& F, const MarchParams&
     const float gR[3] = {GI.g_rgb[3 * r], GI.g_rgb[3 * r + 1], GI.g_rgb[3 * r + 2]};
     const float fg[3] = {GI.rgb[3 * r], GI.rgb[3 * r + 1], GI.rgb[3 * r + 2]};
     const float gT_final = GI.g_T[r] * GI.T[r];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) slots[kSlot * (threadIdx.x & 63) + 16 + j] = b[j];
     int moves = 0;
     float T = 1.f, acc[3] = {0.f, 0.f, 0.f};
     GroupCell Cc;
@@ -1017,11 +1020,27 @@ __device__ void march_ray_group_backward(const MarchField& F, const MarchParams&
     SlotGrad S[kSlots];
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) clear_slot(S[s]);
+    // the slots' sums of the visit just left, added as rows shared by the resolving lanes of the wave
     auto flush = [&]() {
         if (Cc.cell < 0) return;
+        const int lane = threadIdx.x & 63;
+        float* mine = slots + kSlot * lane;
+        const uint64_t act = __ballot(1);
+        const int n_act = __popcll(act);
+        const int rank = __popcll(act & ((uint64_t(1) << lane) - 1));
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
-            if (Cc.k[s] >= 0) flush_slot(G, Cc.k[s], Cc.c[s], b, nb, gR, S[s]);
+            const bool row = Cc.k[s] >= 0 && (S[s].dens || S[s].col);
+            if (row) {
+                mine[0] = S[s].raw;
+#pragma unroll
+                for (int u = 0; u < 6; ++u) mine[1 + u] = S[s].dA[u], mine[7 + u] = S[s].cA[u];
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) mine[13 + ch] = S[s].col && Cc.c[s][ch] > 0.f ? gR[ch] * S[s].aw : 0.f;
+            }
+            __builtin_amdgcn_wave_barrier();
+            add_rows(G, slots, __ballot(row), Cc.k[s], nb, rank, n_act);
+            __builtin_amdgcn_wave_barrier();
             clear_slot(S[s]);
         }
     };
@@ -1081,16 +1100,18 @@ __device__ void march_ray_group_backward(const MarchField& F, const MarchParams&
 
 __global__ void __launch_bounds__(kBlock)
     march_group_backward_kernel(MarchField F, MarchParams M, MarchRays R, MarchGradIn GI, MarchGradOut G) {
+    static_assert(kBlock == 64, "the gradient slots are per wave: one wave per workgroup");
+    __shared__ float slots[kSlot * 64];
     const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
     const int g = threadIdx.x % kGroup;
     if (r >= R.n) return;
     const int cur = R.start[r];
     if (cur < 0 || cur >= F.n_sites) return;
     switch (F.sh_deg) {
-        case 0: march_ray_group_backward<sh_vec4_f32(0)>(F, M, R, GI, G, r, cur, g); break;
-        case 1: march_ray_group_backward<sh_vec4_f32(1)>(F, M, R, GI, G, r, cur, g); break;
-        case 2: march_ray_group_backward<sh_vec4_f32(2)>(F, M, R, GI, G, r, cur, g); break;
-        default: march_ray_group_backward<sh_vec4_f32(3)>(F, M, R, GI, G, r, cur, g); break;
+        case 0: march_ray_group_backward<sh_vec4_f32(0)>(F, M, R, GI, G, r, cur, g, slots); break;
+        case 1: march_ray_group_backward<sh_vec4_f32(1)>(F, M, R, GI, G, r, cur, g, slots); break;
+        case 2: march_ray_group_backward<sh_vec4_f32(2)>(F, M, R, GI, G, r, cur, g, slots); break;
+        default: march_ray_group_backward<sh_vec4_f32(3)>(F, M, R, GI, G, r, cur, g, slots); break;
     }
 }
 
@@ -1459,9 +1480,12 @@ extern "C" int64_t vgr_march_backward_work_size(int64_t n_sites, int64_t sh_deg)
 
 namespace vgr {
 namespace {
-// Launches of fewer rays take the 16-lane group layout: below about one wave per CU in one ray per lane, the launch is
-// bound by its rays' serial chains of loads, which the group shortens.
-constexpr int64_t kGroupRays = 16384;
+// Launches of fewer rays take the 16-lane group layout, for forward and backward alike (the backward replays the
+// forward's sums). Config 5, ms forward / backward, one ray per lane against 16 lanes per ray: 4,096 rays 34 / 86
+// against 6 / 17; 65,536 rays 42 / 192 against 24 / 72; 262,144 rays 77 / 407 against 83 / 252; the whole 16.7M-ray
+// batch forward 3,350 against 5,264. Below about one wave per CU in one ray per lane a launch is bound by its rays'
+// serial chains of loads, which the group shortens; its backward adds gradient rows shared by the wave.
+constexpr int64_t kGroupRays = 262144;
 
 int64_t march_lanes(int64_t lanes, int64_t n_rays) { return lanes != 0 ? lanes : n_rays < kGroupRays ? kGroup : 1; }
 }  // namespace
