@@ -1,16 +1,17 @@
-"""Operator boundary of the forward/inference path: the reference's ext.py API (ext.py:11-216) backed by the
+"""Operator boundary of the renderers and field operators: the reference's ext.py API (ext.py:11-216) backed by the
 hand-written gfx950 kernels of libvgr.so instead of JIT-built CUDA extensions.
 
 Same names, argument meaning and error behaviour as the reference:
   extension().walk / density_forward / color_forward / conic_forward       (csrc/vgf.cu:438-546)
   extension().density_backward / color_backward / conic_backward          (csrc/vgf.cu:121-148,179-198,284-424)
   march_extension().march_forward / march_backward                         (csrc/march.cu:383-428)
+  foam_extension().foam_forward / foam_backward                            (csrc/foam.cu:471-531)
   foam_infer_extension().foam_infer                                        (csrc/foam_infer.cu:376-435)
-  Graph, density, color, conic, conic_reference, march                     (ext.py:46-182)
+  Graph, density, color, conic, conic_reference, march, foam               (ext.py:46-216)
 Inputs are checked like the reference's TORCH_CHECKs (CUDA, contiguous, dtype, shapes) and a violation raises
 RuntimeError; outputs are allocated here with torch on the input's device and the kernels run asynchronously on
-torch's current stream. density, color, conic and march are autograd Functions whose backward runs the gradient
-kernels; the training renderer foam.cu (forward with records, backward) is not part of this build."""
+torch's current stream. density, color, conic, march and foam are autograd Functions whose backward runs the
+gradient kernels."""
 
 import torch
 
