@@ -116,3 +116,35 @@ def test_foam_train_edge_cases(gpu):
 		fx.foam_forward(*field, 4, *rt, 1e-4, 1e-4, 0)
 	with pytest.raises(RuntimeError, match='rec must be'):
 		fx.foam_backward(*field, 3, *rt, 1e-4, 1e-4, rgb, Tt, ones3, ones, rec[:3], stats)
+
+
+def test_render_rays_foam_training_step(gpu):
+	"""render.render_rays_foam (train.py's renderer, render.py:127-140) under autograd on the config-1 scene: the
+	gradients of every field parameter (through ext.conic for the scales and rotations) against the oracle's
+	backward chained with its conic backward, and the background's closed form."""
+	from vgr import render, scenes
+	from vgr.model import VoronoiGaussField
+	sc = scenes.make_scene(1, img_scale=0.5, cache_dir=None, log=None)
+	o, d, start, _ = sc.camera_rays(tile=8)
+	o, d, start = o[::4].copy(), d[::4].copy(), start[::4].copy()
+	model = VoronoiGaussField.from_scene(sc, gpu, requires_grad=True)
+	W = np.random.default_rng(14).normal(size=(len(o), 3)).astype(np.float32)
+	out = render.render_rays_foam(model, T(o, gpu), T(d, gpu), T(start, gpu))
+	(out['rgb'] * T(W, gpu)).sum().backward()
+	near, _, far = render.ray_bounds(T(o, gpu), T(d, gpu), 0.02, 4.0)
+	near, far = near.cpu().numpy(), far.cpu().numpy()
+	dA = oracle.conic(sc.log_scale, sc.quat, 0.0)
+	fw = oracle.foam_forward(sc.points, sc.offsets, sc.adj, sc.raw, dA, dA, sc.sh, sc.sh_deg, o, d, start, near, far)
+	np.testing.assert_allclose(out['rgb'].detach().cpu().numpy(), fw['rgb'] + 0.5 * fw['T'][:, None], atol=1e-4)
+	g_T = (0.5 * W).sum(1)
+	g_raw, g_dA, g_cA, g_sh = oracle.foam_backward(sc.points, sc.offsets, sc.adj, sc.raw, dA, dA, sc.sh, sc.sh_deg, o,
+												   d, start, near, far, fw['rgb'], fw['T'], W, g_T)
+	g_dls, g_dq = oracle.conic_backward(sc.log_scale, sc.quat, g_dA, 0.0)
+	g_cls, g_cq = oracle.conic_backward(sc.log_scale, sc.quat, g_cA, 0.0)
+	for name, p, r in (('raw', model.raw, g_raw), ('d_log_scale', model.d_log_scale, g_dls),
+					   ('d_quat', model.d_quat, g_dq), ('c_log_scale', model.c_log_scale, g_cls),
+					   ('c_quat', model.c_quat, g_cq), ('sh_dc', model.sh_dc, g_sh[:, :1])):
+		assert rel(p.grad.cpu().numpy(), r) < 1e-4, name
+	assert not model.sh_rest.grad.any()  # degree 0: no gradient beyond the DC term
+	np.testing.assert_allclose(model.bg_logit.grad.cpu().numpy(), 0.25 * (fw['T'][:, None] * W).sum(0), rtol=1e-4,
+							   atol=1e-4)

@@ -133,10 +133,20 @@ def render_rays_uniform(model, o, d, start, dt=1 / 512, n_bg=64, near=0.02, far_
 			'walk_steps': stats[:, 2].sum() / stats[:, 0].sum()}
 
 
-def render_rays_foam(*args, **kwargs):
-	"""The training renderer (csrc/foam.cu, render.py:127-140) is out of scope; render_rays_foam_infer computes the
-	same samples and quadrature."""
-	raise NotImplementedError('render_rays_foam (training kernel) is out of scope: use render_rays_foam_infer')
+def render_rays_foam(model, o, d, start, near=0.02, far_radius=4.0, t_thresh=1e-4, w_thresh=1e-4, scale_floor=0.0,
+					 perturb=False):
+	"""Samples at the crossings of each ray with the Voronoi faces (plus x(near) and x(far)), trapezoid
+	compositing, one fused kernel with a backward (ext.foam); train.py's default renderer (render.py:127-140)."""
+	near_t, _, far_t = ray_bounds(o, d, near, far_radius)
+	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
+	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
+	fg, T, depth, stats = ext.foam(model.graph, model.raw, dA, cA, model.sh(), model.sh_deg, o, d, start, near_t,
+								   far_t, t_thresh, w_thresh)
+	rgb = fg + T[:, None] * torch.sigmoid(model.bg_logit)
+	stats = stats.float()
+	segments = (stats[:, 0] - 1).sum().clamp_min(1)
+	return {'rgb': rgb, 'acc': 1.0 - T, 'depth': depth, 'samples': stats[:, 0].mean(),
+			'active': (stats[:, 1].sum() / segments).item(), 'walk_steps': stats[:, 2].mean()}
 
 
 def sh_basis(d, deg):
