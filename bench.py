@@ -380,7 +380,7 @@ def bench_foam_grad(args):
 	import numpy as np
 	import torch
 
-	from vgr import ext, render, scenes
+	from vgr import _lib, ext, render, scenes
 	from vgr.model import VoronoiGaussField
 	dev = torch.device('cuda:0')
 	sc = scenes.make_scene(3, scale=args.scale, log=log)
@@ -401,10 +401,12 @@ def bench_foam_grad(args):
 		fwd = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, 1e-4, 1e-4)
 		gen = torch.Generator(device=dev).manual_seed(0)
 		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
-		f_ms, out, _ = time_steps(lambda: fx.foam_forward(*fwd, 256), args.steps, args.warmup, stream)
+		# one workspace for both passes, as ext.foam's autograd uses it: the backward reuses the forward's blocks
+		work = torch.empty(int(_lib.load().vgr_foam_work_size(sc.n_sites, sc.sh_deg)), dtype=torch.uint8, device=dev)
+		f_ms, out, _ = time_steps(lambda: fx.foam_forward(*fwd, 256, work=work), args.steps, args.warmup, stream)
 		rgb, T, _, stats, rec = out
-		b_ms, _, _ = time_steps(lambda: fx.foam_backward(*fwd, rgb, T, g_rgb, g_T, rec, stats), args.steps,
-								args.warmup, stream)
+		b_ms, _, _ = time_steps(lambda: fx.foam_backward(*fwd, rgb, T, g_rgb, g_T, rec, stats, work=work),
+								args.steps, args.warmup, stream)
 		st = stats.double()
 		bwd_bytes = float(st[:, 0].sum() * (32 + E * 72) + st[:, 1].sum() * 2 * E * (2 * SHB + 24))
 		legs[B] = dict(fwd=float(np.mean(f_ms)), bwd=float(np.mean(b_ms)), bytes=bwd_bytes, rays=rays, rgb=rgb, T=T,
@@ -464,7 +466,7 @@ def bench_march_grad(args):
 	import numpy as np
 	import torch
 
-	from vgr import ext, grid, render, scenes
+	from vgr import _lib, ext, grid, render, scenes
 	from vgr.model import VoronoiGaussField
 	dev = torch.device('cuda:0')
 	sc = scenes.make_scene(5, scale=args.scale, log=log)
@@ -493,12 +495,15 @@ def bench_march_grad(args):
 		fwd_args = (g.points, g.offsets, g.adj, model.raw, dA, cA, sh, sc.sh_deg, *rays, dt, n_bg, 1e-4, 1e-4)
 		gen = torch.Generator(device=dev).manual_seed(0)
 		g_rgb, g_T = torch.randn(B, 3, device=dev, generator=gen), torch.randn(B, device=dev, generator=gen)
+		# one workspace for both passes, as ext.march's autograd uses it: the backward reuses the forward's blocks
+		work = torch.empty(int(_lib.load().vgr_march_backward_work_size(sc.n_sites, sc.sh_deg)), dtype=torch.uint8,
+						   device=dev)
 		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 262144 rays
-			f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args, lanes=lanes), args.steps, args.warmup,
-									  stream)
+			f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args, lanes=lanes, work=work), args.steps,
+									  args.warmup, stream)
 			rgb, T, _, stats = out
-			b_ms, grads, _ = time_steps(lambda: me.march_backward(*fwd_args, rgb, T, g_rgb, g_T, lanes=lanes),
-										args.steps, args.warmup, stream)
+			b_ms, grads, _ = time_steps(lambda: me.march_backward(*fwd_args, rgb, T, g_rgb, g_T, lanes=lanes,
+																  work=work), args.steps, args.warmup, stream)
 			st = stats.double()
 			fwd_bytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
 							  st[:, 1].sum() * E * (24 + SHB))

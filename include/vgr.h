@@ -143,7 +143,8 @@ int vgr_march_forward_lanes(const float* points, int64_t n_sites, const int32_t*
  *   -> g_raw f32 (N), g_dA f32 (N, 6), g_cA f32 (N, 6), g_sh f32 (N, 16, 3), overwritten (zeroed first). The sums
  *   use fp32 atomics, so they agree with a sequential sum to rounding, not bitwise.
  * lanes_per_ray: the forward's layout (0, 1 or 16 as for vgr_march_forward_lanes); it must be the one that produced
- * rgb and T, since the backward replays that forward's sums.
+ * rgb and T, since the backward replays that forward's sums. blocks_ready: nonzero when `work` is the forward's
+ * workspace, still holding the site blocks it packed from these same field arrays (the pack is then skipped).
  * work: device scratch of vgr_march_backward_work_size(N, sh_deg) bytes (the forward's site blocks plus a 256-byte
  * gradient block per site), 256-byte aligned.
  */
@@ -154,7 +155,7 @@ int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offs
                        const float* mid_t, const float* far_t, int64_t n_rays, double dt, int64_t n_bg,
                        double t_thresh, double w_thresh, const float* rgb, const float* T, const float* g_rgb,
                        const float* g_T, float* g_raw, float* g_dA, float* g_cA, float* g_sh, int64_t lanes_per_ray,
-                       void* work, int64_t work_bytes, void* stream);
+                       int64_t blocks_ready, void* work, int64_t work_bytes, void* stream);
 
 /*
  * The training renderer: rendering at the ray's crossings of the Voronoi faces with a record of every sample, and
@@ -168,7 +169,8 @@ int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offs
  *   foam_backward takes the forward's rgb, T, rec and stats (records replayed for rays whose samples fit, the others
  *   re-traced with the same arithmetic) and the upstream gradients g_rgb (B, 3), g_T (B) -> g_raw (N), g_dA (N, 6),
  *   g_cA (N, 6), g_sh (N, 16, 3), overwritten. Sums use fp32 atomics (equal to a sequential sum to rounding).
- * work: vgr_foam_work_size(N, sh_deg) bytes, 256-byte aligned, for both.
+ * work: vgr_foam_work_size(N, sh_deg) bytes, 256-byte aligned, for both; blocks_ready as for vgr_march_backward
+ * (nonzero: `work` is the forward's, whose site blocks are reused).
  */
 int64_t vgr_foam_work_size(int64_t n_sites, int64_t sh_deg);
 int vgr_foam_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj, int64_t n_adj,
@@ -181,8 +183,8 @@ int vgr_foam_backward(const float* points, int64_t n_sites, const int32_t* offse
                       int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
                       const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, const float* rgb,
                       const float* T, const float* g_rgb, const float* g_T, const float* rec, int64_t record_cap,
-                      const int32_t* stats, float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work,
-                      int64_t work_bytes, void* stream);
+                      const int32_t* stats, float* g_raw, float* g_dA, float* g_cA, float* g_sh,
+                      int64_t blocks_ready, void* work, int64_t work_bytes, void* stream);
 
 /*
  * Nearest site of every sorted ray sample o + z d by a greedy walk (strict <). Replaces walk() of

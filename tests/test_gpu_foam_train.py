@@ -148,3 +148,31 @@ def test_render_rays_foam_training_step(gpu):
 	assert not model.sh_rest.grad.any()  # degree 0: no gradient beyond the DC term
 	np.testing.assert_allclose(model.bg_logit.grad.cpu().numpy(), 0.25 * (fw['T'][:, None] * W).sum(0), rtol=1e-4,
 							   atol=1e-4)
+
+
+def test_backward_reuses_the_forward_blocks(gpu):
+	"""A backward handed the forward's workspace (site blocks already packed: what the autograd Functions do) equals
+	one that packs them again, for the training renderer and the march."""
+	from vgr import _lib
+	f, dA, cA, field, rays, rt = case(gpu)
+	rng = np.random.default_rng(15)
+	g_rgb = T(rng.normal(size=(len(rays[0]), 3)).astype(np.float32), gpu)
+	g_T = T(rng.normal(size=len(rays[0])).astype(np.float32), gpu)
+	fx = ext.foam_extension()
+	work = torch.empty(int(_lib.load().vgr_foam_work_size(f.n, 3)), dtype=torch.uint8, device=gpu)
+	rgb, Tt, _, stats, rec = fx.foam_forward(*field, 3, *rt, 1e-4, 1e-4, 64, work=work)
+	a = fx.foam_backward(*field, 3, *rt, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T, rec, stats, work=work)
+	b = fx.foam_backward(*field, 3, *rt, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T, rec, stats)
+	for x, y in zip(a, b):
+		assert rel(x.cpu().numpy(), y.cpu().numpy()) < 1e-6
+	mx = ext.march_extension()
+	mid = (rt[3] + rt[4]) * 0.5
+	mrays = rt[:4] + [mid, rt[4]]
+	work = torch.empty(int(_lib.load().vgr_march_backward_work_size(f.n, 3)), dtype=torch.uint8, device=gpu)
+	rgb, Tt, _, _ = mx.march_forward(*field, 3, *mrays, 0.05, 8, 1e-4, 1e-4, work=work)
+	a = mx.march_backward(*field, 3, *mrays, 0.05, 8, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T, work=work)
+	b = mx.march_backward(*field, 3, *mrays, 0.05, 8, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T)
+	for x, y in zip(a, b):
+		assert rel(x.cpu().numpy(), y.cpu().numpy()) < 1e-6
+	with pytest.raises(RuntimeError, match='too small'):
+		mx.march_backward(*field, 3, *mrays, 0.05, 8, 1e-4, 1e-4, rgb, Tt, g_rgb, g_T, work=work[:100])

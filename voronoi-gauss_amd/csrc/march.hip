@@ -1560,8 +1560,8 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
                                   const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays,
                                   double dt, int64_t n_bg, double t_thresh, double w_thresh, const float* rgb,
                                   const float* T, const float* g_rgb, const float* g_T, float* g_raw, float* g_dA,
-                                  float* g_cA, float* g_sh, int64_t lanes_per_ray, void* work, int64_t work_bytes,
-                                  void* stream) {
+                                  float* g_cA, float* g_sh, int64_t lanes_per_ray, int64_t blocks_ready, void* work,
+                                  int64_t work_bytes, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 1 || lanes_per_ray == kGroup,
                 "march_backward: lanes_per_ray must be 0 (by batch size), 1 or 16 (got %lld)",
@@ -1591,8 +1591,9 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
     VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "march_backward: work must be 256-byte aligned");
     float4* rec = static_cast<float4*>(work);
     const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
-                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
+    if (!blocks_ready)
+        hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
+                           reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
     const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
@@ -1675,8 +1676,8 @@ extern "C" int vgr_foam_backward(const float* points, int64_t n_sites, const int
                                  const float* near_t, const float* far_t, int64_t n_rays, double t_thresh,
                                  double w_thresh, const float* rgb, const float* T, const float* g_rgb,
                                  const float* g_T, const float* rec, int64_t record_cap, const int32_t* stats,
-                                 float* g_raw, float* g_dA, float* g_cA, float* g_sh, void* work, int64_t work_bytes,
-                                 void* stream) {
+                                 float* g_raw, float* g_dA, float* g_cA, float* g_sh, int64_t blocks_ready,
+                                 void* work, int64_t work_bytes, void* stream) {
     using namespace vgr;
     VGR_REQUIRE(n_sites > 0 && n_sites <= INT_MAX, "foam_backward: n_sites must be in [1, 2^31)");
     VGR_REQUIRE(g_raw && g_dA && g_cA && g_sh, "foam_backward: null gradient pointer");
@@ -1696,8 +1697,9 @@ extern "C" int vgr_foam_backward(const float* points, int64_t n_sites, const int
     VGR_REQUIRE(record_cap == 0 || (rec && stats), "foam_backward: records need rec and the forward's stats");
     float4* recb = static_cast<float4*>(work);
     const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
-                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
+    if (!blocks_ready)
+        hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
+                           reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
     float* block = reinterpret_cast<float*>(static_cast<char*>(work) + vgr_march_work_size(n_sites, sh_deg));
     hipLaunchKernelGGL(zero_kernel, dim3(kZeroBlocks), dim3(256), 0, s, block, kGradBlock * n_sites);
     const MarchField F{recb, offsets, adj, int(sh_deg), int(n_sites)};

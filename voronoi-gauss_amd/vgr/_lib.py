@@ -30,11 +30,11 @@ SIGNATURES = {
 	'vgr_foam_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64, _P, _P,
 						 _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_foam_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64, _P, _P,
-						  _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _P],
+						  _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_forward_lanes': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64,
 								_I64, _F64, _F64, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
 	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
-						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
+						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
 	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
 								_P],
 	'vgr_walk': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
@@ -61,7 +61,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 _lib = None
 
 

@@ -187,9 +187,10 @@ def _field_work(points, m, records):
 class _MarchExtension:
 	@staticmethod
 	def march_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
-					  t_thresh, w_thresh, trace_cap=0, lanes=0):
+					  t_thresh, w_thresh, trace_cap=0, lanes=0, work=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0).
-		lanes: 1 ray per lane (1), 16 lanes per ray (16) or by batch size (0)."""
+		lanes: 1 ray per lane (1), 16 lanes per ray (16) or by batch size (0). work: optional uint8 device workspace
+		(at least vgr_march_work_size bytes); a training step passes the backward's, which then reuses its blocks."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -209,7 +210,10 @@ class _MarchExtension:
 		if B == 0:
 			return out
 		work_bytes = int(_lib.load().vgr_march_work_size(points.numel() // 3, int(sh_deg)))
-		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
+		if work is None:
+			work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
+		else:
+			work_bytes = work.numel()
 		with torch.cuda.device(dev):
 			call('vgr_march_forward_lanes', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(dA), ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid),
@@ -219,9 +223,10 @@ class _MarchExtension:
 
 	@staticmethod
 	def march_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
-					   t_thresh, w_thresh, rgb, T, g_rgb, g_T, lanes=0):
+					   t_thresh, w_thresh, rgb, T, g_rgb, g_T, lanes=0, work=None):
 		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (march.cu:405-428). lanes: the layout of the
-		forward that produced rgb and T."""
+		forward that produced rgb and T. work: the forward's workspace (vgr_march_backward_work_size bytes), whose
+		site blocks are reused, or None to pack them again."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -238,12 +243,17 @@ class _MarchExtension:
 		g = [torch.empty(n, device=dev), torch.empty(n, 6, device=dev), torch.empty(n, 6, device=dev),
 			 torch.empty(n, 16, 3, device=dev)]
 		work_bytes = int(_lib.load().vgr_march_backward_work_size(n, int(sh_deg)))
-		work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
+		ready = work is not None
+		if ready:
+			_require(work.dtype == torch.uint8 and work.numel() >= work_bytes, 'work is too small')
+			work_bytes = work.numel()
+		else:
+			work = torch.empty(max(work_bytes, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
 			call('vgr_march_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
 				 ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid), ptr(far), B,
 				 float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(g_rgb), ptr(g_T),
-				 *[ptr(x) for x in g], int(lanes), ptr(work), work_bytes, stream_of(dev))
+				 *[ptr(x) for x in g], int(lanes), int(ready), ptr(work), work_bytes, stream_of(dev))
 		return g
 
 
@@ -407,7 +417,7 @@ class _FoamExtension:
 
 	@staticmethod
 	def foam_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-					 record_cap):
+					 record_cap, work=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32, rec (B or 0, record_cap, 8)]
 		(foam.cu:471-497)."""
 		_FoamExtension._check_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
@@ -422,7 +432,11 @@ class _FoamExtension:
 		if B == 0:
 			return [rgb, T, depth, stats, rec]
 		wb = int(_lib.load().vgr_foam_work_size(n, int(sh_deg)))
-		work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
+		if work is None:
+			work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
+		else:
+			_require(work.dtype == torch.uint8 and work.numel() >= wb, 'work is too small')
+			wb = work.numel()
 		with torch.cuda.device(dev):
 			call('vgr_foam_forward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA), ptr(cA),
 				 ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B, float(t_thresh),
@@ -432,9 +446,10 @@ class _FoamExtension:
 
 	@staticmethod
 	def foam_backward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-					  rgb, T, g_rgb, g_T, rec, stats):
+					  rgb, T, g_rgb, g_T, rec, stats, work=None):
 		"""-> [g_raw (N,), g_dA (N, 6), g_cA (N, 6), g_sh (N, 16, 3)] (foam.cu:499-531). rec (B, K, 8) with the
-		forward's stats, or an empty rec to re-trace every ray."""
+		forward's stats, or an empty rec to re-trace every ray. work: the forward's workspace, whose site blocks are
+		reused, or None to pack them again."""
 		_FoamExtension._check_args(points, offsets, adj, raw, dA, cA, sh, o, d, start, near, far)
 		for t, nm in ((rgb, 'rgb'), (T, 'T'), (g_rgb, 'g_rgb'), (g_T, 'g_T'), (rec, 'rec')):
 			_check(t, nm, torch.float32)
@@ -449,12 +464,17 @@ class _FoamExtension:
 		g = [torch.empty(n, device=dev), torch.empty(n, 6, device=dev), torch.empty(n, 6, device=dev),
 			 torch.empty(n, 16, 3, device=dev)]
 		wb = int(_lib.load().vgr_foam_work_size(n, int(sh_deg)))
-		work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
+		ready = work is not None
+		if ready:
+			_require(work.dtype == torch.uint8 and work.numel() >= wb, 'work is too small')
+			wb = work.numel()
+		else:
+			work = torch.empty(max(wb, 1), dtype=torch.uint8, device=dev)
 		with torch.cuda.device(dev):
 			call('vgr_foam_backward', ptr(points), n, ptr(offsets), ptr(adj), adj.numel(), ptr(raw), ptr(dA),
 				 ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B, float(t_thresh),
 				 float(w_thresh), ptr(rgb), ptr(T), ptr(g_rgb), ptr(g_T), ptr(rec) if replay else None, K,
-				 ptr(stats) if replay else None, *[ptr(x) for x in g], ptr(work), wb, stream_of(dev))
+				 ptr(stats) if replay else None, *[ptr(x) for x in g], int(ready), ptr(work), wb, stream_of(dev))
 		return g
 
 
@@ -603,10 +623,14 @@ class _March(torch.autograd.Function):
 
 	@staticmethod
 	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg):
+		# one workspace for both passes: the backward reuses the site blocks the forward packed
+		n = graph.points.numel() // 3
+		work = torch.empty(max(int(_lib.load().vgr_march_backward_work_size(n, cfg[0])), 1), dtype=torch.uint8,
+						   device=raw.device)
 		rgb, T, depth, stats = march_extension().march_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
-															   sh, cfg[0], *rays, *cfg[1:])
+															   sh, cfg[0], *rays, *cfg[1:], work=work)
 		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, *rays)
-		ctx.graph, ctx.cfg = graph, cfg
+		ctx.graph, ctx.cfg, ctx.work = graph, cfg, work
 		ctx.mark_non_differentiable(depth, stats)
 		return rgb, T, depth, stats
 
@@ -617,7 +641,8 @@ class _March(torch.autograd.Function):
 		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
 		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
 		grads = march_extension().march_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays,
-												 *cfg[1:], rgb, T, g_rgb, g_T)
+												 *cfg[1:], rgb, T, g_rgb, g_T, work=ctx.work)
+		ctx.work = None
 		return (*grads, None, None, None)
 
 
@@ -639,10 +664,14 @@ class _Foam(torch.autograd.Function):
 
 	@staticmethod
 	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg, record_cap):
+		# one workspace for both passes: the backward reuses the site blocks the forward packed
+		n = graph.points.numel() // 3
+		work = torch.empty(max(int(_lib.load().vgr_foam_work_size(n, cfg[0])), 1), dtype=torch.uint8,
+						   device=raw.device)
 		rgb, T, depth, stats, rec = foam_extension().foam_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
-																  sh, cfg[0], *rays, *cfg[1:], record_cap)
+																  sh, cfg[0], *rays, *cfg[1:], record_cap, work=work)
 		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, rec, stats, *rays)
-		ctx.graph, ctx.cfg = graph, cfg
+		ctx.graph, ctx.cfg, ctx.work = graph, cfg, work
 		ctx.mark_non_differentiable(depth, stats)
 		return rgb, T, depth, stats
 
@@ -653,7 +682,8 @@ class _Foam(torch.autograd.Function):
 		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
 		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
 		grads = foam_extension().foam_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays, *cfg[1:],
-											   rgb, T, g_rgb, g_T, rec, stats)
+											   rgb, T, g_rgb, g_T, rec, stats, work=ctx.work)
+		ctx.work = None
 		return (*grads, None, None, None, None)
 
 
