@@ -435,7 +435,7 @@ def bench_foam_grad(args):
 		oracle.foam_backward(*host, sc.sh_deg, *[r[sel] for r in rays], *[u[sel] for u in up])
 		secs = time.perf_counter() - t1
 		cpu = {'value': round(len(sel) / secs / 1e3, 4), 'unit': 'Krays/s (backward only)', 'cores': 1,
-			   'kind': 'port', 'sample': f'every {B // len(sel)}th ray of the batch ({len(sel)} rays), C oracle '
+			   'kind': 'port', 'sample': f'{sample_words(B, len(sel))}, C oracle '
 										 f'foam_backward (re-tracing), one thread'}
 	big = legs[16 * args.batch]
 	emit('Mrays/s through foam forward + backward (training batch)', mrays_per_s(args.batch, ms), 'Mrays/s', args, ms,
@@ -536,7 +536,7 @@ def bench_march_grad(args):
 		oracle.march_backward(*host, sc.sh_deg, *[r[sel] for r in rays], dt, n_bg, *[u[sel] for u in up])
 		secs = time.perf_counter() - t1
 		cpu = {'value': round(len(sel) / secs / 1e3, 4), 'unit': 'Krays/s (backward only)', 'cores': 1,
-			   'kind': 'port', 'sample': f'every {B // len(sel)}th ray of the batch ({len(sel)} rays), C oracle '
+			   'kind': 'port', 'sample': f'{sample_words(B, len(sel))}, C oracle '
 										 f'march_backward, one thread'}
 	layouts = {f'{B} rays, {lanes} lanes/ray': {'forward_ms': round(v['fwd'], 3), 'backward_ms': round(v['bwd'], 3),
 												'Mrays_per_s': round(mrays_per_s(B, v['fwd'] + v['bwd']), 3)}
@@ -551,6 +551,11 @@ def bench_march_grad(args):
 		  'frac': round(achieved / 8000.0, 4), 'traffic': None,
 		  'kernel': 'march_group_backward_kernel' if auto == 16 else 'march_backward_kernel',
 		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
+
+
+def sample_words(B, n):
+	"""How a CPU-baseline subset of n of the batch's B rays was drawn."""
+	return f'all {B} rays of the batch' if n == B else f'every {B // n}th ray of the batch ({n} rays)'
 
 
 def mrays_per_s(B, ms):
