@@ -861,7 +861,106 @@ __device__ __forceinline__ void group_colour(const MarchField& F, GroupCell& Cc,
     for (int ch = 0; ch < 3; ++ch) C[ch] = row_sum(cs[ch]) * inv_a;
 }
 
-// Per ray: the sample loop of march_ray with one sample per round.
+// kGroupBatch consecutive samples per round: one round at the walk's site evaluates, for each of them, the walk's
+// argmin, the density and the colour minimum, exactly as a round of its own would (same neighbours per lane in the
+// same order, same butterflies), and resolves the leading samples at which the site wins (march_ray's batching in
+// the group layout). The coloured samples among them are blended by one colour round. Same bits as one sample per
+// round; up to kGroupBatch times fewer rounds.
+constexpr int kGroupBatch = 4;
+
+struct GroupRoundN {
+    float sigma[kGroupBatch], mmin[kGroupBatch];
+    int k[kGroupBatch];
+};
+
+template <int BLK>
+__device__ __forceinline__ void group_round_n(const MarchField& F, int i, const float (&o)[3], const float (&d)[3],
+                                              const float (&t)[kGroupBatch], int g, GroupRoundN& Q) {
+    const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
+    float bd[kGroupBatch], s[kGroupBatch], mm[kGroupBatch];
+    int bk[kGroupBatch];
+#pragma unroll
+    for (int j = 0; j < kGroupBatch; ++j) bd[j] = kInf, s[j] = 0.f, mm[j] = kInf, bk[j] = INT_MAX;
+    for (int e = g; e < n; e += kGroup) {
+        const int k = neighbor(F, i, e0, e);
+        const SiteRec rc = site_rec<BLK>(F, k);
+#pragma unroll
+        for (int j = 0; j < kGroupBatch; ++j) {
+            float x[3], v[3];
+            point_at(o, d, t[j], x);
+            offset_to(rc.q0, x, v);
+            const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+            if (dk < bd[j] || (dk == bd[j] && k < bk[j])) bd[j] = dk, bk[j] = k;
+            s[j] += fexp(rc.q0.w - 0.5f * density_m(rc, v));
+            mm[j] = fminf(mm[j], color_m(rc.q2, rc.q3, v));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kGroupBatch; ++j) {
+        row_argmin(bd[j], bk[j]);
+        Q.k[j] = bk[j], Q.sigma[j] = row_sum(s[j]), Q.mmin[j] = row_min(mm[j]);
+    }
+}
+
+// group_colour for the coloured samples of one round (bit j of `mask`), each with its own weights and sums.
+template <int NV>
+__device__ __forceinline__ void group_colour_n(const MarchField& F, GroupCell& Cc, const float (&o)[3],
+                                               const float (&d)[3], const float (&t)[kGroupBatch],
+                                               const float (&mmin)[kGroupBatch], unsigned mask, const float (&b)[16],
+                                               int nb, int g, float (&C)[kGroupBatch][3], float (&inv)[kGroupBatch]) {
+    cell_colours<NV>(F, b, nb, Cc);
+    float A[kGroupBatch], cs[kGroupBatch][3];
+#pragma unroll
+    for (int j = 0; j < kGroupBatch; ++j) A[j] = cs[j][0] = cs[j][1] = cs[j][2] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) {
+        if (Cc.k[s] >= 0) {
+            const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(Cc.k[s]);
+            const float4 p = r[0], c0 = r[2], c1 = r[3];
+#pragma unroll
+            for (int j = 0; j < kGroupBatch; ++j) {
+                if ((mask >> j) & 1u) {
+                    float x[3], v[3];
+                    point_at(o, d, t[j], x);
+                    offset_to(p, x, v);
+                    const float a = fexp(-0.5f * (color_m(c0, c1, v) - mmin[j]));
+                    A[j] += a;
+#pragma unroll
+                    for (int ch = 0; ch < 3; ++ch) cs[j][ch] += a * fmaxf(Cc.c[s][ch], 0.f);
+                }
+            }
+        }
+    }
+    for (int e = g + kGroup * kSlots; e < Cc.n; e += kGroup) {
+        const int k = neighbor(F, Cc.cell, Cc.e0, e);
+        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
+        const float4 p = r[0], c0 = r[2], c1 = r[3];
+        float c[3];
+        sh_eval_n<NV>(r + kRec, b, nb, c);
+#pragma unroll
+        for (int j = 0; j < kGroupBatch; ++j) {
+            if ((mask >> j) & 1u) {
+                float x[3], v[3];
+                point_at(o, d, t[j], x);
+                offset_to(p, x, v);
+                const float a = fexp(-0.5f * (color_m(c0, c1, v) - mmin[j]));
+                A[j] += a;
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) cs[j][ch] += a * fmaxf(c[ch], 0.f);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kGroupBatch; ++j) {
+        if ((mask >> j) & 1u) {
+            inv[j] = 1.f / row_sum(A[j]);
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) C[j][ch] = row_sum(cs[j][ch]) * inv[j];
+        }
+    }
+}
+
+// Per ray: the sample loop of march_ray, kGroupBatch samples per round.
 template <int NV, bool TRACE>
 __device__ void march_ray_group(const MarchField& F, const MarchParams& M, const MarchRays& R, const MarchOut& O,
                                 int64_t r, int cur, int g) {
@@ -877,33 +976,49 @@ __device__ void march_ray_group(const MarchField& F, const MarchParams& M, const
     float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
     GroupCell Cc;
     Cc.cell = -1;
-    for (int k = 0; k < n_total;) {
-        float t, delta, x[3];
-        sample_at(near, mid, far, n_in, M, k, t, delta);
-        point_at(o, d, t, x);
-        GroupRound Q;
-        group_round<block_vec4(NV)>(F, cur, x, g, Q);
-        if (Q.k != cur && moves < kWalkCap) {
-            cur = Q.k, ++walk_steps, ++moves;
-            continue;
-        }
-        moves = 0;
-        if (TRACE && g == 0 && n_samples < O.trace_cap) O.trace[r * O.trace_cap + n_samples] = cur;
-        const float alpha = 1.f - fexp(-Q.sigma * delta);
-        const float w = T * alpha;
-        ++n_samples;
-        if (w > M.w_thresh) {
-            if (Cc.cell != cur) enter_cell(F, cur, g, Cc);
-            float inv_a, C[3];
-            group_colour<NV>(F, Cc, x, b, nb, Q.mmin, g, inv_a, C);
+    bool live = true;
+    for (int k = 0; live && k < n_total;) {
+        float t[kGroupBatch], delta[kGroupBatch], w[kGroupBatch];
 #pragma unroll
-            for (int a = 0; a < 3; ++a) acc[a] += w * C[a];
-            dep += w * t;
-            ++n_color;
+        for (int j = 0; j < kGroupBatch; ++j) sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), t[j], delta[j]);
+        GroupRoundN Q;
+        group_round_n<block_vec4(NV)>(F, cur, o, d, t, g, Q);
+        int nres = 0, next = cur;
+        unsigned coloured = 0u;
+        bool run = true;
+#pragma unroll
+        for (int j = 0; j < kGroupBatch; ++j) {
+            w[j] = 0.f;
+            if (!run || k + j >= n_total) {
+                run = false;
+            } else if (Q.k[j] == cur || (j == 0 && moves >= kWalkCap)) {
+                if (TRACE && g == 0 && n_samples < O.trace_cap) O.trace[r * O.trace_cap + n_samples] = cur;
+                const float alpha = 1.f - fexp(-Q.sigma[j] * delta[j]);
+                w[j] = T * alpha;
+                ++n_samples, ++nres;
+                if (w[j] > M.w_thresh) coloured |= 1u << j, ++n_color;
+                T *= 1.f - alpha;
+                if (T < M.t_thresh) run = live = false;
+            } else {
+                next = Q.k[j], run = false;
+            }
         }
-        T *= 1.f - alpha;
-        ++k;
-        if (T < M.t_thresh) break;
+        if (coloured) {
+            if (Cc.cell != cur) enter_cell(F, cur, g, Cc);
+            float C[kGroupBatch][3], inv[kGroupBatch];
+            group_colour_n<NV>(F, Cc, o, d, t, Q.mmin, coloured, b, nb, g, C, inv);
+#pragma unroll
+            for (int j = 0; j < kGroupBatch; ++j) {
+                if ((coloured >> j) & 1u) {
+#pragma unroll
+                    for (int a = 0; a < 3; ++a) acc[a] += w[j] * C[j][a];
+                    dep += w[j] * t[j];
+                }
+            }
+        }
+        k += nres;
+        moves = nres > 0 ? 0 : moves;
+        if (live && k < n_total && next != cur) cur = next, ++walk_steps, ++moves;
     }
     if (g == 0) {
 #pragma unroll
