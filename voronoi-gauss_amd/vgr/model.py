@@ -1,7 +1,8 @@
 """Per-site parameters of the field (model.py:19-59 of the reference): density Gaussian (rho = exp(raw), scale,
 rotation), colour Gaussian (scale, rotation), SH colour (sh_dc + sh_rest) and a background logit.
 
-The forward path only reads them; there is no optimiser here (training is out of scope)."""
+They are nn.Parameters: the renderers' autograd Functions (ext.foam, ext.march, ext.density, ext.color, ext.conic)
+give them gradients; the optimiser and the training loop are the reference's own train.py."""
 
 import math
 
