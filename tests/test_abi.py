@@ -82,5 +82,16 @@ def test_library_reports_argument_errors_without_a_gpu():
 	assert lib.vgr_march_forward(*margs) == 1 and b'256-byte aligned' in lib.vgr_last_error()
 	margs[16] = 0  # no rays: nothing to check or launch
 	assert lib.vgr_march_forward(*margs) == 0
+	# the layout argument and the training entries' workspaces are checked before any launch
+	margs[16] = 8
+	largs = margs[:27] + [8] + margs[27:]
+	assert lib.vgr_march_forward_lanes(*largs) == 1 and b'lanes_per_ray' in lib.vgr_last_error()
+	assert lib.vgr_march_backward_work_size(1000, 3) == 256000 + 256000
+	assert lib.vgr_foam_work_size(1000, 1) == 128000 + 256000
+	fargs = [fake, 1000, fake, fake, 15000, fake, fake, fake, fake, 3, fake, fake, fake, fake, fake, 8, 1e-4, 1e-4,
+			 fake, fake, fake, fake, None, 0, fake, 1000, None]
+	assert lib.vgr_foam_forward(*fargs) == 1 and b'work must hold 512000 bytes' in lib.vgr_last_error()
+	fargs[9] = 5
+	assert lib.vgr_foam_forward(*fargs) == 1 and b'sh_deg' in lib.vgr_last_error()
 	# field records: 64 bytes per site
 	assert lib.vgr_field_work_size(0) == 0 and lib.vgr_field_work_size(1000) == 64000
