@@ -498,7 +498,7 @@ def bench_march_grad(args):
 		# one workspace for both passes, as ext.march's autograd uses it: the backward reuses the forward's blocks
 		work = torch.empty(int(_lib.load().vgr_march_backward_work_size(sc.n_sites, sc.sh_deg)), dtype=torch.uint8,
 						   device=dev)
-		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 262144 rays
+		for lanes in (1, 16):  # both ray layouts; the library's default picks 16 below 524288 rays
 			f_ms, out, _ = time_steps(lambda: me.march_forward(*fwd_args, lanes=lanes, work=work), args.steps,
 									  args.warmup, stream)
 			rgb, T, _, stats = out
@@ -515,7 +515,7 @@ def bench_march_grad(args):
 			log(f'{B} rays, {lanes} lane(s) per ray: forward {L["fwd"]:.3f} ms, backward {L["bwd"]:.3f} ms '
 				f'({bwd_bytes / L["bwd"] / 1e6:.0f} GB/s algorithmic); samples/ray {L["samples"]:.1f}, coloured '
 				f'{L["coloured"]:.1f}')
-	auto = 16 if args.batch < 262144 else 1
+	auto = 16 if args.batch < 524288 else 1
 	L = legs[args.batch, auto]
 	ms = L['fwd'] + L['bwd']
 	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
@@ -702,7 +702,7 @@ def bench_march(args):
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
-		  'lanes_per_ray': lanes or (16 if B < 262144 else 1)},
+		  'lanes_per_ray': lanes or (16 if B < 524288 else 1)},
 		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
 		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
 		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)

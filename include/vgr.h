@@ -124,7 +124,7 @@ int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offse
 /*
  * vgr_march_forward with the ray layout chosen by the caller: lanes_per_ray 1 (one ray per lane), 16 (a group of
  * 16 lanes per ray, one neighbour per lane: for small batches, whose launches are bound by each ray's serial chain
- * of loads) or 0 (by batch size: 16 below 262144 rays, else 1, which is what vgr_march_forward does). The layouts
+ * of loads) or 0 (by batch size: 16 below 524288 rays, else 1, which is what vgr_march_forward does). The layouts
  * visit the same sites; their sums differ in the order of addition. Same reference function as vgr_march_forward.
  */
 int vgr_march_forward_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,

@@ -1596,11 +1596,12 @@ extern "C" int64_t vgr_march_backward_work_size(int64_t n_sites, int64_t sh_deg)
 namespace vgr {
 namespace {
 // Launches of fewer rays take the 16-lane group layout, for forward and backward alike (the backward replays the
-// forward's sums). Config 5, ms forward / backward, one ray per lane against 16 lanes per ray: 4,096 rays 34 / 86
-// against 6 / 17; 65,536 rays 42 / 192 against 24 / 72; 262,144 rays 77 / 407 against 83 / 252; the whole 16.7M-ray
-// batch forward 3,350 against 5,264. Below about one wave per CU in one ray per lane a launch is bound by its rays'
-// serial chains of loads, which the group shortens; its backward adds gradient rows shared by the wave.
-constexpr int64_t kGroupRays = 262144;
+// forward's sums). Config 5, ms forward / backward, one ray per lane against 16 lanes per ray: 4,096 rays 34 / 85
+// against 5 / 16; 65,536 rays 41 / 189 against 19 / 70; 262,144 rays 75 / 408 against 67 / 251; 1,048,576 rays
+// 236 / 1531 against 255 / 974. A training step (forward + backward) is faster in the group layout at every size
+// measured, a forward alone from about half a million rays in one ray per lane (the whole 16.7M-ray inference
+// batch: 3,350 against 5,264 ms), hence the switch at 2^19 rays.
+constexpr int64_t kGroupRays = 524288;
 
 int64_t march_lanes(int64_t lanes, int64_t n_rays) { return lanes != 0 ? lanes : n_rays < kGroupRays ? kGroup : 1; }
 }  // namespace
