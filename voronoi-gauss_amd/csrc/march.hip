@@ -68,21 +68,40 @@ __device__ __forceinline__ int neighbor(const MarchField& F, int i, int e0, int 
     return e == 0 ? i : F.adj[e0 + e - 1];
 }
 
+// One lane per float4 of the blocks (the record's four, then the SH row's nv), so that a wave's stores are
+// consecutive 16-byte pieces of consecutive blocks.
 __global__ void __launch_bounds__(256)
     march_pack_kernel(const float* __restrict__ points, const float* __restrict__ raw, const float* __restrict__ dA,
-                      const float* __restrict__ cA, const float4* __restrict__ sh, int nv, int blk, int n,
+                      const float* __restrict__ cA, const float4* __restrict__ sh, int nv, int blk, int64_t n,
                       float4* __restrict__ rec) {
-    const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (k >= n) return;
-    const float* p = points + 3 * k;
+    const int per = kRec + nv;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n * per) return;
+    const int64_t k = i / per;
+    const int q = static_cast<int>(i - k * per);
     const float* a = dA + 6 * k;
     const float* c = cA + 6 * k;
-    float4* r = rec + blk * k;
-    r[0] = make_float4(p[0], p[1], p[2], fminf(raw[k], 30.f));
-    r[1] = make_float4(a[0], a[1], a[2], a[3]);
-    r[2] = make_float4(a[4], a[5], c[0], c[1]);
-    r[3] = make_float4(c[2], c[3], c[4], c[5]);
-    for (int q = 0; q < nv; ++q) r[kRec + q] = sh[12 * k + q];
+    float4 v;
+    if (q == 0) {
+        const float* p = points + 3 * k;
+        v = make_float4(p[0], p[1], p[2], fminf(raw[k], 30.f));
+    } else if (q == 1) {
+        v = make_float4(a[0], a[1], a[2], a[3]);
+    } else if (q == 2) {
+        v = make_float4(a[4], a[5], c[0], c[1]);
+    } else if (q == 3) {
+        v = make_float4(c[2], c[3], c[4], c[5]);
+    } else {
+        v = sh[12 * k + (q - kRec)];
+    }
+    rec[blk * k + q] = v;
+}
+
+void launch_pack(const float* points, const float* raw, const float* dA, const float* cA, const float* sh, int64_t n,
+                 int64_t sh_deg, float4* rec, hipStream_t s) {
+    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
+    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n * (kRec + nv), 256)), dim3(256), 0, s, points, raw, dA, cA,
+                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), n, rec);
 }
 
 struct SiteRec {
@@ -1634,9 +1653,7 @@ extern "C" int vgr_march_forward_lanes(const float* points, int64_t n_sites, con
     VGR_REQUIRE(work && work_bytes >= need, "march_forward: work must hold %lld bytes", static_cast<long long>(need));
     VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "march_forward: work must be 256-byte aligned");
     float4* rec = static_cast<float4*>(work);
-    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, as_stream(stream), points, raw,
-                       dA, cA, reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
+    launch_pack(points, raw, dA, cA, sh, n_sites, sh_deg, rec, as_stream(stream));
     const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
@@ -1706,10 +1723,7 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
     VGR_REQUIRE(work && work_bytes >= need, "march_backward: work must hold %lld bytes", static_cast<long long>(need));
     VGR_REQUIRE(reinterpret_cast<uintptr_t>(work) % 256 == 0, "march_backward: work must be 256-byte aligned");
     float4* rec = static_cast<float4*>(work);
-    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    if (!blocks_ready)
-        hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
-                           reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), rec);
+    if (!blocks_ready) launch_pack(points, raw, dA, cA, sh, n_sites, sh_deg, rec, s);
     const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
     const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
@@ -1774,9 +1788,7 @@ extern "C" int vgr_foam_forward(const float* points, int64_t n_sites, const int3
     VGR_REQUIRE(record_cap == 0 || rec, "foam_forward: record_cap > 0 needs rec");
     const hipStream_t s = as_stream(stream);
     float4* recb = static_cast<float4*>(work);
-    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
-                       reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
+    launch_pack(points, raw, dA, cA, sh, n_sites, sh_deg, recb, s);
     const MarchField F{recb, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{1.f, 0, float(t_thresh), float(w_thresh)};
     const TrainRays R{o, d, start, near_t, far_t, n_rays};
@@ -1812,10 +1824,7 @@ extern "C" int vgr_foam_backward(const float* points, int64_t n_sites, const int
     VGR_REQUIRE(rgb && T && g_rgb && g_T, "foam_backward: null forward output or upstream gradient pointer");
     VGR_REQUIRE(record_cap == 0 || (rec && stats), "foam_backward: records need rec and the forward's stats");
     float4* recb = static_cast<float4*>(work);
-    const int nv = sh_vec4_f32(static_cast<int>(sh_deg));
-    if (!blocks_ready)
-        hipLaunchKernelGGL(march_pack_kernel, dim3(grid_for(n_sites, 256)), dim3(256), 0, s, points, raw, dA, cA,
-                           reinterpret_cast<const float4*>(sh), nv, block_vec4(nv), int(n_sites), recb);
+    if (!blocks_ready) launch_pack(points, raw, dA, cA, sh, n_sites, sh_deg, recb, s);
     float* block = reinterpret_cast<float*>(static_cast<char*>(work) + vgr_march_work_size(n_sites, sh_deg));
     hipLaunchKernelGGL(zero_kernel, dim3(kZeroBlocks), dim3(256), 0, s, block, kGradBlock * n_sites);
     const MarchField F{recb, offsets, adj, int(sh_deg), int(n_sites)};
