@@ -430,24 +430,24 @@ struct MarchGradOut {
     float* __restrict__ block;  // (N, 64)
 };
 
-// Copies the gradient blocks to g_raw (N), g_dA (N, 6), g_cA (N, 6) and g_sh (N, 16, 3): one lane per output float.
+// Copies the gradient blocks to g_raw (N), g_dA (N, 6), g_cA (N, 6) and g_sh (N, 16, 3): one lane per block float
+// (contiguous reads; the stores of a block's density-conic, colour-conic and SH floats are contiguous too).
 __global__ void __launch_bounds__(256)
     grad_unpack_kernel(const float* __restrict__ block, int64_t n, float* __restrict__ g_raw,
                        float* __restrict__ g_dA, float* __restrict__ g_cA, float* __restrict__ g_sh) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= 61 * n) return;
-    if (i < n) {
-        g_raw[i] = block[kGradBlock * i];
-    } else if (i < 7 * n) {
-        const int64_t j = i - n;
-        g_dA[j] = block[kGradBlock * (j / 6) + 1 + j % 6];
-    } else if (i < 13 * n) {
-        const int64_t j = i - 7 * n;
-        g_cA[j] = block[kGradBlock * (j / 6) + 7 + j % 6];
-    } else {
-        const int64_t j = i - 13 * n;
-        g_sh[j] = block[kGradBlock * (j / 48) + kGradSh + j % 48];
-    }
+    if (i >= kGradBlock * n) return;
+    const int64_t k = i / kGradBlock;
+    const int t = static_cast<int>(i - k * kGradBlock);
+    const float v = block[i];
+    if (t == 0)
+        g_raw[k] = v;
+    else if (t < 7)
+        g_dA[6 * k + t - 1] = v;
+    else if (t < 13)
+        g_cA[6 * k + t - 7] = v;
+    else if (t >= kGradSh)
+        g_sh[48 * k + t - kGradSh] = v;
 }
 
 constexpr float kMinColourWeight = 1e-7f;
@@ -999,7 +999,8 @@ __device__ void march_ray_group(const MarchField& F, const MarchParams& M, const
     for (int k = 0; live && k < n_total;) {
         float t[kGroupBatch], delta[kGroupBatch], w[kGroupBatch];
 #pragma unroll
-        for (int j = 0; j < kGroupBatch; ++j) sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), t[j], delta[j]);
+        for (int j = 0; j < kGroupBatch; ++j)
+            sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), t[j], delta[j]);
         GroupRoundN Q;
         group_round_n<block_vec4(NV)>(F, cur, o, d, t, g, Q);
         int nres = 0, next = cur;
@@ -1743,8 +1744,8 @@ extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const in
     else
         hipLaunchKernelGGL(march_backward_kernel<false>, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0, s, F, M, R,
                            GI, G);
-    hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(61 * n_sites, 256)), dim3(256), 0, s, block, n_sites, g_raw,
-                       g_dA, g_cA, g_sh);
+    hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(kGradBlock * n_sites, 256)), dim3(256), 0, s, block, n_sites,
+                       g_raw, g_dA, g_cA, g_sh);
     return launch_status("march_backward_kernel");
 }
 
@@ -1834,7 +1835,7 @@ extern "C" int vgr_foam_backward(const float* points, int64_t n_sites, const int
     const MarchGradOut G{block};
     hipLaunchKernelGGL(train_backward_kernel, dim3(grid_for(n_rays * kGroup, kBlock)), dim3(kBlock), 0, s, F, M, R,
                        GI, G, record_cap > 0 ? rec : nullptr, int(record_cap), stats);
-    hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(61 * n_sites, 256)), dim3(256), 0, s, block, n_sites, g_raw,
-                       g_dA, g_cA, g_sh);
+    hipLaunchKernelGGL(grad_unpack_kernel, dim3(grid_for(kGradBlock * n_sites, 256)), dim3(256), 0, s, block, n_sites,
+                       g_raw, g_dA, g_cA, g_sh);
     return launch_status("train_backward_kernel");
 }
