@@ -34,7 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, 'voronoi-gauss_amd'))
 
 METRIC = 'Mrays/s and FPS @1080p (2M sites) on 1 MI355X; achieved HBM GB/s vs peak'
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'foam_infer_config3_pmc.md')
+PROFILES = os.path.join(ROOT, 'profiles')
 
 
 def log(*a):
@@ -52,17 +52,78 @@ def copy_probe(dev):
 	log('copy probe: 1 GiB read + 1 GiB written')
 
 
-def measured_traffic(workload):
-	"""DRAM bytes per launch of this workload from the committed rocprofv3 PMC summary (a line
-	'traffic_bytes_per_launch: <bytes> workload: <key>'), or None when no summary matches."""
+def source_hash(*names):
+	"""16 hex digits of SHA-256 over the named kernel sources, the two headers every kernel includes and the hipcc
+	flags: it names the build a DRAM-traffic profile was measured on."""
+	import hashlib
+
+	from vgr import build
+	h = hashlib.sha256()
+	for n in sorted(set(names) | {'vgr_device.h', 'vgr_abi.h'}):
+		h.update(n.encode())
+		with open(os.path.join(build.CSRC, n), 'rb') as f:
+			h.update(f.read())
+	h.update(' '.join(build.HIPCC_FLAGS).encode())
+	return h.hexdigest()[:16]
+
+
+def measured_traffic(workload, src):
+	"""DRAM bytes per launch of this workload from a committed rocprofv3 PMC summary under profiles/ (a line
+	'traffic_bytes_per_launch: <bytes> workload: <key> source: <hash>'), only when it was measured on this build
+	(same source hash) -> (bytes or None, where it came from or why it is missing)."""
+	import glob
 	import re
-	if not os.path.exists(TRAFFIC_FILE):
-		return None
-	for line in open(TRAFFIC_FILE):
-		m = re.match(r'\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)\s+workload:\s*(\S+)', line)
-		if m and m.group(2) == workload:
-			return float(m.group(1))
-	return None
+	stale = None
+	for path in sorted(glob.glob(os.path.join(PROFILES, '*.md'))):
+		for line in open(path):
+			m = re.match(r'\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)\s+workload:\s*(\S+)\s+source:\s*(\S+)', line)
+			if m and m.group(2) == workload:
+				if m.group(3) == src:
+					return float(m.group(1)), f'{os.path.relpath(path, ROOT)} (rocprofv3 FETCH_SIZE + WRITE_SIZE, source {src})'
+				stale = f'{os.path.relpath(path, ROOT)} was measured on source {m.group(3)}, not this build ({src})'
+	return None, stale or f'no PMC profile of workload {workload} under profiles/'
+
+
+def hbm_roofline(ms, workload, src, model_bytes, model, kernel):
+	"""The HBM roofline of a launch of `ms` milliseconds: achieved = DRAM bytes per launch (rocprofv3, this build)
+	/ the launch time, frac = achieved / 8 TB/s; both null when no profile of this build exists. The byte model of
+	the workload (model_bytes, described by `model`) is reported beside it under its own keys and never feeds them."""
+	traffic, source = measured_traffic(workload, src)
+	r = {'bound': 'hbm', 'kernel': kernel, 'achieved': None, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': None,
+		 'traffic': traffic, 'traffic_source': source, 'source_hash': src}
+	if traffic is not None:
+		gbs = traffic / (ms * 1e-3) / 1e9
+		r['achieved'], r['frac'] = round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
+	r['model'] = model
+	r['model_bytes_per_launch'] = model_bytes
+	r['model_GBps'] = round(model_bytes / (ms * 1e-3) / 1e9, 1)
+	if traffic is not None:
+		r['model_over_dram'] = round(model_bytes / traffic, 3)
+	return r
+
+
+def cpu_model():
+	"""The host CPU's model name and logical core count (lscpu's 'Model name', from /proc/cpuinfo)."""
+	name = None
+	try:
+		for line in open('/proc/cpuinfo'):
+			if line.startswith('model name'):
+				name = line.split(':', 1)[1].strip()
+				break
+	except OSError:
+		pass
+	return f'{name or "unknown CPU"} ({os.cpu_count()} logical cores visible)'
+
+
+def timed_cpu(run, reps=3):
+	"""1 untimed warmup run, then the median of `reps` timed runs of run() -> (median seconds, last result)."""
+	import numpy as np
+	run()
+	times, res = [], None
+	for _ in range(reps):
+		res = run()
+		times.append(res['seconds'])
+	return float(np.median(times)), res
 
 
 def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray):
@@ -248,10 +309,18 @@ def bench_foam(args):
 		quality = None
 		log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
 	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
-	achieved = abytes / (ms * 1e-3) / 1e9
 	st = stats.double()
 	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}'
-	traffic = None if fast else measured_traffic(key)
+	if fast:
+		key += f'-sh{"16" if args.sh_half else "32"}-ec{args.eps_color:g}-ed{args.eps_density:g}'
+	src = source_hash('foam_infer.hip')
+	log(f'kernel source hash (foam_infer.hip): {src}; workload key {key}')
+	roofline = hbm_roofline(ms, key, src, abytes,
+							'cache-oblivious gather bytes from the per-ray counters: 56 B per ray + 24 B per sample + '
+							'84 B per neighbourhood edge + SH bytes per distinct blended site (counts every L1/L2/LDS '
+							'hit as a fetch, so it can exceed the HBM peak)',
+							'foam_infer_kernel' if (args.lanes_per_ray or (4 if args.colors == 'exact' else 1)) == 1
+							else 'foam_group_kernel')
 
 	cpu = None
 	if args.cpu_seconds > 0 and args.colors != 'baked':
@@ -281,20 +350,16 @@ def bench_foam(args):
 			'distinct_sites_traced_rays': u_rays or None, 'quality': quality,
 			'mean_T': round(float(T.double().mean()), 4),
 		},
-		'roofline': {
-			'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-			'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic,
-			'algorithmic_bytes_per_launch': abytes,
-			'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1),
-		},
+		'roofline': roofline,
 		'cpu_baseline': cpu,
 	}
 	print(json.dumps(res), flush=True)
 
 
 def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu, color_cut=math.inf):
-	"""The CPU oracle (C/OpenMP, thread per ray) on every k-th ray of the same workload, k chosen so the timed
-	loop takes about `seconds` on all host cores; also the max |rgb - GPU| on that subset."""
+	"""The CPU oracle (C/OpenMP, thread per ray, all host cores) on every k-th ray of the same workload, k chosen so
+	that one timed pass takes about seconds / 4: 1 untimed warmup pass, then the median of 3 timed passes (the
+	parallel loop only, steady_clock inside the oracle). Also the max |rgb - GPU| and |T - GPU| on that subset."""
 	import numpy as np
 
 	sys.path.insert(0, os.path.join(ROOT, 'oracle'))
@@ -305,16 +370,18 @@ def cpu_baseline(pack, sc, o, d, start, near, far, mode, seconds, rgb_gpu, T_gpu
 	probe = np.arange(0, B, max(1, B // 20000), dtype=np.int64)
 	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_cut=color_cut, color_mode=mode, rays=probe)
 	rate = len(probe) / max(r['seconds'], 1e-6)
-	k = max(1, int(B / (rate * seconds)))
+	k = max(1, int(B / (rate * seconds / 4)))
 	sel = np.arange(0, B, k, dtype=np.int64)
-	r = oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_cut=color_cut, color_mode=mode, rays=sel)
+	secs, r = timed_cpu(lambda: oracle.foam_infer(pk, sc.sh_deg, o, d, start, near, far, color_cut=color_cut,
+												  color_mode=mode, rays=sel))
 	err = float(np.abs(r['rgb'] - rgb_gpu[sel]).max())
 	errT = float(np.abs(r['T'] - T_gpu[sel]).max())
-	log(f'cpu oracle: {len(sel)} rays (every {k}th) in {r["seconds"]:.2f} s on {threads} threads; '
-		f'max |rgb - gpu| {err:.2e}, max |T - gpu| {errT:.2e}')
-	return {'value': round(len(sel) / r['seconds'] / 1e6, 4), 'unit': 'Mrays/s', 'cores': threads, 'kind': 'port',
+	log(f'cpu oracle: {len(sel)} rays (every {k}th), median of 3 passes {secs:.2f} s on {threads} threads '
+		f'({cpu_model()}); max |rgb - gpu| {err:.2e}, max |T - gpu| {errT:.2e}')
+	return {'value': round(len(sel) / secs / 1e6, 4), 'unit': 'Mrays/s', 'cores': threads, 'kind': 'port',
+			'cpu': cpu_model(), 'timing': '1 warmup pass, then the median of 3 timed passes of the parallel loop',
 			'sample': f'every {k}th ray of the same {B}-ray workload ({len(sel)} rays), same pack and colour mode, '
-					  f'C/OpenMP thread per ray',
+					  f'C/OpenMP thread per ray, schedule(dynamic)',
 			'parity_max_abs_rgb': err, 'parity_max_abs_T': errT}
 
 
@@ -417,7 +484,6 @@ def bench_foam_grad(args):
 			f'coloured segments {L["coloured"]:.1f}, rays within the records {100 * L["fits"]:.1f} %')
 	L = legs[args.batch]
 	ms = L['fwd'] + L['bwd']
-	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
 		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
@@ -446,9 +512,9 @@ def bench_foam_grad(args):
 		  'rays_within_records': round(L['fits'], 4),
 		  f'rays_{16 * args.batch}': {'forward_ms': round(big['fwd'], 3), 'backward_ms': round(big['bwd'], 3),
 									  'Mrays_per_s': round(mrays_per_s(16 * args.batch, big['fwd'] + big['bwd']), 3)}},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
-		  'frac': round(achieved / 8000.0, 4), 'traffic': None, 'kernel': 'train_backward_kernel',
-		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
+		 hbm_roofline(L['bwd'], f'config3-foam-grad-b{args.batch}', source_hash('march.hip'), L['bytes'],
+					  'cache-oblivious bytes of the backward launch (records, site blocks and gradient rows per sample)',
+					  'train_backward_kernel'), cpu)
 
 
 def bench_march_grad(args):
@@ -518,7 +584,6 @@ def bench_march_grad(args):
 	auto = 16 if args.batch < 524288 else 1
 	L = legs[args.batch, auto]
 	ms = L['fwd'] + L['bwd']
-	achieved = L['bytes'] / (L['bwd'] * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
 		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
@@ -547,10 +612,9 @@ def bench_march_grad(args):
 		  'rays_per_step': args.batch, 'lanes_per_ray': auto, 'forward_ms': round(L['fwd'], 4),
 		  'backward_ms': round(L['bwd'], 4), 'samples_per_ray': round(L['samples'], 2),
 		  'coloured_per_ray': round(L['coloured'], 2), 'layouts': layouts},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': 8000.0, 'unit': 'GB/s',
-		  'frac': round(achieved / 8000.0, 4), 'traffic': None,
-		  'kernel': 'march_group_backward_kernel' if auto == 16 else 'march_backward_kernel',
-		  'algorithmic_bytes_per_launch': L['bytes']}, cpu)
+		 hbm_roofline(L['bwd'], f'config5-march-grad-b{args.batch}', source_hash('march.hip'), L['bytes'],
+					  'cache-oblivious bytes of the backward launch (site blocks per neighbour visit, gradient rows)',
+					  'march_group_backward_kernel' if auto == 16 else 'march_backward_kernel'), cpu)
 
 
 def sample_words(B, n):
@@ -585,7 +649,6 @@ def bench_locate(args):
 		f'mean {ms:.3f} ms, wall {wall:.3f} ms/step')
 	# compulsory bytes of one launch: query in (12 B), site out (4 B); the grid and points read once
 	abytes = 16.0 * B + 16.0 * N + 4.0 * N + 4.0 * (n_cells + 1)
-	achieved = abytes / (ms * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
 		from scipy.spatial import cKDTree
@@ -613,8 +676,9 @@ def bench_locate(args):
 		 {'workload': f'config 5 start cells: nearest of {N} sites (seeded uniform draw) for each of {B} ray '
 					  f'origins', 'sites': N, 'queries': B, 'grid_res': g.res,
 		  'grid_build_ms': round(float(np.mean(build_ms)), 3)},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+		 hbm_roofline(ms, f'config5-locate', source_hash('grid.hip'), abytes,
+					  'compulsory bytes: each query point, site and grid word read once, each answer written once',
+					  'grid_nearest'), cpu)
 
 
 def bench_march(args):
@@ -659,7 +723,6 @@ def bench_march(args):
 	# per sample: walk steps (8 + 16 E) each, density (8 + E (16 + 28)), colour when active E (24 + SHB); rays 56 B
 	abytes = float(56 * B + st[:, 2].sum() * (8 + 16 * E) + st[:, 0].sum() * (8 + E * 44) +
 				   st[:, 1].sum() * E * (24 + SHB))
-	achieved = abytes / (ms * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
 		sys.path.insert(0, os.path.join(ROOT, 'oracle'))
@@ -694,7 +757,6 @@ def bench_march(args):
 							  'sample sets; the thresholds-off figures compare the arithmetic'}
 	if args.copy_probe:
 		copy_probe(dev)
-	traffic = measured_traffic(f'config5-scale{args.scale}-march')
 	emit('Mrays/s march_forward (config 5: 4M sites, 16.7M incoherent rays) on 1 MI355X', B / ms / 1e3, 'Mrays/s',
 		 args, ms,
 		 {'workload': f'config 5 march: {sc.n_sites} sites, {B} rays, dt 1/512 inside the unit ball + {n_bg} '
@@ -703,9 +765,9 @@ def bench_march(args):
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
 		  'lanes_per_ray': lanes or (16 if B < 524288 else 1)},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic, 'algorithmic_bytes_per_launch': abytes,
-		  'dram_GBps': None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)}, cpu)
+		 hbm_roofline(ms, f'config5-scale{args.scale}-march', source_hash('march.hip'), abytes,
+					  'cache-oblivious bytes from the per-ray counters: per walk step 8 + 16 E, per sample 8 + 44 E, '
+					  'per coloured sample E (24 + SH bytes)', 'march_forward_kernel'), cpu)
 
 
 def bench_traverse(args):
@@ -770,7 +832,6 @@ def bench_traverse(args):
 	E = 1.0 + len(sc.adj) / sc.n_sites
 	# per visited cell: the cell position (16 B) and offsets (8 B), then per face the edge record (16 B) and nbr (4 B)
 	abytes = float(56 * B + st[:, 0].sum() * (24 + 20 * E))
-	achieved = abytes / (ms_face * 1e-3) / 1e9
 	emit(f'Mrays/s cell traversal, {args.lanes} lanes per ray (config {args.config}: {sc.n_sites} sites, 4 x 1080p)',
 		 B / ms_face / 1e3, 'Mrays/s', args, ms_face,
 		 {'workload': f'config {args.config}: foam_infer stage 0 (walk + exit faces) over {B} camera rays',
@@ -778,8 +839,9 @@ def bench_traverse(args):
 		  'thread_per_ray_ms': round(ms_lane, 4),
 		  'lane_per_face_ms': {str(g): round(ms, 4) for g, ms in group_ms.items()},
 		  'identical_stats': same, 'cells_per_ray': round(float(st[:, 0].mean()), 2)},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+		 hbm_roofline(ms_face, f'config{args.config}-traverse-l{args.lanes}', source_hash('foam_faces.hip'), abytes,
+					  'cache-oblivious bytes: 56 B per ray, per visited cell 24 B + 20 B per face',
+					  'foam_faces_kernel'), cpu)
 
 
 def bench_pack(args):
@@ -810,7 +872,6 @@ def bench_pack(args):
 	# edge 16 per self-first entry) written once
 	shb = 192
 	abytes = float(N * (12 + 4 + 4 + 24 + 32 + shb) + 4 * M + N * (16 + 4 + 80 + shb + 20) + (M + N) * 20)
-	achieved = abytes / (ms * 1e-3) / 1e9
 	cpu = None
 	if args.cpu_seconds > 0:
 		# the host pack takes the device conics (conic_forward is its own row), then builds everything else
@@ -839,8 +900,9 @@ def bench_pack(args):
 		 'Msites/s', args, ms,
 		 {'workload': f'config {args.config} pack: {N} sites, {M} adjacency entries, SH degree {sc.sh_deg}, Z-order '
 					  f'renumbering', 'sites': N, 'adjacency': M, 'peak_extra_GiB': round(peak, 2)},
-		 {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-		  'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None, 'algorithmic_bytes_per_launch': abytes}, cpu)
+		 hbm_roofline(ms, f'config{args.config}-pack', source_hash('pack.hip'), abytes,
+					  'compulsory bytes: every input read once and every packed record written once',
+					  'pack_foam (all passes)'), cpu)
 
 
 def bench_field(args):
@@ -950,9 +1012,9 @@ def bench_field(args):
 					  f'weight > 1e-4; conic over {sc.n_sites} sites', 'samples': m, 'active_samples': ma,
 		  'ms': {k: round(v, 3) for k, v in ms.items()}, 'GBps': {k: round(v, 1) for k, v in gbs.items()},
 		  'walk_steps_per_sample': round(float(steps.double().sum()) / m, 3)},
-		 {'bound': 'hbm', 'kernel': f'{top}_forward' if top != 'walk' else 'walk', 'achieved': round(gbs[top], 1),
-		  'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs[top] / HBM_PEAK_GBS, 4), 'traffic': None,
-		  'algorithmic_bytes_per_launch': nb[top]}, cpu)
+		 hbm_roofline(ms[top], f'config3-field-{top}', source_hash('field.hip'), nb[top],
+					  'cache-oblivious bytes per sample and neighbour (site record, adjacency, SH when coloured)',
+					  f'{top}_forward' if top != 'walk' else 'walk'), cpu)
 
 
 def bench_grad(args):
@@ -1065,9 +1127,9 @@ def bench_grad(args):
 		  'active_samples': ma, 'ms': {k: round(v, 3) for k, v in ms.items()},
 		  'GBps': {k: round(v, 1) for k, v in gbs.items()},
 		  'grad_norms': {'raw': float(dgrad[0].norm()), 'sh': float(cgrad[2].norm())}},
-		 {'bound': 'hbm', 'kernel': f'{top}_backward', 'achieved': round(gbs[top], 1), 'peak': HBM_PEAK_GBS,
-		  'unit': 'GB/s', 'frac': round(gbs[top] / HBM_PEAK_GBS, 4), 'traffic': None,
-		  'algorithmic_bytes_per_launch': nb[top]}, cpu)
+		 hbm_roofline(ms[top], f'config3-grad-{top}', source_hash('field_grad.hip'), nb[top],
+					  'cache-oblivious bytes per sample and neighbour (site parameters, gradient scatter)',
+					  f'{top}_backward'), cpu)
 
 
 if __name__ == '__main__':

@@ -90,10 +90,15 @@ def trace(pts, offsets, adj, o, d, near, far, cell):
 	return np.array(t), np.array(cells)
 
 
-def foam_dense(pts, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, t, cells):
+def foam_dense(pts, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, t, cells, color_cut=np.inf, fused=False, r2=None,
+			   baked=None):
 	"""Foreground rgb (3,) and final T of one ray with samples t (S,) evaluated in `cells` (S,), thresholds off:
 	sigma = sum over {c} U adj(c) of exp(raw) exp(-m_dA / 2), colour = softmax(-m_cA / 2) blend of
-	max(SH + 1/2, 0), trapezoid rule."""
+	max(SH + 1/2, 0), trapezoid rule. The approximate modes of foam_infer.cu:229-249,266-276:
+	  r2 (N,): a density term counts only where |x - p_j|^2 <= r2_j (eps_density);
+	  color_cut: a colour term counts only where m <= m_min + color_cut, m_min the sample's smallest m (exact mode),
+	    or, fused, where m <= (the smallest m of the neighbours before it in {c} U adj(c) order) + color_cut;
+	  baked (N, 3): site colours used instead of the SH colours."""
 	pts = np.asarray(pts, np.float64)
 	X = o[None] + t[:, None] * d[None]
 	b = sh_basis(d[None], sh_deg)[0]
@@ -102,11 +107,21 @@ def foam_dense(pts, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, t, cells):
 	for s, (x, c) in enumerate(zip(X, cells)):
 		nb = neighborhood(offsets, adj, c)
 		v = x[None] - pts[nb]
-		sig[s] = (np.exp(raw[nb]) * np.exp(-0.5 * maha6(dA[nb], v))).sum()
-		lw = -0.5 * maha6(cA[nb], v)
+		dens = np.exp(raw[nb]) * np.exp(-0.5 * maha6(dA[nb], v))
+		if r2 is not None:
+			dens = np.where((v * v).sum(1) <= r2[nb], dens, 0.0)
+		sig[s] = dens.sum()
+		m = maha6(cA[nb], v)
+		if fused:
+			run = np.minimum.accumulate(np.concatenate([[np.inf], m[:-1]]))
+			keep = m <= run + color_cut
+		else:
+			keep = m <= m.min() + color_cut
+		lw = np.where(keep, -0.5 * m, -np.inf)
 		a = np.exp(lw - lw.max())
 		a /= a.sum()
-		ck = np.maximum(np.einsum('j,njc->nc', b, sh[nb]) + 0.5, 0)
+		ck = np.asarray(baked, np.float64)[nb] if baked is not None else \
+			np.maximum(np.einsum('j,njc->nc', b, sh[nb]) + 0.5, 0)
 		C[s] = a @ ck
 	delta = t[1:] - t[:-1]
 	alpha = 1 - np.exp(-0.5 * (sig[1:] + sig[:-1]) * delta)

@@ -1,0 +1,237 @@
+"""GPU parity at the stated sizes of the benchmark configurations 2-5: each scene is built at its full site count
+(500K, 2M, 8M and 4M sites, Delaunay by Qhull in background processes, see conftest.py), the GPU renders the
+whole workload (every ray of every camera, or config 5's 16,777,216-ray batch), and the C oracle re-renders a
+deterministic subset of those rays (every k-th ray) on the host:
+
+- default thresholds, fused and exact colours: rgb and T within 1e-4 on every checked ray, PSNR >= 60 dB over
+  them, per-ray statistics equal on >= 99.5 % of them, and every ray whose statistics differ is a ray that ended
+  (or coloured a segment) at a transmittance or weight within ulps of its threshold: its cell sequence is
+  identical with the thresholds off;
+- cell sequences: bit-exact with the thresholds off (stage 0, the geometric traversal, and stage 2), identical
+  common prefixes with them on;
+- the safety caps (8192 cells per ray, 4096 walk steps) are counted over the whole workload and printed.
+
+Config 5 also runs march_forward on all 16,777,216 rays in the default layout (one ray per lane at this size),
+checked on every k-th ray (values within 1e-4, walked sites bit-exact), and march_backward on 524,288 of its rays
+(the smallest batch that takes the one-ray-per-lane layout), with upstream gradients on every 256th ray only, so
+that the oracle's backward over those rays gives the same gradients (relative error 2e-5).
+
+VGR_STATED_CONFIGS=2,3 (say) restricts the configurations."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import stated_configs, wait_for_geometry
+from helpers import ray_bounds_np
+from test_gpu_foam import compare, psnr, ref_foam
+from test_oracle_grad import rel
+from vgr import ext, render, scenes
+from vgr.model import VoronoiGaussField
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(1200)]
+
+TOL = 1e-4
+MAX_CELLS, WALK_CAP = 8192, 4096
+SUBSET = {2: 16384, 3: 16384, 4: 8192, 5: 8192}
+
+
+class Stated:
+	"""One full-size configuration: the scene, its GPU pack (Z-order renumbered, as the bench packs it), the host
+	copy of the pack for the oracle, and the rays of all cameras (8x8 tiles) or of config 5's batch."""
+
+	def __init__(self, config, dev):
+		wait_for_geometry(config)
+		self.config = config
+		self.sc = sc = scenes.make_scene(config, log=None)
+		assert sc.n_sites >= 0.999 * scenes.SITE_COUNTS[config]
+		self.model = VoronoiGaussField.from_scene(sc, dev)
+		self.pack = render.pack_foam(self.model, reorder=True)
+		self.pk = {k: self.pack[k].cpu().numpy() for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh', 'orig')}
+		o, d, start, _ = sc.camera_rays(tile=8)
+		self.o, self.d = o, d
+		self.start_orig = start
+		self.start = self.pk['orig'].argsort()[start].astype(np.int32)  # old -> new numbering
+		self.near, self.mid, self.far = ray_bounds_np(o, d, 0.02, sc.far_radius)
+		self.dev = dev
+		self.B = len(o)
+
+	def t(self, a):
+		return torch.as_tensor(np.ascontiguousarray(a), device=self.dev)
+
+	def subset(self, n):
+		k = max(1, self.B // n)
+		return np.arange(k // 2, self.B, k, dtype=np.int64)[:n]
+
+	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0):
+		"""GPU foam_infer over the selected rays (all by default) -> dict of numpy arrays."""
+		pick = (lambda a: a) if sel is None else (lambda a: a[sel])
+		p = self.pack
+		empty = torch.empty(0, dtype=torch.int32, device=self.dev)
+		out = ext.foam_infer_extension().foam_infer(
+			p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], self.sc.sh_deg, self.t(pick(self.o)),
+			self.t(pick(self.d)), self.t(pick(self.start)), self.t(pick(self.near)), self.t(pick(self.far)),
+			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap)
+		torch.cuda.synchronize()
+		res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
+		res.setdefault('trace', None)
+		return res
+
+	def oracle(self, sel, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0):
+		return ref_foam(self.pk, self.sc.sh_deg, self.o, self.d, self.start, self.near, self.far, t_thresh, w_thresh,
+						color_mode=mode, stage=stage, rays=sel, trace_cap=trace_cap)
+
+
+@pytest.fixture(scope='module', params=stated_configs())
+def stated(request, gpu):
+	s = Stated(request.param, gpu)
+	yield s
+	del s
+	torch.cuda.empty_cache()
+
+
+def rows(res, sel):
+	return {k: (None if v is None else v[sel]) for k, v in res.items()}
+
+
+def test_foam_full_workload(stated):
+	"""The whole workload in fused colours (the bench's mode) on the GPU; the oracle on every k-th ray."""
+	s = stated
+	full = s.foam()
+	sel = s.subset(SUBSET[s.config])
+	r = s.oracle(sel)
+	g = rows(full, sel)
+	same = (g['stats'] == r['stats']).all(1)
+	err = np.abs(g['rgb'] - r['rgb']).max()
+	print(f'\n[stated sizes] config {s.config}: {s.sc.n_sites} sites, {s.B} rays; oracle on {len(sel)} rays: max '
+		  f'|rgb| {err:.2e}, max |T| {np.abs(g["T"] - r["T"]).max():.2e}, stats equal on {same.mean():.5f}, PSNR '
+		  f'{psnr(g["rgb"], r["rgb"]):.1f} dB; mean samples {full["stats"][:, 0].mean():.1f}', flush=True)
+	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
+	assert psnr(g['rgb'], r['rgb']) >= 60.0
+	# rays whose statistics differ: same cells with the thresholds off (the difference is where a threshold fell)
+	diff = sel[~same]
+	if len(diff):
+		go = s.foam(diff, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
+		ro = s.oracle(diff, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
+		np.testing.assert_array_equal(go['trace'], ro['trace'])
+	caps = {'rays hitting the 8192-cell cap': int((full['stats'][:, 0] > MAX_CELLS).sum()),
+			'rays hitting the 4096-step walk cap': int((full['stats'][:, 2] >= WALK_CAP).sum())}
+	print(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}', flush=True)
+
+
+def test_foam_traces_and_exact_colours(stated):
+	"""On the subset: the fused render's cell sequences (common prefixes with the thresholds on), exact (two-pass)
+	colours within 1e-4, and with the thresholds off the stage-0 traversal and the full stage-2 render bit-exact
+	in their cells with every statistic equal."""
+	s = stated
+	sel = s.subset(SUBSET[s.config])
+	g = s.foam(sel, trace_cap=2048)
+	r = s.oracle(sel, trace_cap=2048)
+	compare(g, r, exact_trace=False, stats_frac=0.995, t_max=s.sc.far_radius)
+	g = s.foam(sel, mode=0)
+	r = s.oracle(sel, mode=0)
+	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
+	assert psnr(g['rgb'], r['rgb']) >= 60.0
+	few = sel[::8]
+	for stage in (0, 2):
+		g = s.foam(few, stage=stage, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
+		r = s.oracle(few, stage=stage, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
+		compare(g, r, t_max=s.sc.far_radius)
+		np.testing.assert_array_equal(g['stats'], r['stats'])
+	print(f'\n[stated sizes] config {s.config}: thresholds off, {len(few)} rays, mean {g["stats"][:, 0].mean():.0f} '
+		  f'cells per ray, cell sequences bit-exact', flush=True)
+
+
+@pytest.fixture(scope='module')
+def config5_field(gpu):
+	if 5 not in stated_configs():
+		pytest.skip('config 5 not selected (VGR_STATED_CONFIGS)')
+	wait_for_geometry(5)
+	sc = scenes.make_scene(5, log=None)
+	model = VoronoiGaussField.from_scene(sc, gpu)
+	dt, n_bg = 1 / 512, 64
+	dA = ext.conic(model.d_log_scale, model.d_quat, 0.5 * dt)
+	cA = ext.conic(model.c_log_scale, model.c_quat, 0.5 * dt)
+	o, d, start, _ = sc.camera_rays()
+	near, mid, far = ray_bounds_np(o, d, 0.02, sc.far_radius)
+	host = dict(points=sc.points, offsets=sc.offsets, adj=sc.adj, raw=sc.raw, dA=dA.cpu().numpy(),
+				cA=cA.cpu().numpy(), sh=sc.sh)
+	yield sc, model, dA, cA, (o, d, start, near, mid, far), host, dt, n_bg
+	torch.cuda.empty_cache()
+
+
+def march_gpu(dev, model, dA, cA, sh_deg, rays, dt, n_bg, t_thresh=1e-4, w_thresh=1e-4, trace_cap=0, lanes=0):
+	g = model.graph
+	rt = [torch.as_tensor(np.ascontiguousarray(a), device=dev) for a in rays]
+	out = ext.march_extension().march_forward(g.points, g.offsets, g.adj, model.raw.detach(), dA, cA,
+											  model.sh().detach().contiguous(), sh_deg, *rt, dt, n_bg, t_thresh,
+											  w_thresh, trace_cap=trace_cap, lanes=lanes)
+	torch.cuda.synchronize()
+	return [x.cpu().numpy() for x in out]
+
+
+def test_march_config5_full_batch(gpu, config5_field):
+	"""march_forward over all 16,777,216 rays of config 5 in the default layout, the oracle on every k-th ray; the
+	walked sites of that subset bit-exact (one ray per lane forced, the layout of the full batch)."""
+	sc, model, dA, cA, rays, host, dt, n_bg = config5_field
+	B = len(rays[0])
+	rgb, T, depth, stats = march_gpu(gpu, model, dA, cA, sc.sh_deg, rays, dt, n_bg)
+	sel = np.arange(511, B, B // 16384, dtype=np.int64)
+	r = oracle.march_forward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
+							 host['sh'], sc.sh_deg, *rays, dt, n_bg, rays=sel)
+	same = (stats[sel] == r['stats']).all(1)
+	print(f'\n[stated sizes] config 5 march: {B} rays, oracle on {len(sel)}: max |rgb| '
+		  f'{np.abs(rgb[sel] - r["rgb"]).max():.2e}, max |T| {np.abs(T[sel] - r["T"]).max():.2e}, stats equal on '
+		  f'{same.mean():.5f}, mean samples {stats[:, 0].mean():.1f}', flush=True)
+	np.testing.assert_allclose(rgb[sel], r['rgb'], atol=TOL, rtol=0)
+	np.testing.assert_allclose(T[sel], r['T'], atol=TOL, rtol=0)
+	assert same.mean() >= 0.995
+	few = sel[::16]
+	sub = tuple(a[few] for a in rays)
+	_, _, _, st, tr = march_gpu(gpu, model, dA, cA, sc.sh_deg, sub, dt, n_bg, trace_cap=2048, lanes=1)
+	rt = oracle.march_forward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
+							  host['sh'], sc.sh_deg, *sub, dt, n_bg, trace_cap=2048)
+	n = np.minimum(np.minimum(st[:, 0], rt['stats'][:, 0]), 2048)
+	for i in range(len(few)):
+		np.testing.assert_array_equal(tr[i, :n[i]], rt['trace'][i, :n[i]])
+	# thresholds off: every sample of every ray, sites and counts identical
+	sub = tuple(a[few[:128]] for a in rays)
+	_, _, _, st, tr = march_gpu(gpu, model, dA, cA, sc.sh_deg, sub, dt, n_bg, 0.0, -1.0, trace_cap=4096, lanes=1)
+	rt = oracle.march_forward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
+							  host['sh'], sc.sh_deg, *sub, dt, n_bg, 0.0, -1.0, trace_cap=4096)
+	np.testing.assert_array_equal(st, rt['stats'])
+	np.testing.assert_array_equal(tr, rt['trace'])
+
+
+def test_march_backward_config5_default_layout(gpu, config5_field):
+	"""march_backward over 524,288 rays of config 5 (one ray per lane, the default at this size, forward and
+	backward) with upstream gradients on every 256th ray: against the oracle's backward over those rays."""
+	sc, model, dA, cA, rays, host, dt, n_bg = config5_field
+	B = 524288
+	sub = tuple(np.ascontiguousarray(a[:B]) for a in rays)
+	g = model.graph
+	rt = [torch.as_tensor(a, device=gpu) for a in sub]
+	sh = model.sh().detach().contiguous()
+	fx = ext.march_extension()
+	rgb, T, _, _ = fx.march_forward(g.points, g.offsets, g.adj, model.raw.detach(), dA, cA, sh, sc.sh_deg, *rt, dt,
+									n_bg, 1e-4, 1e-4)
+	rng = np.random.default_rng(11)
+	g_rgb = np.zeros((B, 3), np.float32)
+	g_T = np.zeros(B, np.float32)
+	hot = np.arange(0, B, 256)
+	g_rgb[hot] = rng.normal(size=(len(hot), 3))
+	g_T[hot] = rng.normal(size=len(hot))
+	got = fx.march_backward(g.points, g.offsets, g.adj, model.raw.detach(), dA, cA, sh, sc.sh_deg, *rt, dt, n_bg,
+							1e-4, 1e-4, rgb, T, torch.as_tensor(g_rgb, device=gpu), torch.as_tensor(g_T, device=gpu))
+	torch.cuda.synchronize()
+	ref = oracle.march_backward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
+								host['sh'], sc.sh_deg, *[a[hot] for a in sub], dt, n_bg, rgb.cpu().numpy()[hot],
+								T.cpu().numpy()[hot], g_rgb[hot], g_T[hot])
+	errs = {name: rel(a.cpu().numpy(), r) for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref)}
+	print(f'\n[stated sizes] config 5 march backward, {B} rays, {len(hot)} with gradients: relative errors {errs}',
+		  flush=True)
+	for name, e in errs.items():
+		assert e < 2e-5, name

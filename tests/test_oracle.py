@@ -164,6 +164,94 @@ def test_foam_sh_degree0_colour_closed_form(oracle_lib):
 	np.testing.assert_allclose(out['rgb'], (1 - out['T'])[:, None] * c[None], atol=2e-6)
 
 
+def test_foam_baked_colours_closed_forms(foam_case):
+	"""Baked colours (foam_infer.cu:242-244), pinned without the oracle's SH path: (a) one colour c baked into every
+	site gives rgb = c (1 - T), blends of equal colours; (b) arbitrary per-site colours against foam_dense blending
+	the same colours in float64; (c) colours baked as max(1/2 + 0.28209479 sh0, 0) give what the fused mode
+	computes from degree-0 SH, which depends on no direction."""
+	f, pk0, rays = foam_case
+	o, d, start, near, _, far = rays
+	pk = dict(pk0, attr=pk0['attr'].copy())
+	c = np.array([0.3, 0.8, 0.05], np.float32)
+	pk['attr'][:, 16:19] = c
+	out = oracle.foam_infer(pk, 3, o, d, start, near, far, 0.0, -1.0, color_mode=1, trace_cap=4096)
+	np.testing.assert_allclose(out['rgb'], (1 - out['T'])[:, None] * c[None], atol=2e-6)
+	assert (out['stats'][:, 4] == 0).all()  # no SH evaluation in baked mode
+	colours = np.random.default_rng(9).uniform(0, 1, (f.n, 3)).astype(np.float32)
+	pk['attr'][:, 16:19] = colours
+	out = oracle.foam_infer(pk, 3, o, d, start, near, far, 0.0, -1.0, color_mode=1, trace_cap=4096)
+	dense_check(f, pk, rays, out, baked=colours)
+	g = Field(seed=7, n=250, sh_deg=0)
+	o, d, start, near, _, far = g.rays(B=48, seed=7)
+	pk = g.pack()
+	pk['attr'][:, 16:19] = np.maximum(0.5 + np.float32(0.28209479177387814) * g.sh[:, 0], 0)
+	baked = oracle.foam_infer(pk, 0, o, d, start, near, far, 0.0, -1.0, color_mode=1)
+	fused = oracle.foam_infer(pk, 0, o, d, start, near, far, 0.0, -1.0, color_mode=2, use_cache=False)
+	np.testing.assert_allclose(baked['rgb'], fused['rgb'], atol=2e-6)
+	np.testing.assert_array_equal(baked['T'], fused['T'])
+	np.testing.assert_array_equal(baked['stats'][:, :4], fused['stats'][:, :4])
+
+
+def dense_check(f, pk, rays, out, atol=2e-5, **kw):
+	"""The oracle's rgb and T against foam_dense (float64, same mode options) on every ray whose cells agree with
+	the float64 re-trace (at least 95 % of them)."""
+	o, d, start, near, _, far = rays
+	checked = 0
+	for r in range(len(o)):
+		o64, d64 = o[r].astype(np.float64), d[r].astype(np.float64)
+		t, cells = dense.trace(f.points, f.offsets, f.adj, o64, d64, float(near[r]), float(far[r]),
+							   f.tree.query(o64 + near[r] * d64)[1])
+		n = out['stats'][r, 0]
+		if n != len(cells) or list(out['trace'][r, :n]) != list(cells):
+			continue
+		rgb, T = dense.foam_dense(f.points, f.offsets, f.adj, f.raw.astype(np.float64), pk['dA'].astype(np.float64),
+								  pk['cA'].astype(np.float64), f.sh.astype(np.float64), f.sh_deg, o64, d64, t, cells,
+								  **kw)
+		np.testing.assert_allclose(out['rgb'][r], rgb, atol=atol, rtol=1e-4)
+		np.testing.assert_allclose(out['T'][r], T, atol=2e-6, rtol=1e-4)
+		checked += 1
+	assert checked >= 0.95 * len(o)
+
+
+@pytest.mark.parametrize('mode', [0, 2])
+def test_foam_eps_color_matches_float64_dense(foam_case, mode):
+	"""A finite colour cut (foam_infer.cu:236,240,271,276) against foam_dense applying the same rule in float64:
+	exact mode keeps m <= m_min + cut, fused mode m <= (running minimum in neighbourhood order) + cut. The cut
+	must drop terms (fewer SH evaluations) and change the colours; transmittance and cells stay unchanged."""
+	f, pk, rays = foam_case
+	cut = 2 * np.log(1 / 1e-2)
+	exact = run_foam(f, pk, rays, stage=2, color_mode=mode, use_cache=False)
+	out = run_foam(f, pk, rays, stage=2, color_mode=mode, use_cache=False, color_cut=cut)
+	np.testing.assert_array_equal(out['T'], exact['T'])
+	np.testing.assert_array_equal(out['trace'], exact['trace'])
+	assert out['stats'][:, 4].sum() < 0.8 * exact['stats'][:, 4].sum()
+	assert np.abs(out['rgb'] - exact['rgb']).max() > 1e-4
+	dense_check(f, pk, rays, out, color_cut=cut, fused=mode == 2)
+
+
+def test_foam_eps_density_matches_float64_dense(oracle_lib):
+	"""eps_density (foam_infer.cu:229, render.py:191-197): against foam_dense dropping a term where |x - p_j|^2 >
+	r2_j (the half-precision r2 of the pack); and the bound the rule exists for: a dropped term is
+	rho_j G_j(x) <= exp(raw_j - |v|^2 / (2 s_max^2)) < eps, so T rises by at most a factor exp(eps E_max (far - near))
+	over the exact render's."""
+	f = Field(seed=8, n=300, raw_mu=0.5)
+	rays = f.rays(B=48, seed=8)
+	o, d, start, near, _, far = rays
+	eps = 0.05
+	exact = oracle.foam_infer(f.pack(), 3, o, d, start, near, far, 0.0, -1.0, trace_cap=4096)
+	pk = f.pack(eps_density=eps)
+	out = oracle.foam_infer(pk, 3, o, d, start, near, far, 0.0, -1.0, trace_cap=4096)
+	np.testing.assert_array_equal(out['trace'], exact['trace'])
+	assert out['stats'][:, 3].sum() < 0.9 * exact['stats'][:, 3].sum()  # terms were dropped
+	tol = 1e-6 * (1 + exact['T'])
+	assert (out['T'] >= exact['T'] - tol).all() and (out['T'] > exact['T'] + 1e-6).any()
+	e_max = int(np.diff(pk['offsets']).max())
+	assert (out['T'] <= exact['T'] * np.exp(eps * e_max * (far - near)) + tol).all()
+	r2 = np.empty(f.n)
+	r2[pk['nbr']] = (pk['edge'][:, 3].view(np.uint32) & 0xFFFF).astype(np.uint16).view(np.float16)
+	dense_check(f, pk, rays, out, r2=r2)
+
+
 def test_fp16_sh_oracle_close_to_fp32(foam_case):
 	f, pk, rays = foam_case
 	ph = f.pack(sh_half=True)

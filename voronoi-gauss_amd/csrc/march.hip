@@ -129,10 +129,7 @@ __device__ __forceinline__ float color_m(const float4& c0, const float4& c1, con
 // 1/2 + sum_{j < (deg+1)^2} b_j sh_kj per channel, reading only the float4 that hold those coefficients, kShChunk
 // float4 at a time (the scheduling barrier keeps the next chunk's loads from being hoisted, which bounds the
 // registers the loads occupy).
-#ifndef VGR_MARCH_SHCHUNK
-#define VGR_MARCH_SHCHUNK 4
-#endif
-constexpr int kShChunk = VGR_MARCH_SHCHUNK;
+constexpr int kShChunk = 4;
 
 template <int NV>
 __device__ __forceinline__ void sh_eval_n(const float4* __restrict__ s, const float (&b)[16], int nb, float (&c)[3]) {
@@ -179,17 +176,7 @@ __device__ __forceinline__ void sample_at(float near, float mid, float far, int 
 // neighbours, same order, same roundings); the first sample at which i loses walks on from its argmin, and the
 // pass at the next site covers it and the samples after it. Each quantity accumulates over the neighbours in the
 // same order as the reference's separate passes.
-#ifndef VGR_MARCH_BATCH
-#define VGR_MARCH_BATCH 6
-#endif
-constexpr int kBatch = VGR_MARCH_BATCH;
-
-#ifndef VGR_MARCH_PIPE
-#define VGR_MARCH_PIPE 0
-#endif
-#ifndef VGR_MARCH_NOHOIST
-#define VGR_MARCH_NOHOIST 1
-#endif
+constexpr int kBatch = 6;
 
 struct CellPass {
     int best[kBatch];
@@ -212,23 +199,14 @@ __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const
     for (int j = 0; j < kBatch; ++j) bd[j] = kInf, s[j] = 0.f, mm[j] = kInf, bk[j] = INT_MAX;
     int k = i;
     int kn = neighbor(F, i, e0, min(1, n - 1));
-#if VGR_MARCH_PIPE
-    SiteRec rc = site_rec<BLK>(F, k);
-#endif
     for (int e = 0; e < n; ++e) {
         const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));  // in flight: the neighbour after next
-#if VGR_MARCH_PIPE
-        const SiteRec rn = site_rec<BLK>(F, kn);  // in flight: the next neighbour's record
-#else
         const SiteRec rc = site_rec<BLK>(F, k);
-#endif
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             float x[3], v[3];
             float tj = t[j];
-#if VGR_MARCH_NOHOIST
             asm volatile("" : "+v"(tj));  // recompute x per neighbour: 3 fewer live registers per sample
-#endif
             point_at(o, d, tj, x);
             offset_to(rc.q0, x, v);
             const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
@@ -237,9 +215,6 @@ __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const
             mm[j] = fminf(mm[j], color_m(rc.q2, rc.q3, v));
         }
         k = kn, kn = k2;
-#if VGR_MARCH_PIPE
-        rc = rn;
-#endif
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) R.best[j] = bk[j], R.sigma[j] = s[j], R.mmin[j] = mm[j];
@@ -283,9 +258,7 @@ __device__ void flush(const MarchField& F, const float (&o)[3], const float (&d)
             if (s < P.n) {
                 float x[3], v[3];
                 float ts = P.t[s];
-#if VGR_MARCH_NOHOIST
-                asm volatile("" : "+v"(ts));
-#endif
+                asm volatile("" : "+v"(ts));  // recompute x per neighbour (registers)
                 point_at(o, d, ts, x);
                 offset_to(p, x, v);
                 const float a = fexp(-0.5f * (color_m(c0, c1, v) - P.mmin[s]));
@@ -376,12 +349,10 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
 
 // Minimum waves per SIMD the register allocation must allow. At 4 the colour pass spills about 17 VGPRs to scratch
 // and the kernel is still 5 % faster than at its natural 3 waves (146 VGPRs): it is bound by the gathers in flight.
-#ifndef VGR_MARCH_WAVES
-#define VGR_MARCH_WAVES 4
-#endif
+constexpr int kMarchWaves = 4;
 
 template <bool TRACE>
-__global__ void __launch_bounds__(kBlock, VGR_MARCH_WAVES)
+__global__ void __launch_bounds__(kBlock, kMarchWaves)
     march_forward_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
     const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
     if (r >= R.n) return;

@@ -506,7 +506,8 @@ def foam_infer_extension():
 
 
 class Graph:
-	"""Fixed sites and their Delaunay adjacency (CSR, int32) on the GPU (ext.py:46-58)."""
+	"""Fixed sites (N, 3) and their Delaunay adjacency as int32 CSR, resident on the GPU (the reference's ext.Graph,
+	ext.py:46-58)."""
 
 	def __init__(self, points, offsets, adj):
 		self.points = points.float().contiguous()
@@ -514,189 +515,206 @@ class Graph:
 		self.adj = adj.int().contiguous()
 
 	def walk(self, o, d, z, start):
-		"""Nearest site of every sample o + z d; z (B, S) sorted along each ray, start (B,) a site near o."""
-		site, steps = extension().walk(self.points, self.offsets, self.adj, o.float().contiguous(),
-									   d.float().contiguous(), z.float().contiguous(), start.int().contiguous())
-		return site, steps
+		"""-> (site (B, S), steps (B,)) int32: the nearest site of each sample o + z d, z (B, S) sorted along each
+		ray, by greedy Delaunay walks from start (B,), a site near each origin."""
+		return extension().walk(self.points, self.offsets, self.adj, o.float().contiguous(), d.float().contiguous(),
+								z.float().contiguous(), start.int().contiguous())
 
 
-class _Density(torch.autograd.Function):
-	"""sigma with the backward of vgr_density_backward (ext.py:61-75)."""
+# Differentiable operators. Each _*Op below pairs a forward kernel call with its gradient kernel call; one generic
+# autograd Function (_Differentiable) runs any of them, so the reference's density / color / conic / march / foam
+# (ext.py:61-216) keep their signatures and gradients while the plumbing lives in one place. An op's forward returns
+# (outputs, extra tensors the backward needs, state shared with the backward); its leading `n_diff` outputs carry
+# gradients, the rest (depths, counters) are marked non-differentiable.
 
-	@staticmethod
-	def forward(ctx, raw, log_scale, quat, x, site, graph):
-		sigma = extension().density_forward(graph.points, graph.offsets, graph.adj, raw, log_scale, quat, x, site, 1.0)
-		ctx.save_for_backward(raw, log_scale, quat, x, site)
-		ctx.graph = graph
-		return sigma
+class _Differentiable(torch.autograd.Function):
 
 	@staticmethod
-	def backward(ctx, grad_sigma):
-		raw, log_scale, quat, x, site = ctx.saved_tensors
-		g = ctx.graph
-		g_raw, g_ls, g_quat = extension().density_backward(g.points, g.offsets, g.adj, raw, log_scale, quat, x, site,
-														   grad_sigma.float().contiguous())
-		return g_raw, g_ls, g_quat, None, None, None
+	def forward(ctx, op, args, *params):
+		outs, extra, state = op.forward(params, args)
+		ctx.op, ctx.args, ctx.state = op, args, state
+		ctx.split = (len(params), len(params) + len(outs))
+		ctx.save_for_backward(*params, *outs, *extra)
+		ctx.mark_non_differentiable(*outs[op.n_diff:])
+		return outs
+
+	@staticmethod
+	def backward(ctx, *grad_outs):
+		saved = ctx.saved_tensors
+		a, b = ctx.split
+		outs = saved[a:b]
+		upstream = [torch.zeros_like(o, dtype=torch.float32) if g is None else g.float().contiguous()
+					for o, g in zip(outs, grad_outs)]
+		grads = ctx.op.backward(saved[:a], ctx.args, outs, saved[b:], upstream, ctx.state)
+		ctx.state = None  # the workspace goes back to torch's allocator
+		return (None, None, *grads)
+
+
+def _evaluate(op, args, params):
+	"""The op's outputs: through autograd when grad mode is on and a parameter requires a gradient, else the plain
+	forward kernel on the detached parameters."""
+	params = [p.contiguous() for p in params]
+	if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+		return _Differentiable.apply(op, args, *params)
+	return op.forward([p.detach() for p in params], args)[0]
+
+
+class _DensityOp:
+	"""params (raw, log_scale, quat); args (graph, x, site)."""
+	n_diff = 1
+
+	@staticmethod
+	def forward(p, a):
+		g, x, site = a
+		return (extension().density_forward(g.points, g.offsets, g.adj, *p, x, site, 1.0),), (), None
+
+	@staticmethod
+	def backward(p, a, outs, extra, grads, state):
+		g, x, site = a
+		return extension().density_backward(g.points, g.offsets, g.adj, *p, x, site, grads[0])
+
+
+class _ColorOp:
+	"""params (log_scale, quat, sh); args (graph, x, dirs, site, sh_deg)."""
+	n_diff = 1
+
+	@staticmethod
+	def forward(p, a):
+		g, x, dirs, site, sh_deg = a
+		return (extension().color_forward(g.points, g.offsets, g.adj, *p, sh_deg, x, dirs, site),), (), None
+
+	@staticmethod
+	def backward(p, a, outs, extra, grads, state):
+		g, x, dirs, site, sh_deg = a
+		return extension().color_backward(g.points, g.offsets, g.adj, *p, sh_deg, x, dirs, site, outs[0], grads[0])
+
+
+class _ConicOp:
+	"""params (log_scale, quat); args (floor,)."""
+	n_diff = 1
+
+	@staticmethod
+	def forward(p, a):
+		return (extension().conic_forward(*p, a[0]),), (), None
+
+	@staticmethod
+	def backward(p, a, outs, extra, grads, state):
+		return extension().conic_backward(*p, a[0], grads[0])
+
+
+class _MarchOp:
+	"""params (raw, dA, cA, sh); args (graph, rays (o, d, start, near, mid, far), (sh_deg, dt, n_bg, t_thresh,
+	w_thresh)). Under autograd both passes run 16 lanes per ray, the faster layout for a training step at every batch
+	size measured, and share one workspace: the backward reuses the site blocks the forward packed."""
+	n_diff = 2
+
+	@staticmethod
+	def forward(p, a):
+		g, rays, cfg = a
+		n = g.points.numel() // 3
+		work = torch.empty(max(int(_lib.load().vgr_march_backward_work_size(n, cfg[0])), 1), dtype=torch.uint8,
+						   device=g.points.device)
+		outs = march_extension().march_forward(g.points, g.offsets, g.adj, *p, cfg[0], *rays, *cfg[1:], lanes=16,
+											   work=work)
+		return tuple(outs), (), work
+
+	@staticmethod
+	def backward(p, a, outs, extra, grads, work):
+		g, rays, cfg = a
+		return march_extension().march_backward(g.points, g.offsets, g.adj, *p, cfg[0], *rays, *cfg[1:], outs[0],
+												outs[1], grads[0], grads[1], lanes=16, work=work)
+
+
+class _FoamOp:
+	"""params (raw, dA, cA, sh); args (graph, rays (o, d, start, near, far), (sh_deg, t_thresh, w_thresh),
+	record_cap). The forward keeps up to record_cap samples per ray for the backward, which replays them (or
+	re-traces rays that did not fit) with the forward's site blocks."""
+	n_diff = 2
+
+	@staticmethod
+	def forward(p, a):
+		g, rays, cfg, record_cap = a
+		n = g.points.numel() // 3
+		work = torch.empty(max(int(_lib.load().vgr_foam_work_size(n, cfg[0])), 1), dtype=torch.uint8,
+						   device=g.points.device)
+		rgb, T, depth, stats, rec = foam_extension().foam_forward(g.points, g.offsets, g.adj, *p, cfg[0], *rays,
+																  *cfg[1:], record_cap, work=work)
+		return (rgb, T, depth, stats), (rec,), work
+
+	@staticmethod
+	def backward(p, a, outs, extra, grads, work):
+		g, rays, cfg, _ = a
+		rgb, T, _, stats = outs
+		return foam_extension().foam_backward(g.points, g.offsets, g.adj, *p, cfg[0], *rays, *cfg[1:], rgb, T,
+											  grads[0], grads[1], extra[0], stats, work=work)
 
 
 def density(graph, raw, log_scale, quat, x, site, scale_mult=1.0):
-	"""sigma(x) = sum over the Voronoi neighborhood of site of exp(raw_k) G_k(x); scale_mult widens the
-	Gaussians (proposal passes, no gradient). Reference: ext.py:78-87."""
-	x = x.detach().float().contiguous()
-	site = site.int().contiguous()
-	params = [p.contiguous() for p in (raw, log_scale, quat)]
-	if scale_mult != 1.0 or not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
-		return extension().density_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params], x,
-										   site, float(scale_mult))
-	return _Density.apply(*params, x, site, graph)
-
-
-class _Color(torch.autograd.Function):
-	"""rgb with the backward of vgr_color_backward (ext.py:90-105)."""
-
-	@staticmethod
-	def forward(ctx, log_scale, quat, sh, x, dirs, site, graph, sh_deg):
-		rgb = extension().color_forward(graph.points, graph.offsets, graph.adj, log_scale, quat, sh, sh_deg, x, dirs,
-										site)
-		ctx.save_for_backward(log_scale, quat, sh, x, dirs, site, rgb)
-		ctx.graph, ctx.sh_deg = graph, sh_deg
-		return rgb
-
-	@staticmethod
-	def backward(ctx, grad_rgb):
-		log_scale, quat, sh, x, dirs, site, rgb = ctx.saved_tensors
-		g = ctx.graph
-		g_ls, g_quat, g_sh = extension().color_backward(g.points, g.offsets, g.adj, log_scale, quat, sh, ctx.sh_deg,
-														x, dirs, site, rgb, grad_rgb.float().contiguous())
-		return g_ls, g_quat, g_sh, None, None, None, None, None
+	"""sigma(x) (m,): sum over the neighbourhood {site} U adj(site) of exp(raw_k) G_k(x), differentiable in raw,
+	log_scale and quat. scale_mult != 1 widens every Gaussian (the proposal rounds) and is never differentiated
+	(ext.py:78-87)."""
+	x, site = x.detach().float().contiguous(), site.int().contiguous()
+	if scale_mult != 1.0:
+		return extension().density_forward(graph.points, graph.offsets, graph.adj,
+										   *[p.detach().contiguous() for p in (raw, log_scale, quat)], x, site,
+										   float(scale_mult))
+	out = _evaluate(_DensityOp, (graph, x, site), (raw, log_scale, quat))
+	return out[0] if isinstance(out, tuple) else out
 
 
 def color(graph, log_scale, quat, sh, x, dirs, site, sh_deg=3):
-	"""C(x, d) = sum_k H_k(x) c_k(d) / sum_k H_k(x) over the Voronoi neighborhood of site; sh (N, 16, 3).
-	Reference: ext.py:108-117."""
-	x = x.detach().float().contiguous()
-	dirs = dirs.detach().float().contiguous()
-	site = site.int().contiguous()
-	params = [p.contiguous() for p in (log_scale, quat, sh)]
-	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
-		return extension().color_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
-										 int(sh_deg), x, dirs, site)
-	return _Color.apply(*params, x, dirs, site, graph, int(sh_deg))
-
-
-class _Conic(torch.autograd.Function):
-	"""Conics with the backward of vgr_conic_backward (ext.py:120-131)."""
-
-	@staticmethod
-	def forward(ctx, log_scale, quat, floor):
-		ctx.save_for_backward(log_scale, quat)
-		ctx.floor = floor
-		return extension().conic_forward(log_scale, quat, floor)
-
-	@staticmethod
-	def backward(ctx, gA):
-		log_scale, quat = ctx.saved_tensors
-		g_ls, g_quat = extension().conic_backward(log_scale, quat, ctx.floor, gA.float().contiguous())
-		return g_ls, g_quat, None
+	"""C(x, d) (m, 3): the colours max(SH_k(d) + 1/2, 0) of the neighbourhood of site, blended with the normalised
+	colour-Gaussian weights H_k(x); sh (N, 16, 3); differentiable in log_scale, quat and sh (ext.py:108-117)."""
+	args = (graph, x.detach().float().contiguous(), dirs.detach().float().contiguous(), site.int().contiguous(),
+			int(sh_deg))
+	out = _evaluate(_ColorOp, args, (log_scale, quat, sh))
+	return out[0] if isinstance(out, tuple) else out
 
 
 def conic(log_scale, quat, floor=0.0):
-	"""(N, 6) inverse covariances (xx, xy, xz, yy, yz, zz) of R diag(s^2 + floor^2) R^T (ext.py:134-136)."""
-	return _Conic.apply(log_scale.contiguous(), quat.contiguous(), float(floor))
+	"""(N, 6) conics (xx, xy, xz, yy, yz, zz) = the inverses of R diag(e^(2 log_scale) + floor^2) R^T, R the rotation
+	of the normalised quaternion; differentiable (ext.py:134-136)."""
+	out = _evaluate(_ConicOp, (float(floor),), (log_scale, quat))
+	return out[0] if isinstance(out, tuple) else out
 
 
 def conic_reference(log_scale, quat, floor=0.0):
-	"""PyTorch version of conic (for tests), ext.py:139-149."""
+	"""The conic in plain torch ops, for tests (the reference's ext.py:139-149): R = (w^2 - |v|^2) I + 2 v v^T +
+	2 w [v]_x for the unit quaternion (w, v), A = sum over the axes a of r_a r_a^T / (e^(2 s_a) + floor^2), r_a the
+	columns of R."""
 	q = quat / quat.norm(dim=-1, keepdim=True).clamp_min(1e-12)
-	w, x, y, z = q.unbind(-1)
-	R = torch.stack([
-		1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
-		2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
-		2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1).view(-1, 3, 3)
+	w, v = q[:, 0], q[:, 1:]
+	zero = torch.zeros_like(w)
+	skew = torch.stack([zero, -v[:, 2], v[:, 1], v[:, 2], zero, -v[:, 0], -v[:, 1], v[:, 0], zero], -1).view(-1, 3, 3)
+	eye = torch.eye(3, dtype=q.dtype, device=q.device)
+	R = ((w * w - (v * v).sum(-1))[:, None, None] * eye + 2 * v[:, :, None] * v[:, None, :] +
+		 2 * w[:, None, None] * skew)
 	inv_var = 1.0 / (torch.exp(2 * log_scale.clamp(-20, 20)) + floor * floor)
-	A = (R * inv_var[:, None, :]) @ R.transpose(1, 2).contiguous()
-	return torch.stack([A[:, 0, 0], A[:, 0, 1], A[:, 0, 2], A[:, 1, 1], A[:, 1, 2], A[:, 2, 2]], -1).contiguous()
-
-
-class _March(torch.autograd.Function):
-	"""The march with its backward (vgr_march_backward re-marches every ray; ext.py:150-169)."""
-
-	@staticmethod
-	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg):
-		# one workspace for both passes: the backward reuses the site blocks the forward packed
-		n = graph.points.numel() // 3
-		work = torch.empty(max(int(_lib.load().vgr_march_backward_work_size(n, cfg[0])), 1), dtype=torch.uint8,
-						   device=raw.device)
-		rgb, T, depth, stats = march_extension().march_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
-															   sh, cfg[0], *rays, *cfg[1:], work=work)
-		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, *rays)
-		ctx.graph, ctx.cfg, ctx.work = graph, cfg, work
-		ctx.mark_non_differentiable(depth, stats)
-		return rgb, T, depth, stats
-
-	@staticmethod
-	def backward(ctx, g_rgb, g_T, _g_depth, _g_stats):
-		raw, dA, cA, sh, rgb, T, *rays = ctx.saved_tensors
-		g, cfg = ctx.graph, ctx.cfg
-		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
-		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
-		grads = march_extension().march_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays,
-												 *cfg[1:], rgb, T, g_rgb, g_T, work=ctx.work)
-		ctx.work = None
-		return (*grads, None, None, None)
+	A = (R[:, :, None, :] * R[:, None, :, :] * inv_var[:, None, None, :]).sum(-1)
+	rows, cols = [0, 0, 0, 1, 1, 2], [0, 1, 2, 1, 2, 2]
+	return A[:, rows, cols].contiguous()
 
 
 def march(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg, t_thresh=1e-4, w_thresh=1e-4):
-	"""Uniform-step fused rendering -> foreground rgb (B, 3) (without background), final transmittance (B,),
-	depth (B,), per-ray stats (B, 3) int: samples marched, samples with color, walk steps (ext.py:172-182)."""
+	"""The uniform-step fused renderer (ext.py:172-182) -> foreground rgb (B, 3) (no background), transmittance T
+	(B,), depth (B,), stats (B, 3) int32: samples, coloured samples, walk steps. rgb and T are differentiable in raw,
+	dA, cA and sh."""
 	rays = tuple(t.float().contiguous() for t in (o, d)) + (start.int().contiguous(),) + \
 		tuple(t.float().contiguous() for t in (near, mid, far))
-	params = [p.float().contiguous() for p in (raw, dA, cA, sh)]
-	cfg = (int(sh_deg), float(dt), int(n_bg), float(t_thresh), float(w_thresh))
-	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
-		return march_extension().march_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
-											   cfg[0], *rays, *cfg[1:])
-	return _March.apply(*params, graph, rays, cfg)
-
-
-class _Foam(torch.autograd.Function):
-	"""The training renderer with its backward (ext.py:185-206)."""
-
-	@staticmethod
-	def forward(ctx, raw, dA, cA, sh, graph, rays, cfg, record_cap):
-		# one workspace for both passes: the backward reuses the site blocks the forward packed
-		n = graph.points.numel() // 3
-		work = torch.empty(max(int(_lib.load().vgr_foam_work_size(n, cfg[0])), 1), dtype=torch.uint8,
-						   device=raw.device)
-		rgb, T, depth, stats, rec = foam_extension().foam_forward(graph.points, graph.offsets, graph.adj, raw, dA, cA,
-																  sh, cfg[0], *rays, *cfg[1:], record_cap, work=work)
-		ctx.save_for_backward(raw, dA, cA, sh, rgb, T, rec, stats, *rays)
-		ctx.graph, ctx.cfg, ctx.work = graph, cfg, work
-		ctx.mark_non_differentiable(depth, stats)
-		return rgb, T, depth, stats
-
-	@staticmethod
-	def backward(ctx, g_rgb, g_T, _g_depth, _g_stats):
-		raw, dA, cA, sh, rgb, T, rec, stats, *rays = ctx.saved_tensors
-		g, cfg = ctx.graph, ctx.cfg
-		g_rgb = torch.zeros_like(rgb) if g_rgb is None else g_rgb.float().contiguous()
-		g_T = torch.zeros_like(T) if g_T is None else g_T.float().contiguous()
-		grads = foam_extension().foam_backward(g.points, g.offsets, g.adj, raw, dA, cA, sh, cfg[0], *rays, *cfg[1:],
-											   rgb, T, g_rgb, g_T, rec, stats, work=ctx.work)
-		ctx.work = None
-		return (*grads, None, None, None, None)
+	return _evaluate(_MarchOp, (graph, rays, (int(sh_deg), float(dt), int(n_bg), float(t_thresh), float(w_thresh))),
+					 [p.float() for p in (raw, dA, cA, sh)])
 
 
 def foam(graph, raw, dA, cA, sh, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, record_cap=256):
-	"""Rendering at the interaction points of the rays with the Voronoi faces -> foreground rgb (B, 3), final
-	transmittance (B,), depth (B,), per-ray stats (B, 3) int: samples, segments with colour, walk steps to x(near).
-	With gradients, up to record_cap samples per ray are kept for the backward pass (0: re-trace every ray)
-	(ext.py:209-216)."""
+	"""The training renderer at the ray / Voronoi-face crossings (ext.py:205-216) -> foreground rgb (B, 3),
+	transmittance (B,), depth (B,), stats (B, 3) int32: samples, coloured segments, walk steps to x(near). Under
+	autograd up to record_cap samples per ray are recorded for the backward (0: it re-traces every ray)."""
 	rays = tuple(t.float().contiguous() for t in (o, d)) + (start.int().contiguous(),) + \
 		tuple(t.float().contiguous() for t in (near, far))
-	cfg = (int(sh_deg), float(t_thresh), float(w_thresh))
-	params = [p.float().contiguous() for p in (raw, dA, cA, sh)]
-	if not torch.is_grad_enabled() or not any(p.requires_grad for p in params):
-		return foam_extension().foam_forward(graph.points, graph.offsets, graph.adj, *[p.detach() for p in params],
-											 cfg[0], *rays, *cfg[1:], 0)[:4]
-	return _Foam.apply(*params, graph, rays, cfg, int(record_cap))
+	params = [p.float() for p in (raw, dA, cA, sh)]
+	args = (graph, rays, (int(sh_deg), float(t_thresh), float(w_thresh)), int(record_cap))
+	if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+		return _Differentiable.apply(_FoamOp, args, *[p.contiguous() for p in params])
+	g = graph
+	return foam_extension().foam_forward(g.points, g.offsets, g.adj, *[p.detach().contiguous() for p in params],
+										 args[2][0], *rays, *args[2][1:], 0)[:4]

@@ -1,8 +1,10 @@
-"""Per-site parameters of the field (model.py:19-59 of the reference): density Gaussian (rho = exp(raw), scale,
-rotation), colour Gaussian (scale, rotation), SH colour (sh_dc + sh_rest) and a background logit.
+"""The field's per-site parameters as a torch module, and the loader of trained checkpoints.
 
-They are nn.Parameters: the renderers' autograd Functions (ext.foam, ext.march, ext.density, ext.color, ext.conic)
-give them gradients; the optimiser and the training loop are the reference's own train.py."""
+VoronoiGaussField keeps the reference's class name, constructor arguments, parameter names (so a model.pth
+state_dict loads into it) and methods (model.py:19-59): a density Gaussian per site (rho = exp(raw), log-scales,
+rotation quaternion), a colour Gaussian (log-scales, quaternion), SH colour coefficients split into the DC term and
+the rest, and a background logit. The renderers' autograd Functions (ext.foam, ext.march, ext.density, ext.color,
+ext.conic) give the parameters their gradients; the optimiser and the training loop stay the reference's train.py."""
 
 import math
 
@@ -11,66 +13,86 @@ import torch.nn as nn
 
 from .ext import Graph
 
-C0 = 0.28209479177387814
+# SH degree-0 basis value: a site's base colour is 1/2 + SH_DC0 * sh_dc.
+SH_DC0 = 0.28209479177387814
+C0 = SH_DC0  # the reference's name for it (model.py:10)
+
+# state_dict names of the per-site parameters, in the reference's order
+_SITE_PARAMS = ('raw', 'd_log_scale', 'd_quat', 'c_log_scale', 'c_quat', 'sh_dc', 'sh_rest')
 
 
 def identity_quat(n, device):
-	q = torch.zeros(n, 4, device=device)
-	q[:, 0] = 1.0
-	return q
+	"""(n, 4) unit quaternions w x y z of the identity rotation."""
+	return torch.tensor([1.0, 0.0, 0.0, 0.0], device=device).repeat(n, 1)
+
+
+def _opacity_density(spacing, alpha):
+	"""Density rho of a Gaussian of scale `spacing` whose line integral through its centre, rho * s * sqrt(2 pi),
+	is the optical depth -ln(1 - alpha) of opacity alpha."""
+	return -math.log1p(-alpha) / (spacing * math.sqrt(2.0 * math.pi))
 
 
 class VoronoiGaussField(nn.Module):
-	"""points (N, 3) fixed sites; offsets/adj their Delaunay adjacency; colors (N, 3) in [0, 1]; spacing (N,)
-	mean distance to the nearest sites, used as the initial isotropic scale of both Gaussians."""
+	"""Field over the fixed sites `points` (N, 3) with Delaunay adjacency (offsets, adj). colors (N, 3) in [0, 1]
+	set the initial DC colours; spacing (N,) the initial isotropic scale of both Gaussians (clamped to >= 1e-4), and
+	each density starts at the value that gives a lone Gaussian opacity init_alpha along a ray through its centre.
+	sh_deg is the highest SH degree the coefficients hold; the degree in use (sh_deg attribute) starts at 0."""
 
 	def __init__(self, points, offsets, adj, colors, spacing, init_alpha=0.1, sh_deg=3):
 		super().__init__()
-		device = points.device
-		n = len(points)
+		n, dev = points.shape[0], points.device
 		self.graph = Graph(points, offsets, adj)
 		self.max_sh_deg, self.sh_deg = sh_deg, 0
-		s = spacing.clamp_min(1e-4)
-		# a ray through the centre of a lone Gaussian has opacity init_alpha: rho s sqrt(2 pi) = -ln(1 - a)
-		rho = -math.log(1.0 - init_alpha) / (s * math.sqrt(2.0 * math.pi))
-		self.raw = nn.Parameter(rho.log())
-		self.d_log_scale = nn.Parameter(s.log()[:, None].repeat(1, 3))
-		self.d_quat = nn.Parameter(identity_quat(n, device))
-		self.c_log_scale = nn.Parameter(s.log()[:, None].repeat(1, 3))
-		self.c_quat = nn.Parameter(identity_quat(n, device))
-		self.sh_dc = nn.Parameter(((colors.clamp(0, 1) - 0.5) / C0)[:, None])
-		self.sh_rest = nn.Parameter(torch.zeros(n, 15, 3, device=device))
-		self.bg_logit = nn.Parameter(torch.zeros(3, device=device))
+		scale = spacing.clamp_min(1e-4)
+		log_scale = scale.log().unsqueeze(1).expand(n, 3)
+		init = {
+			'raw': _opacity_density(scale, init_alpha).log(),
+			'd_log_scale': log_scale, 'd_quat': identity_quat(n, dev),
+			'c_log_scale': log_scale, 'c_quat': identity_quat(n, dev),
+			'sh_dc': ((colors.clamp(0, 1) - 0.5) / SH_DC0).unsqueeze(1),
+			'sh_rest': torch.zeros(n, 15, 3, device=dev),
+		}
+		for name in _SITE_PARAMS:
+			self.register_parameter(name, nn.Parameter(init[name].contiguous().clone()))
+		self.bg_logit = nn.Parameter(torch.zeros(3, device=dev))
 
 	@classmethod
 	def from_scene(cls, scene, device='cuda', requires_grad=False):
-		"""Field holding a synthetic scene's parameters (scenes.Scene) on `device`."""
-		t = lambda a: torch.as_tensor(a, device=device)  # noqa: E731
+		"""Field holding the parameters of a synthetic scene (scenes.Scene) on `device`."""
+		def on(a):
+			return torch.as_tensor(a, device=device)
 		n = scene.n_sites
-		m = cls(t(scene.points), t(scene.offsets), t(scene.adj), torch.zeros(n, 3, device=device),
+		m = cls(on(scene.points), on(scene.offsets), on(scene.adj), torch.zeros(n, 3, device=device),
 				torch.ones(n, device=device), sh_deg=max(scene.sh_deg, 0))
+		sh = on(scene.sh)
+		values = {'raw': on(scene.raw), 'd_log_scale': on(scene.log_scale), 'c_log_scale': on(scene.log_scale),
+				  'd_quat': on(scene.quat), 'c_quat': on(scene.quat), 'sh_dc': sh[:, :1], 'sh_rest': sh[:, 1:]}
 		with torch.no_grad():
-			m.raw.copy_(t(scene.raw))
-			m.d_log_scale.copy_(t(scene.log_scale))
-			m.c_log_scale.copy_(t(scene.log_scale))
-			m.d_quat.copy_(t(scene.quat))
-			m.c_quat.copy_(t(scene.quat))
-			sh = t(scene.sh)
-			m.sh_dc.copy_(sh[:, :1])
-			m.sh_rest.copy_(sh[:, 1:])
+			for name, v in values.items():
+				getattr(m, name).copy_(v)
 		m.sh_deg = scene.sh_deg
 		m.requires_grad_(requires_grad)
 		return m
 
 	@property
 	def n_sites(self):
-		return len(self.raw)
+		return self.raw.shape[0]
 
 	def sh(self):
+		"""(N, 16, 3) SH coefficients, DC first."""
 		return torch.cat([self.sh_dc, self.sh_rest], 1)
 
 	def walk(self, o, d, z, start):
+		"""Nearest site of each sample o + z d (z sorted along each ray) by the greedy Delaunay walk."""
 		return self.graph.walk(o, d, z, start)
+
+	def param_groups(self, lr):
+		"""Optimiser groups keyed like the reference's (model.py:51-59): lr is a dict with 'raw', 'scale', 'quat',
+		'sh_dc', 'sh_rest' and 'bg'."""
+		groups = {'raw': ['raw'], 'scale': ['d_log_scale', 'c_log_scale'], 'quat': ['d_quat', 'c_quat'],
+				  'sh_dc': ['sh_dc'], 'sh_rest': ['sh_rest'], 'bg': ['bg_logit']}
+		return [{'params': [getattr(self, p) for p in names], 'lr': lr[key], 'name': key}
+				for key, names in groups.items()]
 
 
 # numpy types a reference checkpoint's `normalization` (center array, scale scalar) is made of: the only globals the

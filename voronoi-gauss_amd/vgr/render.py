@@ -1,313 +1,357 @@
-"""Host render orchestration of the forward/inference path: the reference's render.py API (render.py:16-266)
-over the gfx950 operators of ext.py.
+"""Host side of the renderers: ray bounds, the packed records of the inference renderer, a NeRF-style sampler over
+the field operators, and the wrappers that add the background colour.
 
-render_rays_foam_infer (the north-star path), render_rays_uniform and render_rays keep the reference's
-signatures and outputs; pack_foam builds the same inference records (self-first CSR, float4 edges with
-half2 cut-offs, attr (N, 20), optional Z-order renumbering). render_rays_foam (the training renderer) is out of
-scope."""
+The public functions keep the names, arguments and outputs of the reference's render.py (cited per function), so
+code written against it runs unchanged; the bodies are this package's own, written around the gfx950 operators of
+ext.py (libvgr.so). render_rays_foam_infer is the north-star path: one vgr_foam_infer launch per call."""
 
 import math
 
 import torch
+import torch.nn.functional as F
 
 from . import ext
 
+# ---------------------------------------------------------------------------------------------------- ray bounds
+
 
 def sphere_exit(o, d, radius):
-	"""Ray parameter where o + t d leaves the sphere of `radius` about the origin (render.py:16-19)."""
-	b = (o * d).sum(-1)
-	c = (o * o).sum(-1) - radius * radius
-	return -b + (b * b - c).clamp_min(0).sqrt()
+	"""Ray parameter at which o + t d (unit d) leaves the sphere of `radius` about the origin: the larger root of
+	t^2 + 2 (o.d) t + |o|^2 - radius^2 = 0, with a negative discriminant taken as 0 (render.py:16-19)."""
+	od = (o * d).sum(-1)
+	disc = od * od - ((o * o).sum(-1) - radius * radius)
+	return disc.clamp_min(0).sqrt() - od
+
+
+def _exit_after(o, d, radius, earliest):
+	return torch.maximum(sphere_exit(o, d, radius), torch.as_tensor(earliest, dtype=o.dtype, device=o.device))
 
 
 def ray_bounds(o, d, near, far_radius):
-	"""-> near (constant), mid (unit-sphere exit, >= near + 1e-3), far (far-sphere exit, >= mid + 1e-3);
-	render.py:22-25."""
-	t_mid = sphere_exit(o, d, 1.0).clamp_min(near + 1e-3)
-	t_far = torch.maximum(sphere_exit(o, d, far_radius), t_mid + 1e-3)
+	"""(near, mid, far) per ray: near is the constant `near`; mid the exit of the unit sphere, at least near + 1e-3;
+	far the exit of the sphere of radius far_radius, at least mid + 1e-3 (render.py:22-25)."""
+	t_mid = _exit_after(o, d, 1.0, near + 1e-3)
+	t_far = _exit_after(o, d, far_radius, t_mid + 1e-3)
 	return torch.full_like(t_mid, near), t_mid, t_far
 
 
+# ---------------------------------------------------------------------------------------- NeRF-style sampling
+
+
 def s_to_t(s, t_near, t_mid, t_far):
-	"""Normalised ray coordinate -> t: linear to mid on [0, 1/2], linear in disparity beyond (render.py:28-33)."""
-	t_near, t_mid, t_far = t_near[:, None], t_mid[:, None], t_far[:, None]
-	lin = t_near + (t_mid - t_near) * (2 * s).clamp(max=1)
-	u = (2 * s - 1).clamp(min=0)
-	disp = 1.0 / (1.0 / t_mid + u * (1.0 / t_far - 1.0 / t_mid))
-	return torch.where(s < 0.5, lin, disp)
+	"""Ray parameter of the normalised coordinate s in [0, 1]: s in [0, 1/2] maps linearly onto [near, mid], s in
+	[1/2, 1] linearly in disparity 1/t onto [mid, far] (render.py:28-33)."""
+	n, m, f = t_near.unsqueeze(-1), t_mid.unsqueeze(-1), t_far.unsqueeze(-1)
+	inside = torch.lerp(n.expand_as(s), m.expand_as(s), (2 * s).clamp(max=1.0))
+	beyond = 1.0 / torch.lerp((1.0 / m).expand_as(s), (1.0 / f).expand_as(s), (2 * s - 1).clamp(min=0.0))
+	return torch.where(s < 0.5, inside, beyond)
 
 
 def sample_pdf(bins, weights, n, det=True):
-	"""Inverse-CDF sampling of n points per ray from piecewise-constant weights over bins (render.py:36-50)."""
-	weights = weights + 1e-5
-	pdf = weights / weights.sum(-1, keepdim=True)
-	cdf = torch.cat([torch.zeros_like(pdf[:, :1]), torch.cumsum(pdf, -1)], -1)
+	"""n samples per ray from the piecewise-constant density `weights` (+1e-5 each) over the intervals of `bins`
+	(B, S + 1), by inverting its CDF at n evenly spaced (det) or uniform random levels (render.py:36-50)."""
+	w = weights + 1e-5
+	cdf = F.pad(torch.cumsum(w / w.sum(-1, keepdim=True), -1), (1, 0), value=0.0)
+	B = bins.shape[0]
 	if det:
-		u = torch.linspace(0.5 / n, 1 - 0.5 / n, n, device=bins.device).expand(len(bins), n).contiguous()
+		levels = ((torch.arange(n, device=bins.device, dtype=bins.dtype) + 0.5) / n).expand(B, n).contiguous()
 	else:
-		u = torch.rand(len(bins), n, device=bins.device)
-	inds = torch.searchsorted(cdf, u, right=True)
-	below = (inds - 1).clamp_min(0)
-	above = inds.clamp_max(cdf.shape[-1] - 1)
-	cdf_b, cdf_a = cdf.gather(1, below), cdf.gather(1, above)
-	bin_b, bin_a = bins.gather(1, below), bins.gather(1, above)
-	denom = torch.where(cdf_a - cdf_b < 1e-5, torch.ones_like(cdf_a), cdf_a - cdf_b)
-	return bin_b + (u - cdf_b) / denom * (bin_a - bin_b)
+		levels = torch.rand(B, n, device=bins.device, dtype=bins.dtype)
+	hi = torch.searchsorted(cdf, levels, right=True)
+	i0, i1 = (hi - 1).clamp_min(0), hi.clamp_max(cdf.shape[-1] - 1)
+	c0, c1 = cdf.gather(1, i0), cdf.gather(1, i1)
+	span = c1 - c0
+	frac = (levels - c0) / torch.where(span < 1e-5, torch.ones_like(span), span)
+	b0, b1 = bins.gather(1, i0), bins.gather(1, i1)
+	return b0 + frac * (b1 - b0)
 
 
 def composite(sigma, t, t_far):
-	"""NeRF compositing of samples at t: weights (B, S) and final transmittance (B,); render.py:53-57."""
-	delta = torch.cat([t[:, 1:] - t[:, :-1], (t_far[:, None] - t[:, -1:]).clamp_min(0)], 1)
-	alpha = 1.0 - torch.exp(-sigma * delta)
-	trans = torch.cumprod(torch.cat([torch.ones_like(alpha[:, :1]), 1.0 - alpha + 1e-10], 1), 1)
+	"""NeRF alpha compositing of samples at t (B, S) with densities sigma: the last sample's interval reaches t_far
+	(empty when t_far is before it) -> weights (B, S), final transmittance (B,) (render.py:53-57)."""
+	ends = torch.cat([t, torch.maximum(t_far.unsqueeze(-1), t[:, -1:])], 1)
+	alpha = 1.0 - torch.exp(-sigma * torch.diff(ends, dim=1))
+	trans = torch.cumprod(F.pad(1.0 - alpha + 1e-10, (1, 0), value=1.0), 1)
 	return alpha * trans[:, :-1], trans[:, -1]
 
 
+def _points(o, d, t):
+	"""(B * S, 3) sample points o + t d for t (B, S)."""
+	return torch.addcmul(o.unsqueeze(1), d.unsqueeze(1), t.unsqueeze(-1)).reshape(-1, 3)
+
+
 def proposal_weights(model, o, d, s, bounds, start, scale_mult):
-	"""Compositing weights of widened density Gaussians at s (render.py:60-68)."""
+	"""Compositing weights at the normalised coordinates s of the density with every Gaussian widened by
+	scale_mult, as a proposal for the next sampling round (render.py:60-68)."""
 	t = s_to_t(s, *bounds)
 	site, _ = model.walk(o, d, t, start)
-	x = (o[:, None] + d[:, None] * t[..., None]).reshape(-1, 3)
 	with torch.no_grad():
-		sigma = ext.density(model.graph, model.raw, model.d_log_scale, model.d_quat, x, site.reshape(-1),
-							scale_mult).view_as(t)
-	w, _ = composite(sigma, t, bounds[2])
-	return w
+		sigma = ext.density(model.graph, model.raw, model.d_log_scale, model.d_quat, _points(o, d, t),
+							site.reshape(-1), scale_mult)
+	return composite(sigma.view_as(t), t, bounds[2])[0]
 
 
 def resample(s, w, n, det):
-	mid = 0.5 * (s[:, 1:] + s[:, :-1])
-	bins = torch.cat([torch.zeros_like(s[:, :1]), mid, torch.ones_like(s[:, :1])], 1)
-	return sample_pdf(bins, w, n, det)
+	"""n new coordinates drawn from weights w at s, over intervals bounded by the midpoints of s and by 0 and 1."""
+	edges = F.pad(F.pad(0.5 * (s[:, :-1] + s[:, 1:]), (1, 0), value=0.0), (0, 1), value=1.0)
+	return sample_pdf(edges, w, n, det)
 
 
 def render_rays(model, o, d, start, n_coarse=64, n_fine=(64, 64), proposal_mult=(4.0, 2.0), near=0.02,
 				far_radius=4.0, perturb=True, min_weight=1e-4):
-	"""NeRF-style rendering: 64 stratified samples + 2 proposal passes, walked to their sites, density and colour
-	from the field operators, NeRF compositing (render.py:77-106). o, d (B, 3), start (B,) -> dict with rgb
-	(B, 3), acc, depth, walk_steps, active."""
-	B = len(o)
+	"""NeRF-style rendering through the field operators (render.py:77-106): n_coarse stratified coordinates, then one
+	proposal round per entry of n_fine (Gaussians widened by proposal_mult) each adding that many coordinates; the
+	merged, sorted samples are walked to their sites, their density and (where the compositing weight exceeds
+	min_weight) colour evaluated, and composited over the background. -> dict rgb (B, 3), acc, depth, walk_steps
+	(mean walk steps per sample), active (fraction of samples coloured)."""
+	B = o.shape[0]
 	bounds = ray_bounds(o, d, near, far_radius)
-	s = torch.linspace(0, 1, n_coarse + 1, device=o.device)[:-1].expand(B, n_coarse)
-	s = s + (torch.rand_like(s) if perturb else 0.5) / n_coarse
+	cells = torch.arange(n_coarse, device=o.device, dtype=o.dtype).expand(B, n_coarse)
+	jitter = torch.rand_like(cells) if perturb else torch.full_like(cells, 0.5)
+	s = (cells + jitter) / n_coarse
 	with torch.no_grad():
 		for n, mult in zip(n_fine, proposal_mult):
-			w = proposal_weights(model, o, d, s, bounds, start, mult)
-			s_new = resample(s, w, n, det=not perturb)
-			s, _ = torch.sort(torch.cat([s, s_new], 1), 1)
+			extra = resample(s, proposal_weights(model, o, d, s, bounds, start, mult), n, det=not perturb)
+			s = torch.sort(torch.cat([s, extra], 1), 1).values
 		t = s_to_t(s, *bounds)
 		site, steps = model.walk(o, d, t, start)
 	S = t.shape[1]
-	x = (o[:, None] + d[:, None] * t[..., None]).reshape(-1, 3)
-	site = site.reshape(-1)
+	x, site = _points(o, d, t), site.reshape(-1)
 	sigma = ext.density(model.graph, model.raw, model.d_log_scale, model.d_quat, x, site).view(B, S)
-	w, t_final = composite(sigma, t, bounds[2])
+	w, t_last = composite(sigma, t, bounds[2])
+	coloured = torch.nonzero(w.detach().reshape(-1) > min_weight).squeeze(1)
+	ray_dirs = d.unsqueeze(1).expand(B, S, 3).reshape(-1, 3)
+	c = ext.color(model.graph, model.c_log_scale, model.c_quat, model.sh(), x[coloured], ray_dirs[coloured],
+				  site[coloured], model.sh_deg)
+	per_sample = torch.zeros(B * S, 3, device=o.device, dtype=c.dtype).index_put((coloured,), c).view(B, S, 3)
+	rgb = torch.einsum('bs,bsc->bc', w, per_sample) + t_last.unsqueeze(-1) * torch.sigmoid(model.bg_logit)
+	return {'rgb': rgb, 'acc': 1.0 - t_last, 'depth': (w * t).sum(1), 'walk_steps': steps.float().mean() / S,
+			'active': coloured.numel() / (B * S)}
 
-	active = (w.detach() > min_weight).reshape(-1).nonzero().squeeze(1)
-	dirs = d[:, None].expand(B, S, 3).reshape(-1, 3)
-	c = ext.color(model.graph, model.c_log_scale, model.c_quat, model.sh(), x[active], dirs[active], site[active],
-				  model.sh_deg)
-	rgb_s = torch.zeros(B * S, 3, device=o.device, dtype=c.dtype).index_put((active,), c).view(B, S, 3)
-	bg = torch.sigmoid(model.bg_logit)
-	rgb = (w[..., None] * rgb_s).sum(1) + t_final[:, None] * bg
-	depth = (w * t).sum(1)
-	return {'rgb': rgb, 'acc': 1.0 - t_final, 'depth': depth, 'walk_steps': steps.float().mean() / S,
-			'active': len(active) / (B * S)}
+
+# ------------------------------------------------------------------------------------ fused-kernel renderers
+
+
+def _with_background(model, fg, T):
+	return fg + T.unsqueeze(-1) * torch.sigmoid(model.bg_logit)
 
 
 def render_rays_uniform(model, o, d, start, dt=1 / 512, n_bg=64, near=0.02, far_radius=4.0, t_thresh=1e-4,
 						w_thresh=1e-4, scale_floor=None, perturb=False):
-	"""Fixed steps dt inside the unit ball, n_bg steps uniform in disparity beyond, early termination at
-	T < t_thresh, one fused kernel; scale_floor (default dt / 2) is added in quadrature to every Gaussian scale
-	(render.py:109-124)."""
-	near_t, mid_t, far_t = ray_bounds(o, d, near, far_radius)
-	floor = 0.5 * dt if scale_floor is None else scale_floor
-	dA = ext.conic(model.d_log_scale, model.d_quat, floor)
-	cA = ext.conic(model.c_log_scale, model.c_quat, floor)
-	fg, T, depth, stats = ext.march(model.graph, model.raw, dA, cA, model.sh(), model.sh_deg, o, d, start, near_t,
-									mid_t, far_t, dt, n_bg, t_thresh, w_thresh)
-	rgb = fg + T[:, None] * torch.sigmoid(model.bg_logit)
-	stats = stats.float()
-	return {'rgb': rgb, 'acc': 1.0 - T, 'depth': depth, 'samples': stats[:, 0].mean(),
-			'active': (stats[:, 1].sum() / stats[:, 0].sum()).item(),
-			'walk_steps': stats[:, 2].sum() / stats[:, 0].sum()}
+	"""One vgr_march_forward launch (render.py:109-124): steps of dt inside the unit ball, n_bg steps uniform in
+	disparity beyond it, NeRF alpha, early termination at T < t_thresh; every Gaussian's scale gets scale_floor
+	(default dt / 2) added in quadrature. -> dict rgb, acc, depth, samples (mean per ray), active (coloured
+	fraction of the samples), walk_steps (per sample)."""
+	t_near, t_mid, t_far = ray_bounds(o, d, near, far_radius)
+	floor = dt / 2 if scale_floor is None else scale_floor
+	conics = [ext.conic(ls, q, floor) for ls, q in ((model.d_log_scale, model.d_quat),
+													(model.c_log_scale, model.c_quat))]
+	fg, T, depth, stats = ext.march(model.graph, model.raw, *conics, model.sh(), model.sh_deg, o, d, start, t_near,
+									t_mid, t_far, dt, n_bg, t_thresh, w_thresh)
+	n_samples, n_coloured, n_steps = stats.float().sum(0).unbind()
+	return {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth,
+			'samples': n_samples / stats.shape[0], 'active': (n_coloured / n_samples).item(),
+			'walk_steps': n_steps / n_samples}
 
 
 def render_rays_foam(model, o, d, start, near=0.02, far_radius=4.0, t_thresh=1e-4, w_thresh=1e-4, scale_floor=0.0,
 					 perturb=False):
-	"""Samples at the crossings of each ray with the Voronoi faces (plus x(near) and x(far)), trapezoid
-	compositing, one fused kernel with a backward (ext.foam); train.py's default renderer (render.py:127-140)."""
-	near_t, _, far_t = ray_bounds(o, d, near, far_radius)
-	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
-	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
-	fg, T, depth, stats = ext.foam(model.graph, model.raw, dA, cA, model.sh(), model.sh_deg, o, d, start, near_t,
-								   far_t, t_thresh, w_thresh)
-	rgb = fg + T[:, None] * torch.sigmoid(model.bg_logit)
-	stats = stats.float()
-	segments = (stats[:, 0] - 1).sum().clamp_min(1)
-	return {'rgb': rgb, 'acc': 1.0 - T, 'depth': depth, 'samples': stats[:, 0].mean(),
-			'active': (stats[:, 1].sum() / segments).item(), 'walk_steps': stats[:, 2].mean()}
+	"""The training renderer (render.py:127-140): samples at x(near), at every Voronoi-face crossing and at x(far),
+	trapezoid compositing, one vgr_foam_forward launch with its backward under autograd (ext.foam). -> dict rgb,
+	acc, depth, samples (mean per ray), active (coloured fraction of the segments), walk_steps (mean per ray)."""
+	t_near, _, t_far = ray_bounds(o, d, near, far_radius)
+	conics = [ext.conic(ls, q, scale_floor) for ls, q in ((model.d_log_scale, model.d_quat),
+														  (model.c_log_scale, model.c_quat))]
+	fg, T, depth, stats = ext.foam(model.graph, model.raw, *conics, model.sh(), model.sh_deg, o, d, start, t_near,
+								   t_far, t_thresh, w_thresh)
+	st = stats.float()
+	segments = torch.clamp_min((st[:, 0] - 1).sum(), 1)
+	return {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth, 'samples': st[:, 0].mean(),
+			'active': (st[:, 1].sum() / segments).item(), 'walk_steps': st[:, 2].mean()}
+
+
+# ------------------------------------------------------------------------------------------------ SH basis
+
+# Real spherical harmonics up to degree 3 in the sign convention of 3D Gaussian splatting (the constants of
+# render.py:143-165 and foam_infer.cu:95-118); the kernels evaluate the same polynomials.
+_SH0 = 0.28209479177387814
+_SH1 = 0.4886025119029199
+_SH2 = (1.0925484305920792, 0.31539156525252005, 0.5462742152960396)
+_SH3 = (0.5900435899266435, 2.890611442640554, 0.4570457994644658, 0.3731763325901154, 1.445305721320277)
 
 
 def sh_basis(d, deg):
-	"""Real SH basis (B, 16) of unit directions d (B, 3), same constants and signs as the kernels
-	(render.py:143-165)."""
+	"""(B, 16) basis values at the unit directions d (B, 3), zero beyond degree `deg`."""
 	x, y, z = d.unbind(-1)
-	b = torch.zeros(len(d), 16, device=d.device, dtype=d.dtype)
-	b[:, 0] = 0.28209479177387814
+	cols = [torch.full_like(x, _SH0)]
 	if deg >= 1:
-		b[:, 1], b[:, 2], b[:, 3] = -0.4886025119029199 * y, 0.4886025119029199 * z, -0.4886025119029199 * x
+		cols += [-_SH1 * y, _SH1 * z, -_SH1 * x]
 	if deg >= 2:
+		a, b, c = _SH2
 		xx, yy, zz = x * x, y * y, z * z
-		b[:, 4] = 1.0925484305920792 * x * y
-		b[:, 5] = -1.0925484305920792 * y * z
-		b[:, 6] = 0.31539156525252005 * (2 * zz - xx - yy)
-		b[:, 7] = -1.0925484305920792 * x * z
-		b[:, 8] = 0.5462742152960396 * (xx - yy)
+		cols += [a * x * y, -a * y * z, b * (2 * zz - xx - yy), -a * x * z, c * (xx - yy)]
 	if deg >= 3:
-		b[:, 9] = -0.5900435899266435 * y * (3 * xx - yy)
-		b[:, 10] = 2.890611442640554 * x * y * z
-		b[:, 11] = -0.4570457994644658 * y * (4 * zz - xx - yy)
-		b[:, 12] = 0.3731763325901154 * z * (2 * zz - 3 * xx - 3 * yy)
-		b[:, 13] = -0.4570457994644658 * x * (4 * zz - xx - yy)
-		b[:, 14] = 1.445305721320277 * z * (xx - yy)
-		b[:, 15] = -0.5900435899266435 * x * (xx - 3 * yy)
-	return b
+		a, b, c, e, f = _SH3
+		lat = 4 * zz - xx - yy
+		cols += [-a * y * (3 * xx - yy), b * x * y * z, -c * y * lat, e * z * (2 * zz - 3 * xx - 3 * yy), -c * x * lat,
+				 f * z * (xx - yy), -a * x * (xx - 3 * yy)]
+	basis = torch.stack(cols, -1)
+	return F.pad(basis, (0, 16 - basis.shape[-1]))
+
+
+# ------------------------------------------------------------------------------ Z-order and the inference pack
+
+
+def _dilate3(v):
+	"""Spreads the low 21 bits of v (int64) so that bit i lands at bit 3 i."""
+	v = v & 0x1FFFFF
+	v = (v | (v << 32)) & 0x1F00000000FFFF
+	v = (v | (v << 16)) & 0x1F0000FF0000FF
+	v = (v | (v << 8)) & 0x100F00F00F00F00F
+	v = (v | (v << 4)) & 0x10C30C30C30C30C3
+	return (v | (v << 2)) & 0x1249249249249249
 
 
 def morton_codes(points, bits=10):
-	"""Z-order keys of the points over their bounding box, as morton_order sorts them (render.py:168-176): on the
-	GPU one pass of vgr_morton_codes, on the host the same arithmetic in torch."""
+	"""Z-order keys of the points over their bounding box, `bits` bits per axis, x in the lowest bit of each triple
+	(the keys morton_order sorts, render.py:168-176): on the GPU vgr_morton_codes, on the host the same quantisation
+	(p - lo) / (hi - lo) * (2^bits - 1), truncated, then bit-interleaved."""
 	if points.is_cuda:
 		return ext.morton_codes(points.float().contiguous(), bits)
 	lo, hi = points.amin(0), points.amax(0)
 	q = ((points - lo) / (hi - lo).clamp_min(1e-12) * (2 ** bits - 1)).long()
-	code = torch.zeros(len(points), dtype=torch.long, device=points.device)
-	for b in range(bits):
-		for a in range(3):
-			code |= ((q[:, a] >> b) & 1) << (3 * b + a)
-	return code
+	return _dilate3(q[:, 0]) | (_dilate3(q[:, 1]) << 1) | (_dilate3(q[:, 2]) << 2)
 
 
 def morton_order(points, bits=10):
-	"""Permutation sorting the points along a Z-order curve of their bounding box (render.py:168-176)."""
+	"""Permutation that sorts the points along the Z-order curve of their bounding box (render.py:168-176)."""
 	return torch.argsort(morton_codes(points, bits))
 
 
 def cut_bits(r2, lam):
-	"""(N,) f32 whose bit pattern is half2(r2, lam): r2 in the low 16 bits, lam in the high ones, each rounded
-	to nearest even (render.py:197)."""
-	return torch.stack([r2, lam], -1).half().view(torch.float32)[:, 0]
+	"""float32 words whose bits are two halves, r2 in the low 16 bits and lam in the high 16, each rounded to the
+	nearest even half (the packing of render.py:197)."""
+	lo = r2.half().view(torch.int16).to(torch.int32) & 0xFFFF
+	hi = lam.half().view(torch.int16).to(torch.int32) << 16
+	return (lo | hi).view(torch.float32)
+
+
+def _cut_words(raw, d_log_scale, c_log_scale, scale_floor, eps_density):
+	"""Per site, the word of half2(r2, lam): r2 the squared distance beyond which exp(raw) G(x) < eps_density
+	(2 s_max^2 max(raw - ln eps, 0), +inf when eps_density = 0) and lam the smallest eigenvalue of the colour conic,
+	each moved by 2^-9 to the safe side of its half rounding, lam at most 65000."""
+	floor2 = scale_floor * scale_floor
+	if eps_density > 0:
+		s_max2 = (torch.exp(2 * d_log_scale.clamp(-20, 20)) + floor2).amax(-1)
+		r2 = 2 * s_max2 * (raw - math.log(eps_density)).clamp_min(0) * (1 + 2 ** -9)
+	else:
+		r2 = torch.full_like(raw, math.inf)
+	lam = 1.0 / (torch.exp(2 * c_log_scale.clamp(-20, 20)) + floor2).amax(-1)
+	return cut_bits(r2, (lam * (1 - 2 ** -9)).clamp(max=65000.0))
 
 
 @torch.no_grad()
 def pack_foam_arrays(points, offsets, adj, raw, d_log_scale, c_log_scale, dA, cA, sh, scale_floor=0.0,
 					 eps_density=0.0, sh_half=False, reorder=False):
-	"""Inference records from plain tensors (the body of pack_foam, render.py:179-225), conics dA/cA given.
+	"""The inference records (the format of render.py:179-225) from plain tensors with the conics given, in torch
+	on any device; pack_foam builds the same records on the GPU. Each site's neighbourhood is listed self first,
+	then its Delaunay neighbours in CSR order, as one stable sort of (cell, entry) pairs; renumbering (reorder)
+	is a second stable sort by the cells' new numbers, which keeps every neighbourhood's order.
 	-> dict points (N, 4), offsets (N + 1), nbr (E), edge (E, 4), attr (N, 20), sh, sh32, perm, inv, orig."""
-	n = len(points)
-	dev = points.device
+	n, dev = points.shape[0], points.device
 	raw = raw.clamp(max=30.0)
-	if eps_density > 0:
-		s_max2 = (torch.exp(2 * d_log_scale.clamp(-20, 20)) + scale_floor ** 2).amax(-1)
-		r2 = 2 * s_max2 * (raw - math.log(eps_density)).clamp_min(0) * (1 + 2 ** -9)
-	else:
-		r2 = torch.full_like(raw, float('inf'))
-	# smallest eigenvalue of the colour conic, rounded down before the half conversion
-	lam = 1.0 / (torch.exp(2 * c_log_scale.clamp(-20, 20)) + scale_floor ** 2).amax(-1)
-	lam = (lam * (1 - 2 ** -9)).clamp(max=65000.0)
-	cut = cut_bits(r2, lam)
-	off = offsets.long()
-	deg = off[1:] - off[:-1]
-	offsets_sf = off + torch.arange(n + 1, device=dev)
-	row = torch.repeat_interleave(torch.arange(n, device=dev), deg)
-	nbr = torch.empty(len(adj) + n, dtype=torch.long, device=dev)
-	nbr[offsets_sf[:-1]] = torch.arange(n, device=dev)
-	nbr[torch.arange(len(adj), device=dev) + row + 1] = adj.long()
-	edge = torch.cat([points[nbr], cut[nbr, None]], 1).contiguous()
-	pts4 = torch.cat([points, torch.zeros_like(raw)[:, None]], 1).contiguous()
-	z = torch.zeros_like(raw)[:, None]
-	attr = torch.cat([dA, raw[:, None], z, cA, z, z, z, z, z, z], 1).contiguous()
-	sh = sh.contiguous()
+	ids = torch.arange(n, device=dev)
+	deg = (offsets[1:] - offsets[:-1]).long()
+	cell = torch.cat([ids, torch.repeat_interleave(ids, deg)])  # selves first, then the CSR rows
+	member = torch.cat([ids, adj.long()])
+	order = torch.argsort(cell, stable=True)
+	cell, nbr = cell[order], member[order]
+	words = _cut_words(raw, d_log_scale, c_log_scale, scale_floor, eps_density)
+	edge = torch.cat([points[nbr], words[nbr].unsqueeze(1)], 1)
+	pts4 = F.pad(points, (0, 1))
+	attr = points.new_zeros(n, 20)
+	attr[:, 0:6], attr[:, 6], attr[:, 8:14] = dA, raw, cA
+	sizes = deg + 1
 	perm = inv = None
 	if reorder:
 		perm = morton_order(points)
 		inv = torch.empty_like(perm)
-		inv[perm] = torch.arange(n, device=dev)
-		size = (deg + 1)[perm]
-		new_off = torch.cat([torch.zeros_like(size[:1]), torch.cumsum(size, 0)])
-		cell = torch.repeat_interleave(torch.arange(n, device=dev), size)
-		old = offsets_sf[perm][cell] + torch.arange(len(nbr), device=dev) - new_off[cell]
-		offsets_sf, nbr, edge = new_off, inv[nbr[old]], edge[old].contiguous()
-		pts4, attr, sh = pts4[perm].contiguous(), attr[perm].contiguous(), sh[perm].contiguous()
-	return {'points': pts4, 'offsets': offsets_sf.int().contiguous(), 'nbr': nbr.int().contiguous(), 'edge': edge,
-			'attr': attr, 'sh': sh.half() if sh_half else sh, 'sh32': sh, 'perm': perm, 'inv': inv,
-			'orig': (perm if reorder else torch.empty(0, device=dev)).int().contiguous(), 'baked_center': None}
-
-
-@torch.no_grad()
-def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=False):
-	"""Records of the inference renderer (render.py:179-225): self-first neighbourhoods (offsets (N + 1), nbr
-	(E)) with one float4 per edge = (p_j, half2(r2_j, lam_j)), r2 the squared distance beyond which
-	rho_j G_j < eps_density (inf when eps_density = 0) and lam the smallest eigenvalue of the colour conic, both
-	rounded to the safe side; attr (N, 20) = (density conic, min(raw, 30), colour conic, baked rgb); sh in fp32
-	or fp16; reorder renumbers the sites along a Z-order curve (perm: new -> old, inv: old -> new). Built on the GPU
-	by vgr_pack_foam (the Z-order permutation by torch's sort); pack_foam_arrays is the same pack in torch."""
-	g = model.graph
-	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
-	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
-	n = len(g.points)
-	perm = inv = None
-	if reorder:
-		perm = morton_order(g.points)
-		inv = torch.empty_like(perm)
-		inv[perm] = torch.arange(n, device=perm.device)
-	sh = model.sh().detach().float().contiguous()
-	out = ext.pack_foam(g.points, g.offsets, g.adj, model.raw.detach().contiguous(),
-						model.d_log_scale.detach().contiguous(), model.c_log_scale.detach().contiguous(),
-						dA.detach().contiguous(), cA.detach().contiguous(), sh, perm, scale_floor, eps_density, sh_half)
-	return {'points': out['points'], 'offsets': out['offsets'], 'nbr': out['nbr'], 'edge': out['edge'],
-			'attr': out['attr'], 'sh': out['sh16'] if sh_half else out['sh32'], 'sh32': out['sh32'], 'perm': perm,
-			'inv': inv, 'orig': (perm if reorder else torch.empty(0, device=g.points.device)).int().contiguous(),
+		inv[perm] = ids
+		regroup = torch.argsort(inv[cell], stable=True)
+		nbr, edge = inv[nbr[regroup]], edge[regroup]
+		pts4, attr, sh, sizes = pts4[perm], attr[perm], sh[perm], sizes[perm]
+	offsets_sf = F.pad(torch.cumsum(sizes, 0), (1, 0))
+	sh = sh.contiguous()
+	return {'points': pts4.contiguous(), 'offsets': offsets_sf.int(), 'nbr': nbr.int().contiguous(),
+			'edge': edge.contiguous(), 'attr': attr.contiguous(), 'sh': sh.half() if sh_half else sh, 'sh32': sh,
+			'perm': perm, 'inv': inv, 'orig': (perm if reorder else torch.empty(0, device=dev)).int().contiguous(),
 			'baked_center': None}
 
 
 @torch.no_grad()
+def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=False):
+	"""The inference renderer's records for a field (render.py:179-225), built on the GPU by vgr_pack_foam (the
+	renumbering's Z-order sort by torch): self-first neighbourhoods (offsets (N + 1), nbr (E)), one float4 per
+	neighbourhood entry (p_j, half2(r2_j, lam_j)), attr (N, 20) = (density conic, min(raw, 30), colour conic,
+	baked rgb), sh in fp32 or fp16; reorder renumbers the sites along a Z-order curve (perm: new -> old, inv: old ->
+	new, orig: the tie order of the original numbering)."""
+	g = model.graph
+	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
+	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
+	perm = inv = None
+	if reorder:
+		perm = morton_order(g.points)
+		inv = torch.empty_like(perm)
+		inv[perm] = torch.arange(len(perm), device=perm.device)
+	out = ext.pack_foam(g.points, g.offsets, g.adj, *[t.detach().contiguous() for t in (
+		model.raw, model.d_log_scale, model.c_log_scale, dA, cA)], model.sh().detach().float().contiguous(), perm,
+		scale_floor, eps_density, sh_half)
+	empty = torch.empty(0, device=g.points.device)
+	return {'points': out['points'], 'offsets': out['offsets'], 'nbr': out['nbr'], 'edge': out['edge'],
+			'attr': out['attr'], 'sh': out['sh16'] if sh_half else out['sh32'], 'sh32': out['sh32'], 'perm': perm,
+			'inv': inv, 'orig': (empty if perm is None else perm).int().contiguous(), 'baked_center': None}
+
+
+@torch.no_grad()
 def bake_colors(model, pack, center):
-	"""Site colours max(SH_k(d_k) + 1/2, 0) for the view direction d_k from the camera center to site k
-	(render.py:228-235). Packed records on the GPU are baked by vgr_bake_colors; host packs by the torch ops."""
+	"""Bakes one view's site colours max(SH_k(d_k) + 1/2, 0), d_k the unit direction from `center` to site k, into
+	the packed records (attr[:, 16:19]) for the baked colour mode (render.py:228-235): vgr_bake_colors for packs on
+	the GPU, torch for host packs."""
 	if pack['attr'].is_cuda:
 		ext.bake_colors(pack['points'], pack['sh32'], model.sh_deg, center, pack['attr'])
-		pack['baked_center'] = center
-		return
-	points = model.graph.points if pack['perm'] is None else model.graph.points[pack['perm']]
-	dirs = torch.nn.functional.normalize(points - center.view(1, 3), dim=-1)
-	rgb = (sh_basis(dirs, model.sh_deg)[:, :, None] * pack['sh32']).sum(1).add_(0.5).clamp_min_(0.0)
-	pack['attr'][:, 16:19] = rgb
+	else:
+		sites = pack['points'][:, :3]
+		basis = sh_basis(F.normalize(sites - center.view(1, 3), dim=-1), model.sh_deg)
+		pack['attr'][:, 16:19] = torch.einsum('nj,njc->nc', basis, pack['sh32']).add(0.5).clamp_min(0.0)
 	pack['baked_center'] = center
+
+
+# ------------------------------------------------------------------------------------- inference renderer
+
+_COLOR_MODES = {'exact': 0, 'baked': 1, 'fused': 2}
 
 
 @torch.no_grad()
 def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, t_thresh=1e-4, w_thresh=1e-4,
 						   colors='exact', eps_color=0.0, stage=2, cap=None, trace_cap=0):
-	"""Rendering at the ray / Voronoi-face interaction points (render.py:238-257). colors='exact' evaluates the
-	SH in a second pass for the segments with weight > w_thresh, 'fused' blends them in the density pass, both
-	skipping neighbours whose normalised colour weight is below eps_color; 'baked' uses bake_colors. Per-ray
-	stats (B, 5): samples, segments with colour, walk steps, density Gaussians evaluated, SH evaluated.
-	trace_cap > 0 adds 'trace' (B, trace_cap): the cell of every sample in original numbering."""
-	near_t, _, far_t = ray_bounds(o, d, near, far_radius)
-	cap = torch.empty(0, dtype=torch.int32, device=o.device) if cap is None else cap.int().contiguous()
+	"""Rendering at the ray / Voronoi-face crossings with the packed records, one vgr_foam_infer launch
+	(render.py:238-257). colors: 'exact' (SH evaluated in a second pass for segments of weight > w_thresh),
+	'fused' (blended in the density pass) or 'baked' (bake_colors); eps_color > 0 skips colour terms of relative
+	weight below it. start: sites in the model's numbering. -> dict rgb (with the background), acc, depth, stats
+	(B, 5): samples, coloured segments, walk steps, density terms, SH evaluations; with trace_cap > 0 also trace
+	(B, trace_cap), each sample's cell in the model's numbering."""
+	t_near, _, t_far = ray_bounds(o, d, near, far_radius)
 	if pack['inv'] is not None:
 		start = pack['inv'][start.long()]
-	color_cut = 2 * math.log(1 / eps_color) if eps_color > 0 else float('inf')
+	empty = torch.empty(0, dtype=torch.int32, device=o.device)
 	out = ext.foam_infer_extension().foam_infer(
 		pack['points'], pack['offsets'], pack['nbr'], pack['edge'], pack['attr'], pack['sh'], model.sh_deg,
-		o.float().contiguous(), d.float().contiguous(), start.int().contiguous(), near_t.contiguous(),
-		far_t.contiguous(), float(t_thresh), float(w_thresh), color_cut, {'exact': 0, 'baked': 1, 'fused': 2}[colors],
-		int(stage), cap, pack['orig'], trace_cap=trace_cap)
+		o.float().contiguous(), d.float().contiguous(), start.int().contiguous(), t_near.contiguous(),
+		t_far.contiguous(), float(t_thresh), float(w_thresh), 2 * math.log(1 / eps_color) if eps_color > 0 else math.inf,
+		_COLOR_MODES[colors], int(stage), empty if cap is None else cap.int().contiguous(), pack['orig'],
+		trace_cap=trace_cap)
 	fg, T, depth, stats = out[:4]
-	rgb = fg + T[:, None] * torch.sigmoid(model.bg_logit)
-	res = {'rgb': rgb, 'acc': 1.0 - T, 'depth': depth, 'stats': stats}
+	res = {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth, 'stats': stats}
 	if trace_cap > 0:
 		res['trace'] = out[4]
 	return res
@@ -315,9 +359,10 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 
 @torch.no_grad()
 def render_image(model, scene, i, start, chunk=8192, renderer=render_rays, **kw):
-	"""Renders view i of a scene exposing image_rays(i) -> (o, d, gt), in chunks (render.py:260-266)."""
+	"""View i of a scene with image_rays(i) -> (o, d, gt), rendered `chunk` rays at a time from the start site
+	`start` -> (image (H, W, 3) clamped to [0, 1], gt) (render.py:260-266)."""
 	o, d, gt = scene.image_rays(i)
-	start = torch.full((len(o),), int(start), dtype=torch.int32, device=o.device)
-	out = [renderer(model, o[j:j + chunk], d[j:j + chunk], start[j:j + chunk], perturb=False, **kw)['rgb']
-		   for j in range(0, len(o), chunk)]
-	return torch.cat(out).view(scene.H, scene.W, 3).clamp(0, 1), gt
+	starts = torch.full((o.shape[0],), int(start), dtype=torch.int32, device=o.device)
+	parts = [renderer(model, o[a:a + chunk], d[a:a + chunk], starts[a:a + chunk], perturb=False, **kw)['rgb']
+			 for a in range(0, o.shape[0], chunk)]
+	return torch.cat(parts).view(scene.H, scene.W, 3).clamp(0, 1), gt

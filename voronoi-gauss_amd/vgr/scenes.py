@@ -292,3 +292,22 @@ def site_points(config, scale=1.0):
 	n = max(64, int(round(SITE_COUNTS[config] * scale)))
 	p, _ = _geometry(config, n, np.random.default_rng(SEEDS[config]))
 	return p.astype(np.float32)
+
+
+def _main(argv=None):
+	"""`python -m vgr.scenes --geometry C [C ...] [--cache DIR]`: triangulates the seeded site clouds of the given
+	configurations at their full site counts and stores them in the geometry cache (what make_scene then loads)."""
+	import argparse
+	ap = argparse.ArgumentParser(description=_main.__doc__)
+	ap.add_argument('--geometry', type=int, nargs='+', required=True, choices=sorted(SITE_COUNTS))
+	ap.add_argument('--cache', default=DEFAULT_CACHE)
+	a = ap.parse_args(argv)
+	for c in a.geometry:
+		t0 = time.time()
+		pts, _, adj, _ = load_geometry(c, cache_dir=a.cache, log=lambda *m: print(*m, flush=True))
+		print(f'[scene] config {c}: {len(pts)} sites, {len(adj)} adjacency entries, cached in {time.time() - t0:.1f} s',
+			  flush=True)
+
+
+if __name__ == '__main__':
+	_main()

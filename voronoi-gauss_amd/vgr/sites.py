@@ -8,19 +8,19 @@ import numpy as np
 from scipy.spatial import Delaunay, cKDTree
 
 
-def delaunay_graph(points):
-	"""-> (points kept, index of the kept points, CSR offsets (N + 1), adjacency (M)), int32. Points left out of
-	the triangulation by Qhull (coplanar / nearly coincident) are dropped and the triangulation rebuilt, up to
-	three times (sites.py:24-35)."""
-	idx = np.arange(len(points))
-	for _ in range(3):
-		tri = Delaunay(points[idx])
-		offsets, adj = tri.vertex_neighbor_vertices
-		alone = np.diff(offsets) == 0
-		if not alone.any():
-			return points[idx], idx, offsets.astype(np.int32), adj.astype(np.int32)
-		idx = idx[~alone]
-	raise RuntimeError('Delaunay triangulation keeps dropping points')
+def delaunay_graph(points, attempts=3):
+	"""Delaunay neighbours of the points as int32 CSR -> (kept points, their indices into `points`, offsets
+	(N + 1), adjacency (M)). Qhull leaves some points out of the triangulation (duplicates, near-coincident
+	points); such points have no neighbours, so they are removed and the rest triangulated again, at most
+	`attempts` times in all, the rule of the reference's sites.py:24-35."""
+	kept = np.arange(len(points))
+	for _ in range(attempts):
+		offsets, adj = Delaunay(points[kept]).vertex_neighbor_vertices
+		isolated = offsets[1:] == offsets[:-1]
+		if not isolated.any():
+			return points[kept], kept, offsets.astype(np.int32), adj.astype(np.int32)
+		kept = kept[~isolated]
+	raise RuntimeError(f'Qhull still leaves points without neighbours after {attempts} triangulations')
 
 
 def nearest_sites(points, queries):
