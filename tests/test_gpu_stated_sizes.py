@@ -14,7 +14,9 @@ deterministic subset of those rays (every k-th ray) on the host:
 Config 5 also runs march_forward on all 16,777,216 rays in the default layout (one ray per lane at this size),
 checked on every k-th ray (values within 1e-4, walked sites bit-exact), and march_backward on 524,288 of its rays
 (the smallest batch that takes the one-ray-per-lane layout), with upstream gradients on every 256th ray only, so
-that the oracle's backward over those rays gives the same gradients (relative error 2e-5).
+that the oracle's backward over those rays gives the same gradients (relative errors: 2e-5 for the density gradients
+with the thresholds off, 2e-4 for the colour gradients, whose sample weights 1 - exp(-sigma delta) keep few digits
+in fp32 at config 5's densities; see the test).
 
 VGR_STATED_CONFIGS=2,3 (say) restricts the configurations."""
 
@@ -206,9 +208,22 @@ def test_march_config5_full_batch(gpu, config5_field):
 	np.testing.assert_array_equal(tr, rt['trace'])
 
 
-def test_march_backward_config5_default_layout(gpu, config5_field):
+OFF_BARS = {'raw': 2e-5, 'dA': 2e-5, 'cA': 2e-4, 'sh': 2e-4}
+ON_BARS = {'raw': 1e-4, 'dA': 1e-4, 'cA': 2e-4, 'sh': 2e-4}
+
+
+@pytest.mark.parametrize('t_thresh,w_thresh,bars', [(0.0, -1.0, OFF_BARS), (1e-4, 1e-4, ON_BARS)])
+def test_march_backward_config5_default_layout(gpu, config5_field, t_thresh, w_thresh, bars):
 	"""march_backward over 524,288 rays of config 5 (one ray per lane, the default at this size, forward and
-	backward) with upstream gradients on every 256th ray: against the oracle's backward over those rays."""
+	backward) with upstream gradients on every 256th ray: against the oracle's backward over those rays.
+
+	Bars (relative error, vector norm), thresholds off: density gradients (raw, dA) 2e-5, what fp32 atomics against
+	sequential sums leave. Colour gradients (cA, sh) 2e-4: they scale with each sample's weight w = T (1 - exp(-s d)),
+	and config 5's sigma delta is about 1e-4, where 1 - exp(-x) (the reference's formula, march.cu:241) keeps only
+	about 3 significant digits in fp32, so the ulp by which the device exp and the host's libm exp differ moves w by
+	up to 6e-4 relative per sample (measured: about 5e-5 over the batch, the same in both GPU layouts, which agree
+	with each other to 1.5e-6). Thresholds on: also a few samples whose weight is within ulps of w_thresh are
+	coloured on one side only, 1e-4 for the density gradients."""
 	sc, model, dA, cA, rays, host, dt, n_bg = config5_field
 	B = 524288
 	sub = tuple(np.ascontiguousarray(a[:B]) for a in rays)
@@ -217,7 +232,7 @@ def test_march_backward_config5_default_layout(gpu, config5_field):
 	sh = model.sh().detach().contiguous()
 	fx = ext.march_extension()
 	rgb, T, _, _ = fx.march_forward(g.points, g.offsets, g.adj, model.raw.detach(), dA, cA, sh, sc.sh_deg, *rt, dt,
-									n_bg, 1e-4, 1e-4)
+									n_bg, t_thresh, w_thresh)
 	rng = np.random.default_rng(11)
 	g_rgb = np.zeros((B, 3), np.float32)
 	g_T = np.zeros(B, np.float32)
@@ -225,13 +240,14 @@ def test_march_backward_config5_default_layout(gpu, config5_field):
 	g_rgb[hot] = rng.normal(size=(len(hot), 3))
 	g_T[hot] = rng.normal(size=len(hot))
 	got = fx.march_backward(g.points, g.offsets, g.adj, model.raw.detach(), dA, cA, sh, sc.sh_deg, *rt, dt, n_bg,
-							1e-4, 1e-4, rgb, T, torch.as_tensor(g_rgb, device=gpu), torch.as_tensor(g_T, device=gpu))
+							t_thresh, w_thresh, rgb, T, torch.as_tensor(g_rgb, device=gpu),
+							torch.as_tensor(g_T, device=gpu))
 	torch.cuda.synchronize()
 	ref = oracle.march_backward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
 								host['sh'], sc.sh_deg, *[a[hot] for a in sub], dt, n_bg, rgb.cpu().numpy()[hot],
-								T.cpu().numpy()[hot], g_rgb[hot], g_T[hot])
+								T.cpu().numpy()[hot], g_rgb[hot], g_T[hot], t_thresh, w_thresh)
 	errs = {name: rel(a.cpu().numpy(), r) for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref)}
-	print(f'\n[stated sizes] config 5 march backward, {B} rays, {len(hot)} with gradients: relative errors {errs}',
-		  flush=True)
+	print(f'\n[stated sizes] config 5 march backward (t_thresh {t_thresh}, w_thresh {w_thresh}), {B} rays, '
+		  f'{len(hot)} with gradients: relative errors {errs}', flush=True)
 	for name, e in errs.items():
-		assert e < 2e-5, name
+		assert e < bars[name], name

@@ -30,7 +30,7 @@ def nearest_sites(points, queries):
 	if getattr(points, 'is_cuda', False):
 		from .grid import SiteGrid
 		return SiteGrid(points.contiguous()).nearest(queries.contiguous())
-	return cKDTree(points).query(queries)[1].astype(np.int32)
+	return cKDTree(points).query(queries, workers=-1)[1].astype(np.int32)
 
 
 def neighbor_spacing(points, k=3):
