@@ -316,6 +316,20 @@ int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const f
                    const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work, void* stream);
 
 /*
+ * vgr_grid_build without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The scratch
+ * (the cell of every site, the per-cell counters, the scan's tile sums) is a static device array of
+ * VGR_GRID_NOALLOC_MAX_WORK ints (64 MiB), one per GPU, held until the process ends; a build needing more than
+ * that (vgr_grid_work_size(N, G) > VGR_GRID_NOALLOC_MAX_WORK) is rejected with VGR_ERR_INVALID. It calls no
+ * hipMalloc/hipFree and clears its counters with a kernel. Every call on one GPU uses that GPU's one array: calls
+ * that overlap on a GPU (other streams, other host threads) race and must be serialised by the caller. The device
+ * current on the calling thread must be the stream's. Same arguments and outputs as vgr_grid_build otherwise.
+ */
+#define VGR_GRID_NOALLOC_MAX_WORK (1LL << 24)
+int vgr_grid_build_noalloc(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+                           const int32_t* res, int32_t* cell_start, int32_t* cell_sites, void* stream);
+
+/*
  * Nearest site of every query point: the lexicographic argmin of (float64 squared distance, site index), as
  * cKDTree (float64) answers it up to exact distance ties.
  *   queries f32 (m, 3) -> site i32 (m); the grid arguments as built by vgr_grid_build

@@ -6,6 +6,8 @@
 // rings of grid cells around its own cell until no unscanned cell can hold a closer site. Distances are computed in
 // float64, as cKDTree computes them, and ties go to the smaller site index, so the answer is cKDTree's except
 // where two sites are at exactly the same float64 distance.
+#include <mutex>
+
 #include "vgr_abi.h"
 #include "vgr_device.h"
 #include "vgr_scan.h"
@@ -50,6 +52,42 @@ __global__ void __launch_bounds__(kBlock) grid_fill(int64_t n, const int* __rest
     const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n) return;
     cell_sites[atomicAdd(cursor + cell_of[i], 1)] = static_cast<int>(i);
+}
+
+// Fills n ints with zero (the counters of a build; a kernel rather than hipMemsetAsync, so that a build is made of
+// kernel launches only).
+__global__ void __launch_bounds__(kBlock) zero_ints(int* __restrict__ a, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i < n) a[i] = 0;
+}
+
+// Scratch of vgr_grid_build_noalloc: 2^24 ints (64 MiB), enough for vgr_grid_work_size of 8M sites over 4M cells
+// (the largest benchmark scene at two sites per cell is 12M ints). Each GPU that runs the library holds its own copy
+// until the process ends. Host code never passes `scratch` itself to a kernel (in host code the name is only a
+// stand-in for the symbol); it uses the device address from hipGetSymbolAddress, one per device.
+constexpr int64_t kScratchInts = VGR_GRID_NOALLOC_MAX_WORK;
+static __device__ __align__(256) int scratch[kScratchInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up on the first call on each device (with that device current).
+int scratch_on_current_device(int** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return launch_status("grid_build_noalloc: hipGetDevice");
+    VGR_REQUIRE(dev >= 0 && dev < kMaxDevices, "grid_build_noalloc: device %d beyond the %d supported", dev,
+                kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess)
+            return fail(VGR_ERR_LAUNCH, "grid_build_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+        g_scratch_ptr[dev] = static_cast<int*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return VGR_OK;
 }
 
 // Nearest site of each query: lexicographic argmin of (float64 squared distance, site index).
@@ -159,10 +197,15 @@ extern "C" int64_t vgr_grid_work_size(int64_t n_sites, int64_t n_cells) {
     return n_sites + n_cells + tiles + 1;
 }
 
-extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
-                              const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work,
-                              void* stream) {
-    using namespace vgr;
+namespace vgr {
+namespace {
+
+// Counting sort of the sites into the grid's cells, with `work` (vgr_grid_work_size ints) for the cell of every
+// site, the per-cell counters (then fill cursors) and the scan's tile sums. zero_by_kernel: clear the counters with
+// a kernel (the no-alloc entry point) rather than hipMemsetAsync.
+int grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+               const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work, bool zero_by_kernel,
+               void* stream) {
     int64_t n_cells = 0;
     if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
     VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "grid_build: n_sites must be in [0, 2^31) (got %lld)",
@@ -174,7 +217,12 @@ extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stri
     int* cell_of = work;
     int* count = work + n_sites;
     int* tile_sum = count + n_cells;
-    if (hipMemsetAsync(count, 0, sizeof(int) * n_cells, s) != hipSuccess) return launch_status("grid_build memset");
+    if (zero_by_kernel) {
+        hipLaunchKernelGGL(zero_ints, dim3(grid_for(n_cells, kBlock)), dim3(kBlock), 0, s, count, n_cells);
+        if (int rc = launch_status("grid_build zero_ints")) return rc;
+    } else if (hipMemsetAsync(count, 0, sizeof(int) * n_cells, s) != hipSuccess) {
+        return launch_status("grid_build memset");
+    }
     if (n_sites > 0) {
         hipLaunchKernelGGL(grid_count, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, s, points, int(stride),
                            n_sites, g, cell_of, count);
@@ -188,6 +236,34 @@ extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stri
         return launch_status("grid_fill");
     }
     return VGR_OK;
+}
+
+}  // namespace
+}  // namespace vgr
+
+extern "C" int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
+                              const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work,
+                              void* stream) {
+    return vgr::grid_build(points, n_sites, stride, lo, cell, res, cell_start, cell_sites, work, false, stream);
+}
+
+extern "C" int vgr_grid_build_noalloc(const float* points, int64_t n_sites, int32_t stride, const float* lo,
+                                      const float* cell, const int32_t* res, int32_t* cell_start,
+                                      int32_t* cell_sites, void* stream) {
+    using namespace vgr;
+    int64_t n_cells = 0;
+    if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
+    VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "grid_build_noalloc: n_sites must be in [0, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    const int64_t need = vgr_grid_work_size(n_sites, n_cells);
+    VGR_REQUIRE(need <= kScratchInts,
+                "grid_build_noalloc: %lld sites over %lld cells need %lld scratch ints, beyond the static %lld; use "
+                "vgr_grid_build with a workspace",
+                static_cast<long long>(n_sites), static_cast<long long>(n_cells), static_cast<long long>(need),
+                static_cast<long long>(kScratchInts));
+    int* work = nullptr;
+    if (int rc = scratch_on_current_device(&work)) return rc;
+    return grid_build(points, n_sites, stride, lo, cell, res, cell_start, cell_sites, work, true, stream);
 }
 
 extern "C" int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t stride, const float* lo,

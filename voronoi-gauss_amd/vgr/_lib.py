@@ -56,12 +56,13 @@ SIGNATURES = {
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
+	'vgr_grid_build_noalloc': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P],
 	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
 	'vgr_abi_version': [],
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 19
+ABI_VERSION = 20
 _lib = None
 
 
