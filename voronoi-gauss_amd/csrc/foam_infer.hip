@@ -147,20 +147,22 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
 // ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
 // Colour blocks of site k for this ray come through the wave-shared LDS cache of SH coefficient blocks: SLOTS
-// direct-mapped slots (site k mod SLOTS), stored [12][SLOTS] float4 so that lanes reading different slots hit
-// different banks. The 64 rays of a tile read overlapping sets of sites (45 % of the lookups find their block in
-// LDS on the config-3 scene with 48 slots); the colour itself, max(SH_k(d) + 1/2, 0), is evaluated per lane since
-// it depends on the ray direction. n_sh counts the SH evaluations, i.e. every colour lookup.
+// direct-mapped slots (site k mod SLOTS) plus `overflow` blocks used within one lookup, stored [12][blocks] float4
+// so that lanes reading different slots hit different banks. The 64 rays of a tile read overlapping sets of sites
+// (45 % of the lookups find their block in LDS on the config-3 scene); the colour itself, max(SH_k(d) + 1/2, 0), is
+// evaluated per lane since it depends on the ray direction. n_sh counts the SH evaluations, i.e. every colour
+// lookup.
 //
-// Tuning per colour mode, measured on config 3. Fused and baked colours: 30 slots (6.0 KB of LDS per wave), so that
-// 24 waves (6 per SIMD) fit in a CU's 160 KB, and no software pipelining: the registers that pipelined loads hold
-// are worth more as a sixth wave, whose loads cover the latency instead (48 slots at 4 waves, 36 at 5 and 26 at 7
-// were all slower: 233, 216 and 257 ms against 207). Lazy colours take 36 slots, 5 waves and the pipelined loops
-// (edge records two edges ahead, site records one ahead): 276 ms, against 287 at 4 waves and 48 slots, 305 with
-// the fused tuning and 330 at 5 waves without pipelining.
+// Tuning per colour mode, measured on config 3. Fused and baked colours: 24 slots and 4 overflow blocks (5.8 KB of
+// LDS per wave), so that 24 waves (6 per SIMD) fit in a CU's 160 KB, and no software pipelining: the registers that
+// pipelined loads hold are worth more as a sixth wave, whose loads cover the latency instead (48 slots at 4 waves,
+// 36 at 5 and 26 at 7 were all slower: 233, 216 and 257 ms against 207 without overflow blocks). Lazy colours take
+// 36 slots and no overflow blocks at 5 waves and the pipelined loops (edge records two edges ahead, site records one
+// ahead).
 template <int COLOR>
 struct Tune {
-    static constexpr int slots = COLOR == kLazy ? 36 : 30;
+    static constexpr int slots = COLOR == kLazy ? 36 : 24;
+    static constexpr int overflow = COLOR == kLazy ? 0 : 4;
     static constexpr int waves = COLOR == kLazy ? 5 : 6;
     static constexpr bool pipelined = COLOR == kLazy;
 };
@@ -174,28 +176,37 @@ __device__ __forceinline__ int slot_of(int k) {
 // they would be flat accesses, after each of which the wave waits for all of its outstanding global loads.
 typedef __attribute__((address_space(3))) volatile int lds_int;
 
-template <int SLOTS>
+// The cache of one wave for colour mode COLOR (Tune<COLOR>: `slots` cached slots and `overflow` blocks).
+template <int COLOR>
 struct ColorCache {
-    float4* data;    // [12][SLOTS] coefficient blocks
+    float4* data;    // [12][slots + overflow] coefficient blocks: the cached slots, then the overflow blocks
     lds_int* tag;    // site held by each slot (-1: empty)
     lds_int* claim;  // election word of each slot
-    lds_int* req;    // sites being fetched in the current fill
+    lds_int* ovf_k;  // per slot, in the current lookup: the site its losers' leader fetches into an overflow block
+    lds_int* ovf_b;  // ... and that block (-1: none)
+    lds_int* req_k;  // sites fetched by the current fill ...
+    lds_int* req_b;  // ... and their blocks
 };
 
-// LDS footprint per block of the colour cache, in float4 units (tag, claim and request arrays follow the blocks).
-template <int SLOTS>
+// LDS footprint per block of the colour cache, in float4 units (the words follow the coefficient blocks).
+template <int COLOR>
 constexpr int cache_vec4(bool sh) {
-    return sh ? 12 * SLOTS + (3 * SLOTS + 3) / 4 : 1;
+    constexpr int S = Tune<COLOR>::slots, O = Tune<COLOR>::overflow;
+    return sh ? 12 * (S + O) + (2 * S + (O > 0 ? 2 * S : 0) + 2 * (S + O) + 3) / 4 : 1;
 }
 
-template <int SLOTS>
-__device__ __forceinline__ ColorCache<SLOTS> make_cache(float4* lds) {
-    ColorCache<SLOTS> C;
+template <int COLOR>
+__device__ __forceinline__ ColorCache<COLOR> make_cache(float4* lds) {
+    constexpr int S = Tune<COLOR>::slots, O = Tune<COLOR>::overflow;
+    ColorCache<COLOR> C;
     C.data = lds;
-    C.tag = (lds_int*)(lds + 12 * SLOTS);
-    C.claim = C.tag + SLOTS;
-    C.req = C.claim + SLOTS;
-    for (int i = threadIdx.x; i < SLOTS; i += kBlock) C.tag[i] = -1, C.claim[i] = -1, C.req[i] = 0;
+    C.tag = (lds_int*)(lds + 12 * (S + O));
+    C.claim = C.tag + S;
+    C.ovf_k = C.claim + S;
+    C.ovf_b = C.ovf_k + (O > 0 ? S : 0);
+    C.req_k = C.ovf_b + (O > 0 ? S : 0);
+    C.req_b = C.req_k + S + O;
+    for (int i = threadIdx.x; i < S; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
     __syncthreads();
     return C;
 }
@@ -209,50 +220,77 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // max(SH_k(d) + 1/2, 0) for every active lane (the lanes that need a colour now; control flow is uniform across
 // them), site k's coefficient block read through the wave cache.
 //
-// The texture path and LDS charge a wave-wide load the same cycles however few of its lanes are active, so the
-// fetch keeps load instructions per round low, and it keeps registers low (a block is read and multiplied four
-// float4 at a time) so that four waves fit on each SIMD. Each pass: lanes whose site is cached pin their slot; the
-// missing sites get one elected lane per unpinned slot and are fetched by all active lanes together (one float4 per
-// lane per load, about five blocks per instruction); then every lane whose block is now in LDS reads it and
-// evaluates its colour. Lanes whose slot was pinned by, or went to, another site wait for the next pass; every pass
-// serves at least one slot, so the loop ends (usually after one pass, two in about a third of the rounds).
-template <bool HALF, int NV, int SLOTS>
-__device__ __forceinline__ void cached_colour(ColorCache<SLOTS>& C, const float4* __restrict__ sh, int k,
+// The texture path and LDS charge a wave-wide load the same cycles however few of its lanes are active, and the
+// evaluation (12 LDS reads, 48 FMAs) costs the wave the same however few of its lanes take part, so a lookup aims
+// to serve every lane in one pass. Each pass:
+// - lanes whose site is in its home slot (k mod SLOTS) pin it; the missing sites claim their home slots, the last
+//   claim wins and tags the slot at once (the cache belongs to this wave, which reads a block only after the fill),
+//   and lanes of the winner's site join it;
+// - lanes whose home slot is pinned by, or went to, another site elect one leader per slot; the first `overflow`
+//   leaders' sites get overflow blocks, which serve their lanes in this pass and are not cached;
+// - all active lanes fetch the claimed blocks together (one float4 per lane per load), then every served lane reads
+//   its block, four float4 at a time, multiplying as it goes.
+// Lanes left over (more conflicts than overflow blocks, or a second site in one slot's losers) take another pass;
+// every pass serves at least one lane, so the loop ends (after the first pass in about 4 lookups of 5 on config 3).
+// Wave barriers separate the phases: the lanes of a phase act on what every lane did in the phase before, and the
+// barrier is convergent, so the compiler cannot merge one-sided stores across it.
+template <bool HALF, int NV, int COLOR>
+__device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4* __restrict__ sh, int k,
                                               const float (&b)[16], float (&c)[3]) {
+    constexpr int SLOTS = Tune<COLOR>::slots, OVF = Tune<COLOR>::overflow, BLOCKS = SLOTS + OVF;
     const int lane = static_cast<int>(threadIdx.x);
-    const int slot = slot_of<SLOTS>(k);
+    const int home = slot_of<SLOTS>(k);
     const uint64_t active = __ballot(1);
     const int n_active = __popcll(active), rank = lanes_below(active);
     bool pending = true;
     for (;;) {
-        // The phases are separated by wave barriers: the lanes of a phase act on what every lane did in the phase
-        // before. The barrier is convergent, so the compiler cannot fold two one-sided stores into an if/else and
-        // run the claim read-back (on one side) before the pin (on the other), as it may for independent threads.
-        const bool hit = pending && C.tag[slot] == k;
+        const bool hit = pending && C.tag[home] == k;
         const bool miss = pending && !hit;
-        if (miss) C.claim[slot] = lane;
+        if (miss) C.claim[home] = lane;
         __builtin_amdgcn_wave_barrier();
-        if (hit) C.claim[slot] = -1;  // pin, after the claims
+        if (hit) C.claim[home] = -1;  // pin, after the claims
         __builtin_amdgcn_wave_barrier();
-        const bool win = miss && C.claim[slot] == lane;
-        const uint64_t wins = __ballot(win);
-        if (wins != 0) {
-            if (win) C.req[lanes_below(wins)] = k;
+        const bool win = miss && C.claim[home] == lane;
+        if (win) C.tag[home] = k;
+        __builtin_amdgcn_wave_barrier();
+        const bool lose = miss && !win && C.tag[home] != k;  // the slot holds another site in this lookup
+        int block = home;
+        bool served = hit || (miss && !lose), lead_fetch = false;
+        if (OVF > 0 && __ballot(lose) != 0) {
+            if (lose) C.claim[home] = lane;
             __builtin_amdgcn_wave_barrier();
-            const int total = NV * __popcll(wins);
+            const bool lead = lose && C.claim[home] == lane;
+            const uint64_t leads = __ballot(lead);
+            if (lead) {
+                const int o = lanes_below(leads);
+                lead_fetch = o < OVF;
+                C.ovf_k[home] = k, C.ovf_b[home] = lead_fetch ? SLOTS + o : -1;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lose) {
+                const int ok = C.ovf_k[home], ob = C.ovf_b[home];
+                if (ok == k && ob >= 0) block = ob, served = true;
+            }
+        }
+        const bool fetch = win || lead_fetch;
+        const uint64_t fetches = __ballot(fetch);
+        if (fetches != 0) {
+            if (fetch) {
+                const int r = lanes_below(fetches);
+                C.req_k[r] = k, C.req_b[r] = block;
+            }
+            __builtin_amdgcn_wave_barrier();
+            const int total = NV * __popcll(fetches);
             for (int base = 0; base < total; base += n_active) {
                 const int j = base + rank;
                 if (j < total) {
                     const int r = j / NV, q = j - r * NV;
-                    const int kr = C.req[r];
-                    C.data[q * SLOTS + slot_of<SLOTS>(kr)] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
+                    const int kr = C.req_k[r];
+                    C.data[q * BLOCKS + C.req_b[r]] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
                 }
             }
-            __builtin_amdgcn_wave_barrier();  // publish the tags after the blocks
-            if (win) C.tag[slot] = k;
             __builtin_amdgcn_wave_barrier();
         }
-        const bool served = hit || (miss && C.tag[slot] == k);
         if (served) {
             c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
@@ -260,7 +298,7 @@ __device__ __forceinline__ void cached_colour(ColorCache<SLOTS>& C, const float4
                 float4 f[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
-                    if (q0 + u < NV) f[u] = C.data[(q0 + u) * SLOTS + slot];
+                    if (q0 + u < NV) f[u] = C.data[(q0 + u) * BLOCKS + block];
                 sh_accumulate<HALF>(f, q0, NV, b, c);
                 __builtin_amdgcn_sched_barrier(0);  // one chunk of the block in registers at a time
             }
@@ -341,7 +379,7 @@ __device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
 // indices clamped to the cell so every load stays in bounds.
 template <int STAGE, int COLOR, bool HALF, int DEG>
 __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
-                          const float (&d)[3], const float (&b)[16], ColorCache<Tune<COLOR>::slots>& cache,
+                          const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
                           bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
     const float4 pc = S.points[c];
@@ -413,7 +451,7 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
 // pipelined as eval_cell is).
 template <bool HALF, int DEG>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
-                           const float (&d)[3], const float (&b)[16], ColorCache<Tune<kLazy>::slots>& cache,
+                           const float (&d)[3], const float (&b)[16], ColorCache<kLazy>& cache,
                            float (&C)[3], int& n_sh) {
     float x[3];
     sample_point(o, d, t, x);
@@ -472,10 +510,9 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    constexpr int SLOTS = Tune<COLOR>::slots;
-    __shared__ float4 cache_lds[cache_vec4<SLOTS>(kSH)];
-    ColorCache<SLOTS> cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache<SLOTS>(cache_lds);
+    __shared__ float4 cache_lds[cache_vec4<COLOR>(kSH)];
+    ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache<COLOR>(cache_lds);
     const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
     if (r >= R.n) return;
     const int start = R.start[r];
@@ -660,7 +697,7 @@ __device__ int walk_group(const FoamScene& S, int c, int g, float x0, float x1, 
 // eval_cell for lane g of a group: the lane's share of the neighbourhood, then the group reductions.
 template <int STAGE, int COLOR, bool HALF, int DEG, int G>
 __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, const float (&o)[3],
-                                const float (&d)[3], const float (&b)[16], ColorCache<Tune<COLOR>::slots>& cache,
+                                const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
                                 bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
     const float4 pc = S.points[c];
@@ -725,7 +762,7 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
 template <bool HALF, int DEG, int G>
 __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, float mmin,
                                  const float (&o)[3], const float (&d)[3], const float (&b)[16],
-                                 ColorCache<Tune<kLazy>::slots>& cache, float (&C)[3], int& n_sh) {
+                                 ColorCache<kLazy>& cache, float (&C)[3], int& n_sh) {
     float x[3];
     sample_point(o, d, t, x);
     const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
@@ -759,10 +796,9 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     foam_group_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    constexpr int SLOTS = Tune<COLOR>::slots;
-    __shared__ float4 cache_lds[cache_vec4<SLOTS>(kSH)];
-    ColorCache<SLOTS> cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache<SLOTS>(cache_lds);
+    __shared__ float4 cache_lds[cache_vec4<COLOR>(kSH)];
+    ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
+    if (kSH) cache = make_cache<COLOR>(cache_lds);
     const int g = static_cast<int>(threadIdx.x) % G;
     const int64_t r = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
     if (r >= R.n) return;  // whole groups leave together
