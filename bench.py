@@ -189,6 +189,11 @@ def main():
 						 '1 or 16; default: the library default')
 	ap.add_argument('--lanes', type=int, default=4, choices=[4, 8, 16],
 					help='traverse workload: lanes per ray of the layout the JSON line reports')
+	ap.add_argument('--order', default='auto', choices=['auto', 'on', 'off'],
+					help='trace the rays in the coherent order of vgr_ray_order, computed inside the timed step (auto: '
+						 'on for the incoherent ray batch of config 5, off for camera rays in pixel tiles)')
+	ap.add_argument('--order-dir-res', type=int, default=None, help='direction bins per side of the octahedral map')
+	ap.add_argument('--order-pos-bits', type=int, default=None, help='Z-order bits per axis of the ray origins')
 	ap.add_argument('--workload', default='foam',
 					choices=['foam', 'march', 'locate', 'field', 'grad', 'pack', 'traverse', 'march-grad',
 							 'foam-grad'],
@@ -251,10 +256,17 @@ def bench_foam(args):
 	empty = torch.empty(0, dtype=torch.int32, device=dev)
 	fi = ext.foam_infer_extension()
 
+	ordered = args.order == 'on' or (args.order == 'auto' and not sc.cameras)
+	dir_res, pos_bits = args.order_dir_res or 8, args.order_pos_bits or 7
+	# camera rays in 8x8 tiles: the library's default layout (one ray per lane; 4 lanes per ray for exact colours);
+	# an incoherent batch in coherence order: 8 lanes per ray, the fastest layout on config 5 for every colour mode
+	lanes = args.lanes_per_ray or (8 if ordered else (4 if args.colors == 'exact' else 1))
+
 	def launch(p, sel, m=mode, cut=color_cut):
+		order = ext.ray_order(o[sel], d[sel], dir_res, pos_bits) if ordered else None
 		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
 							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'],
-							 lanes=args.lanes_per_ray)
+							 lanes=lanes, order=order)
 
 	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
 		per = B // frames
@@ -310,7 +322,9 @@ def bench_foam(args):
 		log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
 	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
 	st = stats.double()
-	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}'
+	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}-l{lanes}'
+	if ordered:
+		key += f'-order{dir_res}x{pos_bits}'
 	if fast:
 		key += f'-sh{"16" if args.sh_half else "32"}-ec{args.eps_color:g}-ed{args.eps_density:g}'
 	src = source_hash('foam_infer.hip')
@@ -319,8 +333,7 @@ def bench_foam(args):
 							'cache-oblivious gather bytes from the per-ray counters: 56 B per ray + 24 B per sample + '
 							'84 B per neighbourhood edge + SH bytes per distinct blended site (counts every L1/L2/LDS '
 							'hit as a fetch, so it can exceed the HBM peak)',
-							'foam_infer_kernel' if (args.lanes_per_ray or (4 if args.colors == 'exact' else 1)) == 1
-							else 'foam_group_kernel')
+							'foam_infer_kernel' if lanes == 1 else 'foam_group_kernel')
 
 	cpu = None
 	if args.cpu_seconds > 0 and args.colors != 'baked':
@@ -340,9 +353,11 @@ def bench_foam(args):
 			'sites': sc.n_sites, 'rays_per_step': B, 'frames_per_step': frames,
 			'fps_1080p': round(frames / (ms * 1e-3), 2) if frames else None,
 			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
-			'lanes_per_ray': args.lanes_per_ray or (4 if args.colors == 'exact' else 1),
+			'lanes_per_ray': lanes,
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
-			'ray_order': f'{args.tile}x{args.tile} tiles', 't_thresh': 1e-4, 'w_thresh': 1e-4,
+			'ray_order': (f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside '
+						  f'the timed step' if ordered else f'{args.tile}x{args.tile} tiles'),
+			't_thresh': 1e-4, 'w_thresh': 1e-4,
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
 			'density_terms_per_ray': round(float(st[:, 3].mean()), 1),
 			'sh_evals_per_ray': round(float(st[:, 4].mean()), 1),
@@ -711,8 +726,13 @@ def bench_march(args):
 									   1e-4, 1e-4)
 	stream = torch.cuda.current_stream(dev)
 	lanes = args.lanes_per_ray or 0
-	launch_ms, out, wall = time_steps(lambda: me.march_forward(*args_of(), lanes=lanes), args.steps, args.warmup,
-									  stream)
+	ordered = args.order != 'off'
+	dir_res, pos_bits = args.order_dir_res or 2, args.order_pos_bits or 9
+
+	def step():
+		order = ext.ray_order(o, d, dir_res, pos_bits) if ordered else None
+		return me.march_forward(*args_of(), lanes=lanes, order=order)
+	launch_ms, out, wall = time_steps(step, args.steps, args.warmup, stream)
 	ms = float(np.mean(launch_ms))
 	rgb, T, depth, stats = out
 	st = stats.double()
@@ -764,7 +784,9 @@ def bench_march(args):
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
-		  'lanes_per_ray': lanes or (16 if B < 524288 else 1)},
+		  'lanes_per_ray': lanes or (16 if B < 524288 else 1),
+		  'ray_order': f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside the '
+					   f'timed step' if ordered else 'batch order'},
 		 hbm_roofline(ms, f'config5-scale{args.scale}-march', source_hash('march.hip'), abytes,
 					  'cache-oblivious bytes from the per-ray counters: per walk step 8 + 16 E, per sample 8 + 44 E, '
 					  'per coloured sample E (24 + SH bytes)', 'march_forward_kernel'), cpu)

@@ -78,8 +78,10 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
  * terms by sums, so only their summation order differs), 0 the library's default (the layout vgr_foam_infer runs:
  * 4 lanes per ray for stages 0 and 1 and lazy colours, one ray per lane for fused and baked colours). Fused and
  * baked colours with a finite color_cut always run one ray per lane (their neighbour skipping follows the edge
- * order). trace may be NULL (then trace_cap is ignored). No counterpart in the reference: the layout comparison
- * for vgr_foam_infer, whose arguments and outputs it otherwise shares.
+ * order). trace may be NULL (then trace_cap is ignored). order (NULL = the batch order): a permutation of
+ * 0 .. B - 1 giving the order in which the rays are traced (vgr_ray_order); results are the same in any order, an
+ * entry outside [0, B) is skipped. No counterpart in the reference: the layout comparison for vgr_foam_infer, whose
+ * arguments and outputs it otherwise shares.
  */
 int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                          const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
@@ -87,7 +89,7 @@ int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* of
                          const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
                          int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
                          float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
-                         int64_t lanes_per_ray, void* stream);
+                         const int32_t* order, int64_t lanes_per_ray, void* stream);
 
 /*
  * Cell traversal alone (foam_infer with stage 0: walk to the start cell, then exit faces up to far or cap) with a
@@ -125,15 +127,16 @@ int vgr_march_forward(const float* points, int64_t n_sites, const int32_t* offse
  * vgr_march_forward with the ray layout chosen by the caller: lanes_per_ray 1 (one ray per lane), 16 (a group of
  * 16 lanes per ray, one neighbour per lane: for small batches, whose launches are bound by each ray's serial chain
  * of loads) or 0 (by batch size: 16 below 524288 rays, else 1, which is what vgr_march_forward does). The layouts
- * visit the same sites; their sums differ in the order of addition. Same reference function as vgr_march_forward.
+ * visit the same sites; their sums differ in the order of addition. order (NULL = the batch order): the order in
+ * which the rays are traced, as for vgr_foam_infer_lanes. Same reference function as vgr_march_forward.
  */
 int vgr_march_forward_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
                             int64_t n_adj, const float* raw, const float* dA, const float* cA, const float* sh,
                             int64_t sh_deg, const float* o, const float* d, const int32_t* start,
                             const float* near_t, const float* mid_t, const float* far_t, int64_t n_rays, double dt,
                             int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T, float* depth,
-                            int32_t* stats, int32_t* trace, int64_t trace_cap, int64_t lanes_per_ray, void* work,
-                            int64_t work_bytes, void* stream);
+                            int32_t* stats, int32_t* trace, int64_t trace_cap, const int32_t* order,
+                            int64_t lanes_per_ray, void* work, int64_t work_bytes, void* stream);
 
 /*
  * Fused uniform-step march (backward: re-marches every ray). Replaces march_backward() of csrc/march.cu:405-428
@@ -314,6 +317,18 @@ int vgr_pack_foam(const float* points, int64_t n_sites, const int32_t* offsets, 
 int64_t vgr_grid_work_size(int64_t n_sites, int64_t n_cells);
 int vgr_grid_build(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,
                    const int32_t* res, int32_t* cell_start, int32_t* cell_sites, int32_t* work, void* stream);
+
+/*
+ * Coherent processing order of a ray batch, for the `order` argument of vgr_foam_infer_lanes and
+ * vgr_march_forward_lanes. No counterpart in the reference, which traces rays in the order given (config 5's
+ * incoherent batch: origins uniform in a cube, directions uniform on the sphere). A permutation sorting the rays
+ * by the octahedral bin of the direction on a dir_res x dir_res map (1..64), then by the Z-order of the origin with
+ * pos_bits (1..10) bits per axis over the origins' bounding box (2 log2(dir_res) + 3 pos_bits <= 32 key bits).
+ *   o, d f32 (B, 3) -> order i32 (B); work: vgr_ray_order_work_size(B) bytes, 256-byte aligned.
+ */
+int64_t vgr_ray_order_work_size(int64_t n_rays);
+int vgr_ray_order(const float* o, const float* d, int64_t n_rays, int32_t dir_res, int32_t pos_bits, int32_t* order,
+                  void* work, int64_t work_bytes, void* stream);
 
 /*
  * vgr_grid_build without a workspace argument, for callers that cannot allocate device memory (code under HIP

@@ -30,7 +30,8 @@ def test_header_declares_the_entry_points():
 			  'vgr_walk', 'vgr_density_forward', 'vgr_color_forward', 'vgr_field_work_size', 'vgr_conic_forward', 'vgr_density_backward', 'vgr_density_backward_work_size',
 			  'vgr_color_backward', 'vgr_color_backward_work_size', 'vgr_conic_backward', 'vgr_pack_work_size',
 			  'vgr_pack_foam', 'vgr_morton_work_size', 'vgr_morton_codes', 'vgr_bake_colors', 'vgr_grid_work_size',
-			  'vgr_grid_build', 'vgr_grid_nearest', 'vgr_last_error', 'vgr_abi_version'):
+			  'vgr_grid_build', 'vgr_grid_nearest', 'vgr_ray_order_work_size', 'vgr_ray_order', 'vgr_last_error',
+			  'vgr_abi_version'):
 		assert n in names
 
 
@@ -84,7 +85,7 @@ def test_library_reports_argument_errors_without_a_gpu():
 	assert lib.vgr_march_forward(*margs) == 0
 	# the layout argument and the training entries' workspaces are checked before any launch
 	margs[16] = 8
-	largs = margs[:27] + [8] + margs[27:]
+	largs = margs[:27] + [None, 8] + margs[27:]
 	assert lib.vgr_march_forward_lanes(*largs) == 1 and b'lanes_per_ray' in lib.vgr_last_error()
 	assert lib.vgr_march_backward_work_size(1000, 3) == 256000 + 256000
 	assert lib.vgr_foam_work_size(1000, 1) == 128000 + 256000
@@ -95,3 +96,14 @@ def test_library_reports_argument_errors_without_a_gpu():
 	assert lib.vgr_foam_forward(*fargs) == 1 and b'sh_deg' in lib.vgr_last_error()
 	# field records: 64 bytes per site
 	assert lib.vgr_field_work_size(0) == 0 and lib.vgr_field_work_size(1000) == 64000
+
+
+def test_ray_order_arguments_without_a_gpu():
+	"""vgr_ray_order validates its bin and key-width arguments on the host; an empty batch launches nothing."""
+	from vgr import _lib
+	lib = _lib.load()
+	assert lib.vgr_ray_order(None, None, 10, 0, 7, None, None, 0, None) == 1 and b'dir_res' in lib.vgr_last_error()
+	assert lib.vgr_ray_order(None, None, 10, 8, 11, None, None, 0, None) == 1 and b'pos_bits' in lib.vgr_last_error()
+	assert lib.vgr_ray_order(None, None, 10, 64, 7, None, None, 0, None) == 1 and b'key bits' in lib.vgr_last_error()
+	assert lib.vgr_ray_order(None, None, 0, 8, 7, None, None, 0, None) == 0
+	assert lib.vgr_ray_order_work_size(0) == 0 and lib.vgr_ray_order_work_size(1000) >= 3 * 4000

@@ -45,6 +45,7 @@ struct FoamRays {
     const float* __restrict__ t_far;
     const int* __restrict__ cap;
     int64_t n;
+    const int* __restrict__ order;  // processing order of the rays (a permutation of 0 .. n - 1), or null
 };
 
 struct FoamOut {
@@ -513,8 +514,10 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     __shared__ float4 cache_lds[cache_vec4<COLOR>(kSH)];
     ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
     if (kSH) cache = make_cache<COLOR>(cache_lds);
-    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
-    if (r >= R.n) return;
+    const int64_t i = xcd_block_id() * kBlock + threadIdx.x;
+    if (i >= R.n) return;
+    const int64_t r = R.order != nullptr ? R.order[i] : i;
+    if (r < 0 || r >= R.n) return;  // not a permutation entry: nothing is read or written
     const int start = R.start[r];
     if (start < 0 || start >= S.n_sites) {  // not traced: empty foreground
         O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
@@ -800,8 +803,10 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
     if (kSH) cache = make_cache<COLOR>(cache_lds);
     const int g = static_cast<int>(threadIdx.x) % G;
-    const int64_t r = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
-    if (r >= R.n) return;  // whole groups leave together
+    const int64_t i = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
+    if (i >= R.n) return;  // whole groups leave together
+    const int64_t r = R.order != nullptr ? R.order[i] : i;
+    if (r < 0 || r >= R.n) return;
     const bool writer = g == 0;
     const int start = R.start[r];
     if (start < 0 || start >= S.n_sites) {  // not traced: empty foreground
@@ -948,7 +953,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
                double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
-               int32_t* trace, int64_t trace_cap, int64_t lanes, void* stream) {
+               int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     if (lanes == kDefaultLanes) lanes = default_lanes(stage, color_mode);
     VGR_REQUIRE(lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8,
@@ -978,7 +983,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                       static_cast<int>(n_sites)};
     const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
                        static_cast<int>(sh_deg)};
-    const FoamRays R{o, d, start, near_t, far_t, cap, n_rays};
+    const FoamRays R{o, d, start, near_t, far_t, cap, n_rays, order};
     const FoamOut O{rgb, T, depth, stats, trace, trace_cap};
     const hipStream_t s = as_stream(stream);
     // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
@@ -1000,7 +1005,7 @@ extern "C" int vgr_foam_infer(const float* points, int64_t n_sites, const int32_
                               int32_t* stats, void* stream) {
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, nullptr, 0, vgr::kDefaultLanes, stream);
+                           T, depth, stats, nullptr, 0, nullptr, vgr::kDefaultLanes, stream);
 }
 
 extern "C" int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* offsets,
@@ -1014,7 +1019,7 @@ extern "C" int vgr_foam_infer_traced(const float* points, int64_t n_sites, const
     VGR_REQUIRE(trace != nullptr && trace_cap > 0, "foam_infer_traced: trace must be non-null with trace_cap > 0");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, trace, trace_cap, vgr::kDefaultLanes, stream);
+                           T, depth, stats, trace, trace_cap, nullptr, vgr::kDefaultLanes, stream);
 }
 
 extern "C" int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
@@ -1024,10 +1029,9 @@ extern "C" int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const 
                                     double t_thresh, double w_thresh, double color_cut, int64_t color_mode,
                                     int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
                                     float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
-                                    int64_t lanes_per_ray, void* stream) {
+                                    const int32_t* order, int64_t lanes_per_ray, void* stream) {
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_lanes: trace needs trace_cap > 0");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap,
-                           lanes_per_ray, stream);
+                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream);
 }

@@ -53,6 +53,7 @@ struct MarchRays {
     const float* __restrict__ t_mid;
     const float* __restrict__ t_far;
     int64_t n;
+    const int* __restrict__ order;  // processing order of the rays (a permutation of 0 .. n - 1), or null
 };
 
 struct MarchOut {
@@ -354,8 +355,10 @@ constexpr int kMarchWaves = 4;
 template <bool TRACE>
 __global__ void __launch_bounds__(kBlock, kMarchWaves)
     march_forward_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
-    const int64_t r = xcd_block_id() * kBlock + threadIdx.x;
-    if (r >= R.n) return;
+    const int64_t i = xcd_block_id() * kBlock + threadIdx.x;
+    if (i >= R.n) return;
+    const int64_t r = R.order != nullptr ? R.order[i] : i;
+    if (r < 0 || r >= R.n) return;  // not a permutation entry: nothing is read or written
     const int cur = R.start[r];
     if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground
         O.rgb[3 * r] = O.rgb[3 * r + 1] = O.rgb[3 * r + 2] = 0.f;
@@ -1022,9 +1025,11 @@ __device__ void march_ray_group(const MarchField& F, const MarchParams& M, const
 
 template <bool TRACE>
 __global__ void __launch_bounds__(kBlock) march_group_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
-    const int64_t r = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
+    const int64_t i = (xcd_block_id() * kBlock + threadIdx.x) / kGroup;
     const int g = threadIdx.x % kGroup;
-    if (r >= R.n) return;
+    if (i >= R.n) return;
+    const int64_t r = R.order != nullptr ? R.order[i] : i;
+    if (r < 0 || r >= R.n) return;  // not a permutation entry: the whole group leaves
     const int cur = R.start[r];
     if (cur < 0 || cur >= F.n_sites) {  // not traced: empty foreground
         if (g == 0) {
@@ -1605,7 +1610,8 @@ extern "C" int vgr_march_forward_lanes(const float* points, int64_t n_sites, con
                                        const float* mid_t, const float* far_t, int64_t n_rays, double dt,
                                        int64_t n_bg, double t_thresh, double w_thresh, float* rgb, float* T,
                                        float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
-                                       int64_t lanes_per_ray, void* work, int64_t work_bytes, void* stream) {
+                                       const int32_t* order, int64_t lanes_per_ray, void* work, int64_t work_bytes,
+                                       void* stream) {
     using namespace vgr;
     VGR_REQUIRE(lanes_per_ray == 0 || lanes_per_ray == 1 || lanes_per_ray == kGroup,
                 "march_forward: lanes_per_ray must be 0 (by batch size), 1 or 16 (got %lld)",
@@ -1628,7 +1634,7 @@ extern "C" int vgr_march_forward_lanes(const float* points, int64_t n_sites, con
     launch_pack(points, raw, dA, cA, sh, n_sites, sh_deg, rec, as_stream(stream));
     const MarchField F{rec, offsets, adj, int(sh_deg), int(n_sites)};
     const MarchParams M{float(dt), int(n_bg), float(t_thresh), float(w_thresh)};
-    const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays};
+    const MarchRays R{o, d, start, near_t, mid_t, far_t, n_rays, order};
     const MarchOut O{rgb, T, depth, stats, trace, trace_cap};
     if (march_lanes(lanes_per_ray, n_rays) == kGroup) {
         const dim3 grid(grid_for(n_rays * kGroup, kBlock));
@@ -1656,7 +1662,7 @@ extern "C" int vgr_march_forward(const float* points, int64_t n_sites, const int
                                  int64_t work_bytes, void* stream) {
     return vgr_march_forward_lanes(points, n_sites, offsets, adj, n_adj, raw, dA, cA, sh, sh_deg, o, d, start, near_t,
                                    mid_t, far_t, n_rays, dt, n_bg, t_thresh, w_thresh, rgb, T, depth, stats, trace,
-                                   trace_cap, 0, work, work_bytes, stream);
+                                   trace_cap, nullptr, 0, work, work_bytes, stream);
 }
 
 extern "C" int vgr_march_backward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,

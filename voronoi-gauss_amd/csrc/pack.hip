@@ -21,6 +21,7 @@
 #include "vgr_abi.h"
 #include "vgr_device.h"
 #include "vgr_scan.h"
+#include "vgr_bbox.h"
 
 #include <cmath>
 
@@ -165,59 +166,6 @@ int64_t pack_bytes(int64_t n) {
     return align256p(16 * n) + 2 * align256p(4 * n) + align256p(4 * (scan_tiles_of(n) + 1));
 }
 
-// Per-block bounding boxes of the points: box[6 * block .. + 6) = (min xyz, max xyz).
-__global__ void __launch_bounds__(kBlock)
-    bbox_blocks_kernel(const float* __restrict__ points, int64_t n, float* __restrict__ box) {
-    __shared__ float part[6][kBlock];
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        const float v = i < n ? points[3 * i + a] : points[0];
-        part[a][threadIdx.x] = v, part[3 + a][threadIdx.x] = v;
-    }
-    __syncthreads();
-    for (int off = kBlock / 2; off > 0; off >>= 1) {
-        if (static_cast<int>(threadIdx.x) < off) {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                part[a][threadIdx.x] = fminf(part[a][threadIdx.x], part[a][threadIdx.x + off]);
-                part[3 + a][threadIdx.x] = fmaxf(part[3 + a][threadIdx.x], part[3 + a][threadIdx.x + off]);
-            }
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x < 6) box[6 * int64_t(blockIdx.x) + threadIdx.x] = part[threadIdx.x][0];
-}
-
-// Reduces the per-block boxes in place into box[0 .. 6) (one block; min and max are exact in any order).
-__global__ void __launch_bounds__(kBlock) bbox_final_kernel(float* __restrict__ box, int64_t n_blocks) {
-    __shared__ float part[6][kBlock];
-    float v[6];
-#pragma unroll
-    for (int a = 0; a < 6; ++a) v[a] = box[a];
-    for (int64_t b = threadIdx.x; b < n_blocks; b += kBlock) {
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            v[a] = fminf(v[a], box[6 * b + a]);
-            v[3 + a] = fmaxf(v[3 + a], box[6 * b + 3 + a]);
-        }
-    }
-#pragma unroll
-    for (int a = 0; a < 6; ++a) part[a][threadIdx.x] = v[a];
-    __syncthreads();
-    for (int off = kBlock / 2; off > 0; off >>= 1) {
-        if (static_cast<int>(threadIdx.x) < off) {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                part[a][threadIdx.x] = fminf(part[a][threadIdx.x], part[a][threadIdx.x + off]);
-                part[3 + a][threadIdx.x] = fmaxf(part[3 + a][threadIdx.x], part[3 + a][threadIdx.x + off]);
-            }
-        }
-        __syncthreads();
-    }
-    __syncthreads();
-    if (threadIdx.x < 6) box[threadIdx.x] = part[threadIdx.x][0];
-}
 
 __global__ void __launch_bounds__(kBlock)
     morton_kernel(const float* __restrict__ points, int64_t n, const float* __restrict__ box, int bits,
@@ -300,8 +248,7 @@ extern "C" int vgr_morton_codes(const float* points, int64_t n, int32_t bits, in
                 static_cast<long long>(4 * 6 * blocks));
     float* box = static_cast<float*>(work);
     const hipStream_t s = as_stream(stream);
-    hipLaunchKernelGGL(bbox_blocks_kernel, dim3(blocks), dim3(kBlock), 0, s, points, n, box);
-    hipLaunchKernelGGL(bbox_final_kernel, dim3(1), dim3(kBlock), 0, s, box, blocks);
+    bounding_box(points, n, box, s);
     hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(kBlock), 0, s, points, n, box, int(bits), code);
     return launch_status("morton_codes");
 }

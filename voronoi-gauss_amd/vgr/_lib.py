@@ -21,7 +21,7 @@ SIGNATURES = {
 	'vgr_foam_infer_traced': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64,
 							  _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
 	'vgr_foam_infer_lanes': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64,
-							 _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P],
+							 _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_forward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						  _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_work_size': [_I64, _I64],
@@ -32,7 +32,7 @@ SIGNATURES = {
 	'vgr_foam_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _F64, _F64, _P, _P,
 						  _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P],
 	'vgr_march_forward_lanes': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64,
-								_I64, _F64, _F64, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
+								_I64, _F64, _F64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P, _I64, _P],
 	'vgr_march_backward': [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _F64, _I64,
 						   _F64, _F64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P],
 	'vgr_foam_traverse_faces': [_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64,
@@ -56,13 +56,15 @@ SIGNATURES = {
 	'vgr_conic_forward': [_P, _P, _I64, _F64, _P, _P],
 	'vgr_grid_work_size': [_I64, _I64],
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
+	'vgr_ray_order_work_size': [_I64],
+	'vgr_ray_order': [_P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
 	'vgr_grid_build_noalloc': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P],
 	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
 	'vgr_abi_version': [],
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 20
+ABI_VERSION = 21
 _lib = None
 
 
@@ -87,6 +89,7 @@ def load():
 		lib.vgr_density_backward_work_size.restype = ctypes.c_int64
 		lib.vgr_pack_work_size.restype = ctypes.c_int64
 		lib.vgr_morton_work_size.restype = ctypes.c_int64
+		lib.vgr_ray_order_work_size.restype = ctypes.c_int64
 		if lib.vgr_abi_version() != ABI_VERSION:
 			raise RuntimeError(f'{LIB_PATH} has ABI {lib.vgr_abi_version()}, expected {ABI_VERSION}: rebuild it')
 		_lib = lib

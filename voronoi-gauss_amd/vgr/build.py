@@ -5,7 +5,8 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(HERE), 'csrc')
-SOURCES = ['abi.hip', 'foam_infer.hip', 'foam_faces.hip', 'field_grad.hip', 'pack.hip', 'march.hip', 'field.hip', 'grid.hip']
+SOURCES = ['abi.hip', 'foam_infer.hip', 'foam_faces.hip', 'field_grad.hip', 'pack.hip', 'march.hip', 'field.hip', 'grid.hip',
+		   'order.hip']
 LIB = os.path.join(HERE, 'libvgr.so')
 
 # -ffp-contract=off: traversal arithmetic rounds exactly as written (bit-exact walks against the CPU oracle).

@@ -187,10 +187,11 @@ def _field_work(points, m, records):
 class _MarchExtension:
 	@staticmethod
 	def march_forward(points, offsets, adj, raw, dA, cA, sh, sh_deg, o, d, start, near, mid, far, dt, n_bg,
-					  t_thresh, w_thresh, trace_cap=0, lanes=0, work=None):
+					  t_thresh, w_thresh, trace_cap=0, lanes=0, work=None, order=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0).
 		lanes: 1 ray per lane (1), 16 lanes per ray (16) or by batch size (0). work: optional uint8 device workspace
-		(at least vgr_march_work_size bytes); a training step passes the backward's, which then reuses its blocks."""
+		(at least vgr_march_work_size bytes); a training step passes the backward's, which then reuses its blocks.
+		order: optional int32 (B,) permutation, the order in which the rays are traced (ray_order); same results."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -218,7 +219,8 @@ class _MarchExtension:
 			call('vgr_march_forward_lanes', ptr(points), points.numel() // 3, ptr(offsets), ptr(adj), adj.numel(),
 				 ptr(raw), ptr(dA), ptr(cA), ptr(sh), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(mid),
 				 ptr(far), B, float(dt), int(n_bg), float(t_thresh), float(w_thresh), ptr(rgb), ptr(T), ptr(depth),
-				 ptr(stats), ptr(trace), int(trace_cap), int(lanes), ptr(work), work_bytes, stream_of(dev))
+				 ptr(stats), ptr(trace), int(trace_cap), ptr(_order(order, B, dev)), int(lanes), ptr(work), work_bytes,
+				 stream_of(dev))
 		return out
 
 	@staticmethod
@@ -262,11 +264,12 @@ class _MarchExtension:
 class _FoamInferExtension:
 	@staticmethod
 	def foam_infer(points, offsets, nbr, edge, attr, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None):
+				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None, order=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 5) int32] (+ trace (B, trace_cap) int32, the cell of
 		every sample in original numbering, -1 past the last sample, when trace_cap > 0). lanes: None for the
 		library's default layout, else 1 (one ray per lane) or 2 / 4 / 8 (that many lanes per ray,
-		vgr_foam_infer_lanes)."""
+		vgr_foam_infer_lanes). order: optional int32 (B,) permutation, the order in which the rays are traced
+		(ray_order); the results are the same."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32), (attr, 'attr', torch.float32),
 						 (o, 'o', torch.float32), (d, 'd', torch.float32), (start, 'start', torch.int32),
@@ -304,14 +307,42 @@ class _FoamInferExtension:
 				float(t_thresh), float(w_thresh), float(color_cut), int(color_mode), int(stage), ptr(cp), ptr(og),
 				ptr(rgb), ptr(T), ptr(depth), ptr(stats)]
 		with torch.cuda.device(dev):
-			if lanes is not None:
-				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0, int(lanes),
-					 stream_of(dev))
+			if lanes is not None or order is not None:
+				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
+					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), stream_of(dev))
 			elif trace is None:
 				call('vgr_foam_infer', *args, stream_of(dev))
 			else:
 				call('vgr_foam_infer_traced', *args, ptr(trace), int(trace_cap), stream_of(dev))
 		return out
+
+
+def _order(order, B, dev):
+	"""Checks an optional processing order (int32 CUDA tensor of B entries) -> the tensor or None."""
+	if order is None:
+		return None
+	_check(order, 'order', torch.int32)
+	_require(order.numel() == B and order.device == dev, 'order must hold one entry per ray, on the rays\' device')
+	return order
+
+
+def ray_order(o, d, dir_res=8, pos_bits=7):
+	"""Coherent processing order of a ray batch (vgr_ray_order): int32 (B,) permutation sorting the rays by the
+	octahedral bin of the direction (dir_res x dir_res bins), then by the Z-order of the origin (pos_bits bits per
+	axis). Passed as `order` to foam_infer / march_forward, it changes the order in which rays are traced (the
+	lanes of a wave then share cache lines), not their results."""
+	_check(o, 'o', torch.float32)
+	_check(d, 'd', torch.float32)
+	B, dev = o.size(0), o.device
+	_require(o.dim() == 2 and o.size(1) == 3 and d.shape == o.shape, 'o and d must be (B, 3)')
+	out = torch.empty(B, dtype=torch.int32, device=dev)
+	if B == 0:
+		return out
+	wb = int(_lib.load().vgr_ray_order_work_size(B))
+	work = torch.empty(wb, dtype=torch.uint8, device=dev)
+	with torch.cuda.device(dev):
+		call('vgr_ray_order', ptr(o), ptr(d), B, int(dir_res), int(pos_bits), ptr(out), ptr(work), wb, stream_of(dev))
+	return out
 
 
 def traverse_faces(points, offsets, nbr, edge, o, d, start, near, far, cap=None, orig=None, trace_cap=0, lanes=4):
