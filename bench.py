@@ -137,6 +137,19 @@ def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray):
 	return float(56 * len(s) + 24 * s[:, 0].sum() + 84 * s[:, 3].sum() + sh_bytes * u_sh_per_ray * len(s))
 
 
+def wave_balance(stats, rays_per_wave=64):
+	"""Lane use bounds of one-ray-per-lane waves (64 consecutive rays, one 8x8 tile) from the per-ray counters: the
+	mean over waves of mean/max of the samples per ray (a wave runs until its longest ray ends) and of the density
+	terms per ray (neighbourhood edges: the lockstep also waits for the largest neighbourhood)."""
+	n = (len(stats) // rays_per_wave) * rays_per_wave
+	s = stats[:n].double().view(-1, rays_per_wave, stats.shape[1])
+	out = {}
+	for name, col in (('samples', 0), ('density_terms', 3)):
+		v = s[:, :, col]
+		out[name] = round(float((v.mean(1) / v.max(1).values.clamp_min(1)).mean()), 4)
+	return out
+
+
 def distinct_blended_sites(fi, pack, args_of, n_rays, sh_deg, tiles=256):
 	"""Mean number of distinct sites whose colour a ray blends, over `tiles` 8x8 ray tiles spread evenly over the
 	launch: the rays are traced again (same kernel, outside the timed region) and, exact colours blending every
@@ -364,6 +377,7 @@ def bench_foam(args):
 			'distinct_blended_sites_per_ray': None if fast else round(u_sh, 1),
 			'distinct_sites_traced_rays': u_rays or None, 'quality': quality,
 			'mean_T': round(float(T.double().mean()), 4),
+			'wave_lane_use_bound': wave_balance(stats),
 		},
 		'roofline': roofline,
 		'cpu_baseline': cpu,

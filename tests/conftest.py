@@ -54,7 +54,7 @@ def pytest_sessionfinish(session, exitstatus):
 			proc.wait()
 
 
-def _progress(msg):
+def progress(msg):
 	"""A progress line on stdout and in gpurun_out/stated_sizes_progress.log: a wait of minutes for Qhull then
 	still shows activity when pytest captures the output."""
 	print(msg, flush=True)
@@ -75,14 +75,14 @@ def wait_for_geometry(config, timeout=900):
 			proc.kill()
 			proc.wait()
 			raise RuntimeError(f'triangulation of config {config} did not finish in {timeout} s')
-		_progress(f'[stated sizes] waiting for the config-{config} triangulation ({time.time() - t0:.0f} s)')
+		progress(f'[stated sizes] waiting for the config-{config} triangulation ({time.time() - t0:.0f} s)')
 		try:
 			proc.wait(timeout=20)
 		except subprocess.TimeoutExpired:
 			pass
 	if proc.returncode != 0:
 		raise RuntimeError(f'triangulation of config {config} failed ({proc.returncode}):\n' + open(log).read()[-4000:])
-	_progress(f'[stated sizes] config {config} geometry ready {time.time() - t0:.0f} s after its build started')
+	progress(f'[stated sizes] config {config} geometry ready {time.time() - t0:.0f} s after its build started')
 
 
 @pytest.fixture(scope='session')

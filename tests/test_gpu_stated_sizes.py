@@ -27,7 +27,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import stated_configs, wait_for_geometry
+from conftest import progress, stated_configs, wait_for_geometry
 from helpers import ray_bounds_np
 from test_gpu_foam import compare, psnr, ref_foam
 from test_oracle_grad import rel
@@ -108,9 +108,9 @@ def test_foam_full_workload(stated):
 	g = rows(full, sel)
 	same = (g['stats'] == r['stats']).all(1)
 	err = np.abs(g['rgb'] - r['rgb']).max()
-	print(f'\n[stated sizes] config {s.config}: {s.sc.n_sites} sites, {s.B} rays; oracle on {len(sel)} rays: max '
+	progress(f'[stated sizes] config {s.config}: {s.sc.n_sites} sites, {s.B} rays; oracle on {len(sel)} rays: max '
 		  f'|rgb| {err:.2e}, max |T| {np.abs(g["T"] - r["T"]).max():.2e}, stats equal on {same.mean():.5f}, PSNR '
-		  f'{psnr(g["rgb"], r["rgb"]):.1f} dB; mean samples {full["stats"][:, 0].mean():.1f}', flush=True)
+		  f'{psnr(g["rgb"], r["rgb"]):.1f} dB; mean samples {full["stats"][:, 0].mean():.1f}')
 	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
 	assert psnr(g['rgb'], r['rgb']) >= 60.0
 	# rays whose statistics differ: same cells with the thresholds off (the difference is where a threshold fell)
@@ -121,7 +121,7 @@ def test_foam_full_workload(stated):
 		np.testing.assert_array_equal(go['trace'], ro['trace'])
 	caps = {'rays hitting the 8192-cell cap': int((full['stats'][:, 0] > MAX_CELLS).sum()),
 			'rays hitting the 4096-step walk cap': int((full['stats'][:, 2] >= WALK_CAP).sum())}
-	print(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}', flush=True)
+	progress(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}')
 
 
 def test_foam_traces_and_exact_colours(stated):
@@ -143,8 +143,8 @@ def test_foam_traces_and_exact_colours(stated):
 		r = s.oracle(few, stage=stage, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
 		compare(g, r, t_max=s.sc.far_radius)
 		np.testing.assert_array_equal(g['stats'], r['stats'])
-	print(f'\n[stated sizes] config {s.config}: thresholds off, {len(few)} rays, mean {g["stats"][:, 0].mean():.0f} '
-		  f'cells per ray, cell sequences bit-exact', flush=True)
+	progress(f'[stated sizes] config {s.config}: thresholds off, {len(few)} rays, mean {g["stats"][:, 0].mean():.0f} '
+		  f'cells per ray, cell sequences bit-exact')
 
 
 @pytest.fixture(scope='module')
@@ -185,9 +185,9 @@ def test_march_config5_full_batch(gpu, config5_field):
 	r = oracle.march_forward(host['points'], host['offsets'], host['adj'], host['raw'], host['dA'], host['cA'],
 							 host['sh'], sc.sh_deg, *rays, dt, n_bg, rays=sel)
 	same = (stats[sel] == r['stats']).all(1)
-	print(f'\n[stated sizes] config 5 march: {B} rays, oracle on {len(sel)}: max |rgb| '
+	progress(f'[stated sizes] config 5 march: {B} rays, oracle on {len(sel)}: max |rgb| '
 		  f'{np.abs(rgb[sel] - r["rgb"]).max():.2e}, max |T| {np.abs(T[sel] - r["T"]).max():.2e}, stats equal on '
-		  f'{same.mean():.5f}, mean samples {stats[:, 0].mean():.1f}', flush=True)
+		  f'{same.mean():.5f}, mean samples {stats[:, 0].mean():.1f}')
 	np.testing.assert_allclose(rgb[sel], r['rgb'], atol=TOL, rtol=0)
 	np.testing.assert_allclose(T[sel], r['T'], atol=TOL, rtol=0)
 	assert same.mean() >= 0.995
@@ -247,7 +247,7 @@ def test_march_backward_config5_default_layout(gpu, config5_field, t_thresh, w_t
 								host['sh'], sc.sh_deg, *[a[hot] for a in sub], dt, n_bg, rgb.cpu().numpy()[hot],
 								T.cpu().numpy()[hot], g_rgb[hot], g_T[hot], t_thresh, w_thresh)
 	errs = {name: rel(a.cpu().numpy(), r) for name, a, r in zip(('raw', 'dA', 'cA', 'sh'), got, ref)}
-	print(f'\n[stated sizes] config 5 march backward (t_thresh {t_thresh}, w_thresh {w_thresh}), {B} rays, '
-		  f'{len(hot)} with gradients: relative errors {errs}', flush=True)
+	progress(f'[stated sizes] config 5 march backward (t_thresh {t_thresh}, w_thresh {w_thresh}), {B} rays, '
+		  f'{len(hot)} with gradients: relative errors {errs}')
 	for name, e in errs.items():
 		assert e < bars[name], name
