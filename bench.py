@@ -194,6 +194,8 @@ def main():
 	ap.add_argument('--eps-density', type=float, default=0.0, help='skip density terms below eps')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
+	ap.add_argument('--tile-curve', default='morton', choices=['row', 'morton'],
+					help='order of the pixel tiles of a camera (row-major or Z-order of the tile coordinates)')
 	ap.add_argument('--cpu-seconds', type=float, default=15.0, help='target CPU-oracle time (0: skip)')
 	ap.add_argument('--copy-probe', action='store_true', help='also run a 1 GiB device copy (PMC calibration)')
 	ap.add_argument('--batch', type=int, default=4096, help='grad workload: random rays per training step')
@@ -255,7 +257,7 @@ def bench_foam(args):
 	model = VoronoiGaussField.from_scene(sc, dev)
 	fast = args.sh_half or args.eps_color > 0 or args.eps_density > 0 or args.colors == 'baked'
 	pack = render.pack_foam(model, reorder=not args.no_reorder, sh_half=args.sh_half, eps_density=args.eps_density)
-	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile)
+	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile, curve=args.tile_curve)
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	start = torch.from_numpy(start_np).to(dev)
 	if pack['inv'] is not None:
@@ -369,7 +371,7 @@ def bench_foam(args):
 			'lanes_per_ray': lanes,
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': (f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside '
-						  f'the timed step' if ordered else f'{args.tile}x{args.tile} tiles'),
+						  f'the timed step' if ordered else f'{args.tile}x{args.tile} tiles, {args.tile_curve} order'),
 			't_thresh': 1e-4, 'w_thresh': 1e-4,
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
 			'density_terms_per_ray': round(float(st[:, 3].mean()), 1),
@@ -821,7 +823,7 @@ def bench_traverse(args):
 	sc = scenes.make_scene(args.config, scale=args.scale, log=log)
 	model = VoronoiGaussField.from_scene(sc, dev)
 	pack = render.pack_foam(model, reorder=True)
-	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile)
+	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile, curve=args.tile_curve)
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	start = pack['inv'][torch.from_numpy(start_np).to(dev).long()].int()
 	near, _, far = render.ray_bounds(o, d, 0.02, sc.far_radius)

@@ -102,6 +102,25 @@ def test_tile_order_groups_8x8_tiles():
 		raise AssertionError('expected partial tiles at the image border')
 
 
+def test_morton_tile_order():
+	"""Z-order of the tiles: the same tiles as the row order, each tile's pixels in the same order, and the tiles
+	of a 64 x 64 image (8 x 8 tiles) visited along the Z curve: every aligned run of 4 tiles is a 2 x 2 block and
+	every run of 16 a 4 x 4 block."""
+	H, W = 64, 64
+	perm = scenes.tile_order(H, W, curve='morton')
+	row = scenes.tile_order(H, W, curve='row')
+	assert sorted(perm.tolist()) == list(range(H * W))
+	tiles = perm.reshape(-1, 64)
+	rows = row.reshape(-1, 64)
+	ty, tx = tiles[:, 0] // W // 8, tiles[:, 0] % W // 8
+	np.testing.assert_array_equal(tiles, rows[ty * 8 + tx])
+	assert scenes.morton2(np.array([0, 0, 1, 1, 2]), np.array([0, 1, 0, 1, 0])).tolist() == [0, 1, 2, 3, 8]
+	for n, side in ((4, 2), (16, 4)):
+		for s in range(0, 64, n):
+			assert len(set(ty[s:s + n].tolist())) == side and len(set(tx[s:s + n].tolist())) == side
+	assert ty[:4].tolist() == [0, 0, 1, 1] and tx[:4].tolist() == [0, 1, 0, 1]
+
+
 def test_camera_rays_convention():
 	cam = scenes.Camera(np.array([0.0, 0.0, 3.0]), np.zeros(3), np.array([0.0, 1.0, 0.0]), 64, 48)
 	o, d = cam.rays()

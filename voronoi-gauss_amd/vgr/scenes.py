@@ -82,9 +82,10 @@ class Scene:
 	def n_sites(self):
 		return len(self.points)
 
-	def camera_rays(self, tile=8):
-		"""-> o, d (B, 3) f32 of all cameras (tile order when tile > 0), start (B,) i32 = the site nearest to
-		each camera centre, and the pixel permutation (None for ray batches)."""
+	def camera_rays(self, tile=8, curve='row'):
+		"""-> o, d (B, 3) f32 of all cameras (tile order when tile > 0, the tiles in `curve` order: 'row' or
+		'morton'), start (B,) i32 = the site nearest to each camera centre, and the pixel permutation (None for ray
+		batches)."""
 		if self.ray_batch is not None:
 			o, d = self.ray_batch
 			return o, d, nearest_sites(self.points, o), None
@@ -94,7 +95,7 @@ class Scene:
 		base = 0
 		for c, s in zip(self.cameras, cstart):
 			o, d = c.rays()
-			perm = tile_order(c.height, c.width, tile, tile) if tile else np.arange(len(o))
+			perm = tile_order(c.height, c.width, tile, tile, curve) if tile else np.arange(len(o))
 			os_.append(o[perm])
 			ds.append(d[perm])
 			starts.append(np.full(len(o), s, dtype=np.int32))
@@ -103,11 +104,31 @@ class Scene:
 		return (np.concatenate(os_), np.concatenate(ds), np.concatenate(starts), np.concatenate(perms))
 
 
-def tile_order(H, W, th=8, tw=8):
+def morton2(y, x):
+	"""Z-order key of non-negative integer coordinates below 2^16 (bits of y and x interleaved, y above x)."""
+	def spread(v):
+		v = v.astype(np.int64) & 0xFFFF
+		v = (v | (v << 8)) & 0x00FF00FF
+		v = (v | (v << 4)) & 0x0F0F0F0F
+		v = (v | (v << 2)) & 0x33333333
+		return (v | (v << 1)) & 0x55555555
+	return (spread(y) << 1) | spread(x)
+
+
+def tile_order(H, W, th=8, tw=8, curve='row'):
 	"""Pixel permutation grouping th * tw consecutive rays into th x tw tiles (bench_infer.py:37-41 uses 4 x 8
-	for 32-lane warps; 8 x 8 fills a 64-lane wavefront)."""
+	for 32-lane warps; 8 x 8 fills a 64-lane wavefront). The tiles follow each other in row-major order ('row') or
+	along the Z-order curve of their tile coordinates ('morton'), which keeps any run of consecutive tiles (the
+	tiles a GPU renders at one time) compact in the image."""
 	y, x = np.meshgrid(np.arange(H), np.arange(W), indexing='ij')
-	key = ((y // th) * ((W + tw - 1) // tw) + x // tw) * (th * tw) + (y % th) * tw + x % tw
+	ty, tx = y // th, x // tw
+	if curve == 'row':
+		tkey = ty.astype(np.int64) * ((W + tw - 1) // tw) + tx
+	elif curve == 'morton':
+		tkey = morton2(ty, tx)
+	else:
+		raise ValueError(f'unknown tile curve {curve!r}')
+	key = tkey * (th * tw) + (y % th) * tw + x % tw
 	return np.argsort(key.ravel(), kind='stable')
 
 
