@@ -338,6 +338,8 @@ def bench_foam(args):
 	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
 	st = stats.double()
 	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}-l{lanes}'
+	if not ordered:
+		key += f'-tiles{args.tile}{args.tile_curve}'
 	if ordered:
 		key += f'-order{dir_res}x{pos_bits}'
 	if fast:
