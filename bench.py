@@ -805,7 +805,8 @@ def bench_march(args):
 		  'lanes_per_ray': lanes or (16 if B < 524288 else 1),
 		  'ray_order': f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside the '
 					   f'timed step' if ordered else 'batch order'},
-		 hbm_roofline(ms, f'config5-scale{args.scale}-march', source_hash('march.hip'), abytes,
+		 hbm_roofline(ms, f'config5-scale{args.scale}-march-l{lanes or (16 if B < 524288 else 1)}' +
+					  (f'-order{dir_res}x{pos_bits}' if ordered else ''), source_hash('march.hip', 'order.hip'), abytes,
 					  'cache-oblivious bytes from the per-ray counters: per walk step 8 + 16 E, per sample 8 + 44 E, '
 					  'per coloured sample E (24 + SH bytes)', 'march_forward_kernel'), cpu)
 
