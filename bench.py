@@ -745,7 +745,7 @@ def bench_march(args):
 	stream = torch.cuda.current_stream(dev)
 	lanes = args.lanes_per_ray or 0
 	ordered = args.order != 'off'
-	dir_res, pos_bits = args.order_dir_res or 2, args.order_pos_bits or 9
+	dir_res, pos_bits = args.order_dir_res or 4, args.order_pos_bits or 8
 
 	def step():
 		order = ext.ray_order(o, d, dir_res, pos_bits) if ordered else None
