@@ -95,6 +95,20 @@ def stated(request, gpu):
 	torch.cuda.empty_cache()
 
 
+def spread(stats, wave=64):
+	"""How uneven the work of the rays is: samples per ray (mean, median, 99th percentile, max) and, for waves of 64
+	consecutive rays as the one-ray-per-lane kernel runs them, the mean over waves of mean / max of the samples and
+	of the density terms per ray (the share of lane time a wave would keep busy if it could only wait for its
+	longest ray)."""
+	n = stats[:, 0].astype(np.float64)
+	m = (len(stats) // wave) * wave
+	w = stats[:m].astype(np.float64).reshape(-1, wave, stats.shape[1])
+	use = {name: round(float((w[:, :, col].mean(1) / np.maximum(w[:, :, col].max(1), 1)).mean()), 3)
+		   for name, col in (('samples', 0), ('density_terms', 3))}
+	return {'samples_mean': round(float(n.mean()), 1), 'p50': float(np.percentile(n, 50)),
+			'p99': float(np.percentile(n, 99)), 'max': int(n.max()), 'wave_lane_use_bound': use}
+
+
 def rows(res, sel):
 	return {k: (None if v is None else v[sel]) for k, v in res.items()}
 
@@ -122,6 +136,7 @@ def test_foam_full_workload(stated):
 	caps = {'rays hitting the 8192-cell cap': int((full['stats'][:, 0] > MAX_CELLS).sum()),
 			'rays hitting the 4096-step walk cap': int((full['stats'][:, 2] >= WALK_CAP).sum())}
 	progress(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}')
+	progress(f'[stated sizes] config {s.config} ray-length spread: {spread(full["stats"])}')
 
 
 def test_foam_traces_and_exact_colours(stated):
