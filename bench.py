@@ -137,14 +137,15 @@ def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray):
 	return float(56 * len(s) + 24 * s[:, 0].sum() + 84 * s[:, 3].sum() + sh_bytes * u_sh_per_ray * len(s))
 
 
-def wave_balance(stats, rays_per_wave=64):
-	"""Lane use bounds of one-ray-per-lane waves (64 consecutive rays, one 8x8 tile) from the per-ray counters: the
-	mean over waves of mean/max of the samples per ray (a wave runs until its longest ray ends) and of the density
-	terms per ray (neighbourhood edges: the lockstep also waits for the largest neighbourhood)."""
+def wave_balance(stats, rays_per_wave=64, cols=(('samples', 0), ('density_terms', 3))):
+	"""Lane use bounds of one-ray-per-lane waves (64 consecutive rays in processing order, one 8x8 tile for camera
+	rays) from the per-ray counters: the mean over waves of mean/max of each named column (samples per ray: a wave
+	runs until its longest ray ends; foam_infer's density terms, the neighbourhood edges, since its lockstep also
+	waits for the largest neighbourhood)."""
 	n = (len(stats) // rays_per_wave) * rays_per_wave
 	s = stats[:n].double().view(-1, rays_per_wave, stats.shape[1])
 	out = {}
-	for name, col in (('samples', 0), ('density_terms', 3)):
+	for name, col in cols:
 		v = s[:, :, col]
 		out[name] = round(float((v.mean(1) / v.max(1).values.clamp_min(1)).mean()), 4)
 	return out
@@ -802,6 +803,8 @@ def bench_march(args):
 		  'samples_per_ray': round(float(st[:, 0].mean()), 2),
 		  'coloured_samples_per_ray': round(float(st[:, 1].mean()), 2),
 		  'walk_steps_per_ray': round(float(st[:, 2].mean()), 2), 'mean_T': round(float(T.double().mean()), 4),
+		  'wave_lane_use_bound': wave_balance(stats[ext.ray_order(o, d, dir_res, pos_bits).long()] if ordered else stats,
+											  cols=(('samples', 0), ('walk_steps', 2))),
 		  'lanes_per_ray': lanes or (16 if B < 524288 else 1),
 		  'ray_order': f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside the '
 					   f'timed step' if ordered else 'batch order'},
