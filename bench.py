@@ -352,6 +352,9 @@ def bench_foam(args):
 							'84 B per neighbourhood edge + SH bytes per distinct blended site (counts every L1/L2/LDS '
 							'hit as a fetch, so it can exceed the HBM peak)',
 							'foam_infer_kernel' if lanes == 1 else 'foam_group_kernel')
+	if roofline['frac'] is not None and not fast and mode == 2 and lanes == 1:
+		roofline['limiter'] = ('not HBM: the texture data path is busy 94 % of the launch and the L2 serves 93 % of '
+							   'the gathers (profiles/foam_infer_config3_counters.md)')
 
 	cpu = None
 	if args.cpu_seconds > 0 and args.colors != 'baked':
