@@ -6,7 +6,7 @@ resident in HBM. Prints one JSON line: Mrays/s (value), ms per step, FPS at 1080
 (algorithmic bytes per launch from the kernel's own per-ray counters / the launch time measured with HIP events
 on the launch stream) and the CPU oracle timed on the host on a bounded, deterministic subset of the same rays.
 
-  python bench.py [--steps K] [--warmup W] [--colors exact|fused] [--no-reorder] [--cpu-seconds S]
+  python bench.py [--steps K] [--warmup W] [--colors exact|fused] [--no-reorder] [--no-indexed] [--cpu-seconds S]
 
 Other rows of the path, each as one JSON line of the same form (not the headline):
   --workload march    march_forward on config 5 (4M sites, 16,777,216 incoherent rays, dt = 1/512, 64 bg steps)
@@ -126,15 +126,17 @@ def timed_cpu(run, reps=3):
 	return float(np.median(times)), res
 
 
-def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray):
+def algorithmic_bytes(stats, sh_bytes, u_sh_per_ray, indexed=False):
 	"""Cache-oblivious bytes of one launch from the per-ray counters (B, 5) = samples, coloured segments, walk
 	steps, density terms, SH evaluations:
 	  56 per ray (o, d, near, far, start in; rgb, T, depth out)
 	  + 24 per sample (cell position 16 + offsets 8)
-	  + 84 per neighbourhood edge = density term (edge record 16 + nbr 4 + density record 32 + colour-conic record 32)
+	  + 84 per neighbourhood edge = density term (edge record 16 + nbr 4 + density record 32 + colour-conic record 32;
+	    80 with indexed edge records, which carry the neighbour index in the edge record)
 	  + sh_bytes per distinct site whose colour the ray blends (u_sh_per_ray, measured on traced rays)."""
 	s = stats.double()
-	return float(56 * len(s) + 24 * s[:, 0].sum() + 84 * s[:, 3].sum() + sh_bytes * u_sh_per_ray * len(s))
+	per_edge = 80 if indexed else 84
+	return float(56 * len(s) + 24 * s[:, 0].sum() + per_edge * s[:, 3].sum() + sh_bytes * u_sh_per_ray * len(s))
 
 
 def wave_balance(stats, rays_per_wave=64, cols=(('samples', 0), ('density_terms', 3))):
@@ -194,6 +196,8 @@ def main():
 	ap.add_argument('--eps-color', type=float, default=0.0, help='skip colour terms of relative weight < eps')
 	ap.add_argument('--eps-density', type=float, default=0.0, help='skip density terms below eps')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
+	ap.add_argument('--no-indexed', action='store_true',
+					help='fused colours: read the reference edge records (nbr + edge) instead of the indexed ones')
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
 	ap.add_argument('--tile-curve', default='morton', choices=['row', 'morton'],
 					help='order of the pixel tiles of a camera (row-major or Z-order of the tile coordinates)')
@@ -277,12 +281,17 @@ def bench_foam(args):
 	# camera rays in 8x8 tiles: the library's default layout (one ray per lane; 4 lanes per ray for exact colours);
 	# an incoherent batch in coherence order: 8 lanes per ray, the fastest layout on config 5 for every colour mode
 	lanes = args.lanes_per_ray or (8 if ordered else (4 if args.colors == 'exact' else 1))
+	# fused colours with one ray per lane read the indexed edge records (built once with the pack, untimed)
+	indexed = not args.no_indexed and mode == 2 and lanes == 1
+	if indexed:
+		render.index_pack(pack)
 
 	def launch(p, sel, m=mode, cut=color_cut):
 		order = ext.ray_order(o[sel], d[sel], dir_res, pos_bits) if ordered else None
 		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
 							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'],
-							 lanes=lanes, order=order)
+							 lanes=lanes, order=order,
+							 indexed=(p['edge_i'], p['attr_i']) if 'edge_i' in p and m == 2 else None)
 
 	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
 		per = B // frames
@@ -336,7 +345,7 @@ def bench_foam(args):
 		u_sh, u_rays = distinct_blended_sites(fi, pack, args_of, B, sc.sh_deg)
 		quality = None
 		log(f'distinct blended sites per ray: {u_sh:.1f} (over {u_rays} traced rays)')
-	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh)
+	abytes = algorithmic_bytes(stats.cpu(), sh_bytes, u_sh, indexed)
 	st = stats.double()
 	key = f'config{args.config}-scale{args.scale}-{args.colors}-reorder{int(not args.no_reorder)}-l{lanes}'
 	if not ordered:
@@ -345,12 +354,14 @@ def bench_foam(args):
 		key += f'-order{dir_res}x{pos_bits}'
 	if fast:
 		key += f'-sh{"16" if args.sh_half else "32"}-ec{args.eps_color:g}-ed{args.eps_density:g}'
+	if indexed:
+		key += '-idx'
 	src = source_hash('foam_infer.hip')
 	log(f'kernel source hash (foam_infer.hip): {src}; workload key {key}')
 	roofline = hbm_roofline(ms, key, src, abytes,
 							'cache-oblivious gather bytes from the per-ray counters: 56 B per ray + 24 B per sample + '
-							'84 B per neighbourhood edge + SH bytes per distinct blended site (counts every L1/L2/LDS '
-							'hit as a fetch, so it can exceed the HBM peak)',
+							f'{80 if indexed else 84} B per neighbourhood edge + SH bytes per distinct blended site '
+							'(counts every L1/L2/LDS hit as a fetch, so it can exceed the HBM peak)',
 							'foam_infer_kernel' if lanes == 1 else 'foam_group_kernel')
 	if roofline['frac'] is not None and not fast and mode == 2 and lanes == 1:
 		roofline['limiter'] = ('not HBM: the texture data path is busy 94 % of the launch and the L2 serves 93 % of '
@@ -375,6 +386,7 @@ def bench_foam(args):
 			'fps_1080p': round(frames / (ms * 1e-3), 2) if frames else None,
 			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
 			'lanes_per_ray': lanes,
+			'edge_records': 'indexed (vgr_foam_infer_indexed)' if indexed else 'reference',
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': (f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside '
 						  f'the timed step' if ordered else f'{args.tile}x{args.tile} tiles, {args.tile_curve} order'),

@@ -331,6 +331,34 @@ int vgr_ray_order(const float* o, const float* d, int64_t n_rays, int32_t dir_re
                   void* work, int64_t work_bytes, void* stream);
 
 /*
+ * Indexed edge records of a foam pack, for vgr_foam_infer_indexed. No counterpart in the reference, whose kernel
+ * reads two streams per neighbourhood entry (the float4 record and the int neighbour index, csrc/foam_infer.cu:
+ * 183-184, 212-213, 269-272). This layout carries both in one record: edge_i[e] = (p_j, the bits of j = nbr[e])
+ * and attr_i = attr with column 7 (zero padding in the reference layout) holding the bits of site k's cut-off word
+ * half2(r2_k, lam_k), which every record pointing at k carries in edge[:, 3] (the self entry's, edge[offsets[k]]).
+ *   offsets i32 (N + 1), nbr i32 (E), edge f32 (E, 4), attr f32 (N, 20) as for vgr_foam_infer
+ *   -> edge_i f32 (E, 4), attr_i f32 (N, 20); a snapshot: rebuild after changing the pack.
+ */
+int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float* edge, const float* attr,
+                        int64_t n_sites, int64_t n_edges, float* edge_i, float* attr_i, void* stream);
+
+/*
+ * vgr_foam_infer_lanes with the indexed edge records of vgr_foam_index_pack: the full fused rendering (stage 2,
+ * VGR_COLOR_FUSED) with one ray per lane (lanes_per_ray 0 or 1) reads edge_i and attr_i in place of nbr, edge and
+ * attr, one record stream per neighbourhood entry instead of two. The outputs are bit-identical to
+ * vgr_foam_infer_lanes on the same pack; every other stage, colour mode or layout runs vgr_foam_infer_lanes on the
+ * reference records unchanged. No counterpart in the reference (same function as vgr_foam_infer).
+ */
+int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
+                           const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
+                           int64_t sh_deg, const float* o, const float* d, const int32_t* start, const float* near_t,
+                           const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
+                           int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
+                           float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                           const int32_t* order, int64_t lanes_per_ray, const float* edge_i, const float* attr_i,
+                           void* stream);
+
+/*
  * vgr_grid_build without a workspace argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The scratch
  * (the cell of every site, the per-cell counters, the scan's tile sums) is a static device array of

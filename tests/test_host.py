@@ -65,6 +65,16 @@ def test_pack_self_first_csr_and_records():
 	assert np.isinf(r2h0).all()
 
 
+def test_pack_cut_word_is_per_site():
+	"""Every edge record pointing at site k carries k's cut-off word (the self entry's): the premise of the indexed
+	records, which store it once per site (attr column 7, zero padding in the reference layout)."""
+	f = Field(seed=6, n=250)
+	for pk in (f.pack(), f.pack(eps_density=1e-3, reorder=True)):
+		cut = pk['edge'][pk['offsets'][:-1], 3].view(np.int32)
+		np.testing.assert_array_equal(pk['edge'][:, 3].view(np.int32), cut[pk['nbr']])
+		assert (pk['attr'][:, 7] == 0).all()
+
+
 def test_pack_reorder_keeps_neighbour_order():
 	f = Field(seed=4, n=300)
 	a, b = f.pack(), f.pack(reorder=True)

@@ -20,6 +20,10 @@ namespace {
 
 constexpr int kBlock = 64;  // one wave64 per workgroup = one 8x8 ray tile
 constexpr int kLazy = VGR_COLOR_LAZY, kBaked = VGR_COLOR_BAKED, kFused = VGR_COLOR_FUSED;
+// Fused colours over the indexed edge records (vgr_foam_index_pack): the neighbour's index in the fourth word of its
+// edge record and its cut-off word in attr[:, 7], so a neighbour round loads no separate index. An internal mode of
+// this file: it blends exactly as kFused.
+constexpr int kFusedIdx = 3;
 
 struct FoamScene {
     const float4* __restrict__ points;  // (N) p, w unused
@@ -318,7 +322,9 @@ constexpr int sh_vec4() {
     return HALF ? sh_vec4_f16(DEG) : sh_vec4_f32(DEG);
 }
 
-// Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated.
+// Greedy walk to the lexicographic argmin of (|x - p|^2, tie order) over {c} U adj(c), repeated. IDX: the edge
+// records carry the neighbour index (indexed pack).
+template <bool IDX = false>
 __device__ int walk_to(const FoamScene& S, int c, float x0, float x1, float x2, int& steps) {
     for (int it = 0; it < kWalkCap; ++it) {
         const float4 pc = S.points[c];
@@ -327,7 +333,7 @@ __device__ int walk_to(const FoamScene& S, int c, float x0, float x1, float x2, 
         const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
         for (int e = e0 + 1; e < e1; ++e) {
             const float4 ed = S.edge[e];
-            const int k = S.nbr[e];
+            const int k = IDX ? __float_as_int(ed.w) : S.nbr[e];
             const float v0 = x0 - ed.x, v1 = x1 - ed.y, v2 = x2 - ed.z;
             const float dk = v0 * v0 + v1 * v1 + v2 * v2;
             if (dk < bd || (dk == bd && before(S, k, bk))) bd = dk, bk = k;
@@ -409,14 +415,14 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
             ed2 = S.edge[e2], k2 = S.nbr[e2];
             qn = site_rec<STAGE>(S, k1);
         } else {
-            ed = S.edge[e], k = S.nbr[e];
+            ed = S.edge[e], k = COLOR == kFusedIdx ? __float_as_int(ed.w) : S.nbr[e];
             q = site_rec<STAGE>(S, k);
         }
         if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
         if (STAGE >= 1) {
             float v0, v1, v2, r2;
             offset_of(x, ed, v0, v1, v2, r2);
-            const float2 cut = cutoffs(ed.w);
+            const float2 cut = cutoffs(COLOR == kFusedIdx ? q.q1.w : ed.w);
             if (r2 <= cut.x) {
                 R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
                 ++n_dens;
@@ -536,7 +542,8 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
-    int c = walk_to(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
+    int c = walk_to<COLOR == kFusedIdx>(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2],
+                                        walk_steps);
     CellEval E;
     eval_cell<STAGE, COLOR, HALF, DEG>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
     trace_cell<TRACE>(S, O, r, 0, c);
@@ -886,6 +893,39 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     }
 }
 
+// Indexed edge records from a pack: edge_i[e] = (p_j, the bits of j = nbr[e]) for every entry, and attr_i = attr with
+// column 7 (padding in the reference's layout) holding site k's cut-off word, which every edge record pointing at k
+// carries in the reference's layout (the self entry's, edge[offsets[k]].w). One lane per float4 written.
+__global__ void __launch_bounds__(256) index_pack_kernel(const int* __restrict__ offsets, const int* __restrict__ nbr,
+                                                         const float4* __restrict__ edge, const float* __restrict__ attr,
+                                                         int64_t n_sites, int64_t n_edges, float4* __restrict__ edge_i,
+                                                         float* __restrict__ attr_i) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n_edges) {
+        const float4 ed = edge[i];
+        edge_i[i] = make_float4(ed.x, ed.y, ed.z, __int_as_float(nbr[i]));
+        return;
+    }
+    const int64_t j = i - n_edges;  // one float of attr_i
+    if (j >= 20 * n_sites) return;
+    const int64_t k = j / 20;
+    const int col = static_cast<int>(j - 20 * k);
+    attr_i[j] = col == 7 ? edge[offsets[k]].w : attr[j];
+}
+
+// The fused blend over the indexed edge records: one ray per lane.
+template <bool HALF, bool TRACE>
+int launch_indexed(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
+    const dim3 grid(grid_for(R.n, kBlock)), block(kBlock);
+    switch (P.sh_deg) {
+        case 0: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 0, TRACE>), grid, block, 0, stream, S, P, R, O); break;
+        case 1: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 1, TRACE>), grid, block, 0, stream, S, P, R, O); break;
+        case 2: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 2, TRACE>), grid, block, 0, stream, S, P, R, O); break;
+        default: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 3, TRACE>), grid, block, 0, stream, S, P, R, O);
+    }
+    return launch_status("foam_infer_kernel (indexed edges)");
+}
+
 // lanes: 1 = one ray per lane (foam_infer_kernel), 2, 4 or 8 = a group of that many lanes per ray
 // (foam_group_kernel).
 template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
@@ -953,8 +993,13 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                const float* d, const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
                double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
-               int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream) {
+               int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream,
+               const float* edge_i = nullptr, const float* attr_i = nullptr) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
+    // the indexed edge records serve the fused blend with one ray per lane (its default layout)
+    const bool indexed = edge_i != nullptr && attr_i != nullptr && stage == 2 && color_mode == kFused &&
+                         (lanes == kDefaultLanes || lanes == 1);
+    if (indexed) lanes = 1;
     if (lanes == kDefaultLanes) lanes = default_lanes(stage, color_mode);
     VGR_REQUIRE(lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8,
                 "foam_infer: lanes_per_ray must be 1, 2, 4 or 8 (got %lld)",
@@ -976,8 +1021,8 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     const FoamScene S{reinterpret_cast<const float4*>(points),
                       offsets,
                       nbr,
-                      reinterpret_cast<const float4*>(edge),
-                      reinterpret_cast<const float4*>(attr),
+                      reinterpret_cast<const float4*>(indexed ? edge_i : edge),
+                      reinterpret_cast<const float4*>(indexed ? attr_i : attr),
                       needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
                       orig,
                       static_cast<int>(n_sites)};
@@ -989,6 +1034,11 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
     // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
     if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
+    if (indexed) {
+        const bool half = sh_half != 0;
+        if (trace != nullptr) return half ? launch_indexed<true, true>(S, P, R, O, s) : launch_indexed<false, true>(S, P, R, O, s);
+        return half ? launch_indexed<true, false>(S, P, R, O, s) : launch_indexed<false, false>(S, P, R, O, s);
+    }
     if (trace != nullptr) return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
     return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
 }
@@ -1034,4 +1084,34 @@ extern "C" int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const 
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
                            T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream);
+}
+
+extern "C" int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float* edge, const float* attr,
+                                   int64_t n_sites, int64_t n_edges, float* edge_i, float* attr_i, void* stream) {
+    VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "foam_index_pack: n_sites must be in [0, 2^31)");
+    VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_index_pack: n_edges must be in [N, 2^31)");
+    if (n_sites == 0) return VGR_OK;
+    VGR_REQUIRE(offsets && nbr && edge && attr && edge_i && attr_i, "foam_index_pack: null pointer");
+    const int64_t total = n_edges + 20 * n_sites;
+    hipLaunchKernelGGL(vgr::index_pack_kernel, dim3(vgr::grid_for(total, 256)), dim3(256), 0, vgr::as_stream(stream),
+                       offsets, nbr, reinterpret_cast<const float4*>(edge), attr, n_sites, n_edges,
+                       reinterpret_cast<float4*>(edge_i), attr_i);
+    return vgr::launch_status("index_pack_kernel");
+}
+
+extern "C" int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets,
+                                      const int32_t* nbr, const float* edge, int64_t n_edges, const float* attr,
+                                      const void* sh, int32_t sh_half, int64_t sh_deg, const float* o, const float* d,
+                                      const int32_t* start, const float* near_t, const float* far_t, int64_t n_rays,
+                                      double t_thresh, double w_thresh, double color_cut, int64_t color_mode,
+                                      int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
+                                      float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
+                                      const int32_t* order, int64_t lanes_per_ray, const float* edge_i,
+                                      const float* attr_i, void* stream) {
+    VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_indexed: trace needs trace_cap > 0");
+    VGR_REQUIRE(edge_i && attr_i, "foam_infer_indexed: edge_i and attr_i are required");
+    return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
+                           near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
+                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream,
+                           edge_i, attr_i);
 }

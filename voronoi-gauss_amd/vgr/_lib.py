@@ -58,13 +58,16 @@ SIGNATURES = {
 	'vgr_grid_build': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
 	'vgr_ray_order_work_size': [_I64],
 	'vgr_ray_order': [_P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
+	'vgr_foam_index_pack': [_P, _P, _P, _P, _I64, _I64, _P, _P, _P],
+	'vgr_foam_infer_indexed': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64,
+							   _F64, _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _P],
 	'vgr_grid_build_noalloc': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P],
 	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
 	'vgr_abi_version': [],
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 21
+ABI_VERSION = 22
 _lib = None
 
 

@@ -264,12 +264,14 @@ class _MarchExtension:
 class _FoamInferExtension:
 	@staticmethod
 	def foam_infer(points, offsets, nbr, edge, attr, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None, order=None):
+				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None, order=None, indexed=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 5) int32] (+ trace (B, trace_cap) int32, the cell of
 		every sample in original numbering, -1 past the last sample, when trace_cap > 0). lanes: None for the
 		library's default layout, else 1 (one ray per lane) or 2 / 4 / 8 (that many lanes per ray,
 		vgr_foam_infer_lanes). order: optional int32 (B,) permutation, the order in which the rays are traced
-		(ray_order); the results are the same."""
+		(ray_order); the results are the same. indexed: optional (edge_i, attr_i) from index_pack, read by the
+		fused rendering with one ray per lane in place of nbr / edge / attr (vgr_foam_infer_indexed, bit-identical
+		results); other stages, colour modes and layouts ignore it."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32), (attr, 'attr', torch.float32),
 						 (o, 'o', torch.float32), (d, 'd', torch.float32), (start, 'start', torch.int32),
@@ -306,8 +308,18 @@ class _FoamInferExtension:
 				None if baked else ptr(sh), int(half), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B,
 				float(t_thresh), float(w_thresh), float(color_cut), int(color_mode), int(stage), ptr(cp), ptr(og),
 				ptr(rgb), ptr(T), ptr(depth), ptr(stats)]
+		if indexed is not None:
+			edge_i, attr_i = indexed
+			_check(edge_i, 'edge_i', torch.float32)
+			_check(attr_i, 'attr_i', torch.float32)
+			_require(edge_i.shape == edge.shape and attr_i.shape == attr.shape,
+					 'edge_i and attr_i must have the shapes of edge and attr')
 		with torch.cuda.device(dev):
-			if lanes is not None or order is not None:
+			if indexed is not None:
+				call('vgr_foam_infer_indexed', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
+					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(edge_i), ptr(attr_i),
+					 stream_of(dev))
+			elif lanes is not None or order is not None:
 				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), stream_of(dev))
 			elif trace is None:
@@ -315,6 +327,25 @@ class _FoamInferExtension:
 			else:
 				call('vgr_foam_infer_traced', *args, ptr(trace), int(trace_cap), stream_of(dev))
 		return out
+
+
+def index_pack(offsets, nbr, edge, attr):
+	"""Indexed edge records of a foam pack (vgr_foam_index_pack) -> (edge_i (E, 4), attr_i (N, 20)): edge_i[e] =
+	(p_j, the bits of j = nbr[e]), attr_i = attr with column 7 holding site k's cut-off word edge[offsets[k], 3].
+	A snapshot of the pack: rebuild it after changing edge or attr."""
+	for t, n, dt in ((offsets, 'offsets', torch.int32), (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32),
+					 (attr, 'attr', torch.float32)):
+		_check(t, n, dt)
+	n = attr.size(0)
+	_require(attr.dim() == 2 and attr.size(1) == 20, 'attr must be (N, 20)')
+	_require(offsets.numel() == n + 1, 'offsets must be (N + 1)')
+	_require(edge.dim() == 2 and edge.size(1) == 4 and edge.size(0) == nbr.numel(), 'edge must be (E, 4)')
+	edge_i, attr_i = torch.empty_like(edge), torch.empty_like(attr)
+	dev = edge.device
+	with torch.cuda.device(dev):
+		call('vgr_foam_index_pack', ptr(offsets), ptr(nbr), ptr(edge), ptr(attr), n, nbr.numel(), ptr(edge_i),
+			 ptr(attr_i), stream_of(dev))
+	return edge_i, attr_i
 
 
 def _order(order, B, dev):

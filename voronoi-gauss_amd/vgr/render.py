@@ -313,6 +313,15 @@ def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=Fa
 
 
 @torch.no_grad()
+def index_pack(pack):
+	"""Adds the indexed edge records (ext.index_pack: edge_i, attr_i) to a GPU pack; render_rays_foam_infer then
+	renders fused colours with one record stream per neighbourhood entry, bit-identical to the reference records.
+	A snapshot: call again after changing the pack."""
+	pack['edge_i'], pack['attr_i'] = ext.index_pack(pack['offsets'], pack['nbr'], pack['edge'], pack['attr'])
+	return pack
+
+
+@torch.no_grad()
 def bake_colors(model, pack, center):
 	"""Bakes one view's site colours max(SH_k(d_k) + 1/2, 0), d_k the unit direction from `center` to site k, into
 	the packed records (attr[:, 16:19]) for the baked colour mode (render.py:228-235): vgr_bake_colors for packs on
@@ -339,7 +348,8 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 	'fused' (blended in the density pass) or 'baked' (bake_colors); eps_color > 0 skips colour terms of relative
 	weight below it. start: sites in the model's numbering. -> dict rgb (with the background), acc, depth, stats
 	(B, 5): samples, coloured segments, walk steps, density terms, SH evaluations; with trace_cap > 0 also trace
-	(B, trace_cap), each sample's cell in the model's numbering."""
+	(B, trace_cap), each sample's cell in the model's numbering. A pack with indexed records (index_pack) renders
+	fused colours through them."""
 	t_near, _, t_far = ray_bounds(o, d, near, far_radius)
 	if pack['inv'] is not None:
 		start = pack['inv'][start.long()]
@@ -349,7 +359,7 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 		o.float().contiguous(), d.float().contiguous(), start.int().contiguous(), t_near.contiguous(),
 		t_far.contiguous(), float(t_thresh), float(w_thresh), 2 * math.log(1 / eps_color) if eps_color > 0 else math.inf,
 		_COLOR_MODES[colors], int(stage), empty if cap is None else cap.int().contiguous(), pack['orig'],
-		trace_cap=trace_cap)
+		trace_cap=trace_cap, indexed=(pack['edge_i'], pack['attr_i']) if 'edge_i' in pack else None)
 	fg, T, depth, stats = out[:4]
 	res = {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth, 'stats': stats}
 	if trace_cap > 0:
