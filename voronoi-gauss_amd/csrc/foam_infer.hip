@@ -81,12 +81,13 @@ __device__ __forceinline__ float2 cutoffs(float w) {
     return make_float2(static_cast<float>(lo), static_cast<float>(hi));
 }
 
-// ------------------------------------------------------------------ field arithmetic (contracts to FMA)
-// The density, colour and blend arithmetic below may fuse a product and a sum into one FMA, which rounds once
-// where the CPU oracle rounds twice: each term moves by at most an ulp of its magnitude, and the colours and
-// transmittances by a few ulps of 1 (about 1e-6), well inside the 1e-4 parity bar. The traversal arithmetic (walk
-// distances, exit planes) is never contracted, so the visited cells stay bit-exact.
-#pragma clang fp contract(fast)
+// ------------------------------------------------------------------ field arithmetic (explicit FMA)
+// The density, colour and blend arithmetic below fuses chosen products and sums into one FMA (fmaf), which rounds
+// once where the CPU oracle rounds twice: each term moves by at most an ulp of its magnitude, and the colours and
+// transmittances by a few ulps of 1 (about 1e-6), well inside the 1e-4 parity bar. The fusions are written out, not
+// left to the compiler's contraction, so every kernel of this file that composes these terms rounds them the same
+// way whatever the surrounding code and register schedule. The traversal arithmetic (walk distances, exit planes)
+// is never fused, so the visited cells stay bit-exact.
 
 __device__ __forceinline__ void blend_add(Blend& B, float m, float r, float g, float b) {
     if (m < B.m) {
@@ -94,33 +95,36 @@ __device__ __forceinline__ void blend_add(Blend& B, float m, float r, float g, f
         B.a *= s, B.r *= s, B.g *= s, B.b *= s, B.m = m;
     }
     const float w = fexp(-0.5f * (m - B.m));
-    B.a += w, B.r += w * r, B.g += w * g, B.b += w * b;
+    B.a += w, B.r = fmaf(w, r, B.r), B.g = fmaf(w, g, B.g), B.b = fmaf(w, b, B.b);
 }
 
+// (vx, vy, vz) A (vx, vy, vz)^T for the symmetric conic A = (p.x p.y p.z / . p.w q.x / . . q.y)
 __device__ __forceinline__ float maha_f(const float4& p, const float4& q, float vx, float vy, float vz) {
-    return p.x * vx * vx + p.w * vy * vy + q.y * vz * vz + 2.f * (p.y * vx * vy + p.z * vx * vz + q.x * vy * vz);
+    const float diag = fmaf(p.x * vx, vx, fmaf(p.w * vy, vy, q.y * vz * vz));
+    const float cross = fmaf(p.y * vx, vy, fmaf(p.z * vx, vz, q.x * vy * vz));
+    return fmaf(2.f, cross, diag);
 }
 
 // Sample point o + t d, used by the field terms only (the traversal never reads it).
 __device__ __forceinline__ void sample_point(const float (&o)[3], const float (&d)[3], float t, float (&x)[3]) {
-    x[0] = o[0] + t * d[0], x[1] = o[1] + t * d[1], x[2] = o[2] + t * d[2];
+    x[0] = fmaf(t, d[0], o[0]), x[1] = fmaf(t, d[1], o[1]), x[2] = fmaf(t, d[2], o[2]);
 }
 
 __device__ __forceinline__ void offset_of(const float (&x)[3], const float4& p, float& v0, float& v1, float& v2,
                                           float& r2) {
     v0 = x[0] - p.x, v1 = x[1] - p.y, v2 = x[2] - p.z;
-    r2 = v0 * v0 + v1 * v1 + v2 * v2;
+    r2 = fmaf(v0, v0, fmaf(v1, v1, v2 * v2));
 }
 
 // rho_k G_k(x) from the density record (q0 = xx xy xz yy, q1 = yz zz min(raw, 30) 0).
 __device__ __forceinline__ float density_term(const float4& q0, const float4& q1, float v0, float v1, float v2) {
-    return fexp(q1.z - 0.5f * maha_f(q0, q1, v0, v1, v2));
+    return fexp(fmaf(-0.5f, maha_f(q0, q1, v0, v1, v2), q1.z));
 }
 
 __device__ __forceinline__ float weight_of(float m, float mmin) { return fexp(-0.5f * (m - mmin)); }
 
 __device__ __forceinline__ void accumulate(float& A, float& r, float& g, float& bl, float w, const float (&c)[3]) {
-    A += w, r += w * c[0], g += w * c[1], bl += w * c[2];
+    A += w, r = fmaf(w, c[0], r), g = fmaf(w, c[1], g), bl = fmaf(w, c[2], bl);
 }
 
 // Adds blocks q0 .. q0 + 3 (those below nv) of a site's SH coefficients (fp32, or fp16 pairs) to c: the colour
@@ -138,17 +142,16 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
             for (int u = 0; u < 4; ++u) {
                 const float2 p = cutoffs(fv[u]);
                 const int i0 = 8 * q + 2 * u, i1 = i0 + 1;
-                c[i0 % 3] += b[i0 / 3] * p.x;
-                c[i1 % 3] += b[i1 / 3] * p.y;
+                c[i0 % 3] = fmaf(b[i0 / 3], p.x, c[i0 % 3]);
+                c[i1 % 3] = fmaf(b[i1 / 3], p.y, c[i1 % 3]);
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) c[(4 * q + u) % 3] += b[(4 * q + u) / 3] * fv[u];
+            for (int u = 0; u < 4; ++u) c[(4 * q + u) % 3] = fmaf(b[(4 * q + u) / 3], fv[u], c[(4 * q + u) % 3]);
         }
     }
 }
 
-#pragma clang fp contract(off)
 // ------------------------------------------------------------------ traversal arithmetic (never contracted)
 
 // Colour blocks of site k for this ray come through the wave-shared LDS cache of SH coefficient blocks: SLOTS
@@ -406,6 +409,11 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
         k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
         q = site_rec<STAGE>(S, k);
     }
+    // Indexed records: the edge record of e + 1 is requested in round e, after the density term and before the
+    // colour lookup, whose latency then covers it; round e + 1 starts with its neighbour index in hand. (Issued at
+    // the top of the round it spills the loop's registers; at its end it arrives too late to help.)
+    float4 edn;
+    if constexpr (COLOR == kFusedIdx) edn = S.edge[e0];
     for (int e = e0; e < e1; ++e) {
         float4 ed2;
         int k2;
@@ -414,8 +422,11 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
             const int e2 = min(e + 2, last);
             ed2 = S.edge[e2], k2 = S.nbr[e2];
             qn = site_rec<STAGE>(S, k1);
+        } else if constexpr (COLOR == kFusedIdx) {
+            ed = edn, k = __float_as_int(ed.w);
+            q = site_rec<STAGE>(S, k);
         } else {
-            ed = S.edge[e], k = COLOR == kFusedIdx ? __float_as_int(ed.w) : S.nbr[e];
+            ed = S.edge[e], k = S.nbr[e];
             q = site_rec<STAGE>(S, k);
         }
         if (want_exit && e > e0) exit_candidate(S, pc, ed, k, o, d, R);
@@ -427,6 +438,7 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                 R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
                 ++n_dens;
             }
+            if constexpr (COLOR == kFusedIdx) edn = S.edge[min(e + 1, last)];
             if (STAGE >= 2) {
                 const float lb = r2 * cut.y;
                 if (BLEND) {

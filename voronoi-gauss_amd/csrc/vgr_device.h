@@ -3,8 +3,8 @@
 // Arithmetic contract: every translation unit is compiled with -ffp-contract=off and IEEE fp32 division, so
 // the products and sums that decide a walk or an exit face are rounded exactly as written, the same way the
 // CPU oracle rounds them. Two things differ from the oracle by ulps only: exp (device exp2-based, against the
-// CPU's libm), and the field arithmetic of foam_infer.hip (density, colour, blend), which a
-// `#pragma clang fp contract(fast)` region lets fuse into FMA. Neither decides which cell a ray enters next;
+// CPU's libm), and the field arithmetic of foam_infer.hip (density, colour, blend), which fuses chosen products
+// and sums into explicit FMAs (fmaf). Neither decides which cell a ray enters next;
 // both can move a weight or transmittance across a threshold (w_thresh, t_thresh) when it is within ulps of it.
 #pragma once
 
