@@ -409,11 +409,17 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
         k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
         q = site_rec<STAGE>(S, k);
     }
-    // Indexed records: the edge record of e + 1 is requested in round e, after the density term and before the
-    // colour lookup, whose latency then covers it; round e + 1 starts with its neighbour index in hand. (Issued at
-    // the top of the round it spills the loop's registers; at its end it arrives too late to help.)
+    // Fused blend: the edge record of e + 1 (and, on the reference records, its neighbour index) is requested in
+    // round e, after the density term and before the colour lookup, whose latency then covers it; round e + 1
+    // starts with its neighbour index in hand. (Issued at the top of the round it spills the loop's registers; at
+    // its end it arrives too late to help. Baked colours, with no lookup to cover it, run slower with it.)
+    constexpr bool IDX = COLOR == kFusedIdx, PREF = STAGE >= 2 && (COLOR == kFused || IDX);
     float4 edn;
-    if constexpr (COLOR == kFusedIdx) edn = S.edge[e0];
+    int kn = 0;
+    if constexpr (PREF) {
+        edn = S.edge[e0];
+        if constexpr (!IDX) kn = S.nbr[e0];
+    }
     for (int e = e0; e < e1; ++e) {
         float4 ed2;
         int k2;
@@ -422,8 +428,8 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
             const int e2 = min(e + 2, last);
             ed2 = S.edge[e2], k2 = S.nbr[e2];
             qn = site_rec<STAGE>(S, k1);
-        } else if constexpr (COLOR == kFusedIdx) {
-            ed = edn, k = __float_as_int(ed.w);
+        } else if constexpr (PREF) {
+            ed = edn, k = IDX ? __float_as_int(ed.w) : kn;
             q = site_rec<STAGE>(S, k);
         } else {
             ed = S.edge[e], k = S.nbr[e];
@@ -438,7 +444,11 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                 R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
                 ++n_dens;
             }
-            if constexpr (COLOR == kFusedIdx) edn = S.edge[min(e + 1, last)];
+            if constexpr (PREF) {
+                const int en = min(e + 1, last);
+                edn = S.edge[en];
+                if constexpr (!IDX) kn = S.nbr[en];
+            }
             if (STAGE >= 2) {
                 const float lb = r2 * cut.y;
                 if (BLEND) {
