@@ -68,15 +68,16 @@ class Stated:
 		k = max(1, self.B // n)
 		return np.arange(k // 2, self.B, k, dtype=np.int64)[:n]
 
-	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0):
-		"""GPU foam_infer over the selected rays (all by default) -> dict of numpy arrays."""
+	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0, indexed=None):
+		"""GPU foam_infer over the selected rays (all by default) -> dict of numpy arrays; indexed: the records of
+		ext.index_pack, read in place of the reference records."""
 		pick = (lambda a: a) if sel is None else (lambda a: a[sel])
 		p = self.pack
 		empty = torch.empty(0, dtype=torch.int32, device=self.dev)
 		out = ext.foam_infer_extension().foam_infer(
 			p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], self.sc.sh_deg, self.t(pick(self.o)),
 			self.t(pick(self.d)), self.t(pick(self.start)), self.t(pick(self.near)), self.t(pick(self.far)),
-			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap)
+			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap, indexed=indexed)
 		torch.cuda.synchronize()
 		res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
 		res.setdefault('trace', None)
@@ -137,6 +138,21 @@ def test_foam_full_workload(stated):
 			'rays hitting the 4096-step walk cap': int((full['stats'][:, 2] >= WALK_CAP).sum())}
 	progress(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}')
 	progress(f'[stated sizes] config {s.config} ray-length spread: {spread(full["stats"])}')
+
+
+def test_foam_indexed_records_full_workload(stated):
+	"""The bench's default path at the stated size: fused colours through the indexed edge records over the whole
+	workload, bit-identical on every ray to the reference records (which the oracle checks above)."""
+	s = stated
+	p = s.pack
+	idx = ext.index_pack(p['offsets'], p['nbr'], p['edge'], p['attr'])
+	a, b = s.foam(), s.foam(indexed=idx)
+	del idx
+	for k in ('rgb', 'T', 'depth'):
+		np.testing.assert_array_equal(a[k].view(np.int32), b[k].view(np.int32), err_msg=k)
+	np.testing.assert_array_equal(a['stats'], b['stats'])
+	progress(f'[stated sizes] config {s.config}: indexed records bit-identical to the reference records on all '
+			 f'{s.B} rays')
 
 
 def test_foam_traces_and_exact_colours(stated):
