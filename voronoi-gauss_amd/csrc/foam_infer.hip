@@ -392,11 +392,25 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                           const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
                           bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    const float4 pc = S.points[c];
-    float x[3];
-    sample_point(o, d, t, x);
+    // Fused blend: the edge record of e + 1 (and, on the reference records, its neighbour index) is requested in
+    // round e, after the density term and before the colour lookup, whose latency then covers it; round e + 1
+    // starts with its neighbour index in hand. (Issued at the top of the round it spills the loop's registers; at
+    // its end it arrives too late to help. Baked colours, with no lookup to cover it, run slower with it.) The
+    // first record requested is the cell's own (self-first), which holds its position: on the reference records
+    // the cell position is taken from it (fewer spilled VGPRs there; on the indexed records the separate load is
+    // faster).
+    constexpr bool IDX = COLOR == kFusedIdx, PREF = STAGE >= 2 && (COLOR == kFused || IDX);
     const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
     const int last = e1 - 1;
+    float4 edn;
+    int kn = 0;
+    if constexpr (PREF) {
+        edn = S.edge[e0];
+        if constexpr (!IDX) kn = S.nbr[e0];
+    }
+    const float4 pc = PREF && !IDX ? edn : S.points[c];
+    float x[3];
+    sample_point(o, d, t, x);
     R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
     blend_init(R.B);
     constexpr bool PIPE = Tune<COLOR>::pipelined;
@@ -408,17 +422,6 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
         ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
         k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
         q = site_rec<STAGE>(S, k);
-    }
-    // Fused blend: the edge record of e + 1 (and, on the reference records, its neighbour index) is requested in
-    // round e, after the density term and before the colour lookup, whose latency then covers it; round e + 1
-    // starts with its neighbour index in hand. (Issued at the top of the round it spills the loop's registers; at
-    // its end it arrives too late to help. Baked colours, with no lookup to cover it, run slower with it.)
-    constexpr bool IDX = COLOR == kFusedIdx, PREF = STAGE >= 2 && (COLOR == kFused || IDX);
-    float4 edn;
-    int kn = 0;
-    if constexpr (PREF) {
-        edn = S.edge[e0];
-        if constexpr (!IDX) kn = S.nbr[e0];
     }
     for (int e = e0; e < e1; ++e) {
         float4 ed2;
