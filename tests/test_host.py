@@ -2,6 +2,7 @@
 seeded scenes and cameras. Closed forms and format invariants; no GPU."""
 
 import math
+import os
 
 import numpy as np
 import torch
@@ -174,3 +175,18 @@ def test_delaunay_graph_matches_scipy_and_drops_duplicates():
 	q = np.concatenate([p, p[:3]])  # duplicates are left out by Qhull and dropped
 	pts, idx, off, adj = delaunay_graph(q)
 	assert len(pts) <= 200 and (np.diff(off) > 0).all()
+
+
+def test_profiles_bind_the_default_workloads_to_these_sources():
+	"""The DRAM traffic that bench.py's roofline reads for its two default workloads (config 3 foam_infer, config 5
+	march) comes from a committed rocprofv3 profile measured on these kernel sources; a kernel change without a new
+	profile would leave the bench's roofline empty."""
+	import sys
+	root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+	if root not in sys.path:
+		sys.path.insert(0, root)
+	import bench
+	for key, src in (('config3-scale1.0-fused-reorder1-l1-tiles8morton-idx', bench.source_hash('foam_infer.hip')),
+					 ('config5-scale1.0-march-l1-order4x8', bench.source_hash('march.hip', 'order.hip'))):
+		traffic, where = bench.measured_traffic(key, src)
+		assert traffic is not None and traffic > 0, where
