@@ -741,9 +741,18 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
     const int e0 = S.offsets[c], e1 = S.offsets[c + 1];
     R.sigma = 0.f, R.mmin = kInf, R.t_exit = kInf, R.next = INT_MAX;
     blend_init(R.B);
+    // Fused blend: the lane's next edge record and neighbour index are requested mid-round, as in eval_cell
+    // (indices clamped to the cell: a lane without a further edge reads the cell's last one).
+    constexpr bool PREF = STAGE >= 2 && COLOR == kFused;
+    float4 edn;
+    int kn = 0;
+    if constexpr (PREF) {
+        const int ef = min(e0 + g, e1 - 1);
+        edn = S.edge[ef], kn = S.nbr[ef];
+    }
     for (int e = e0 + g; e < e1; e += G) {
-        const float4 ed = S.edge[e];
-        const int k = S.nbr[e];
+        const float4 ed = PREF ? edn : S.edge[e];
+        const int k = PREF ? kn : S.nbr[e];
         const SiteRec q = site_rec<STAGE>(S, k);
         if (want_exit && e > e0) {
             const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
@@ -761,6 +770,10 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
             if (r2 <= cut.x) {
                 R.sigma += density_term(q.q0, q.q1, v0, v1, v2);
                 ++n_dens;
+            }
+            if constexpr (PREF) {
+                const int en = min(e + G, e1 - 1);
+                edn = S.edge[en], kn = S.nbr[en];
             }
             if (STAGE >= 2) {
                 const float lb = r2 * cut.y;
