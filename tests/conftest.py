@@ -55,8 +55,8 @@ def pytest_sessionfinish(session, exitstatus):
 
 
 def progress(msg):
-	"""A progress line on stdout and in gpurun_out/stated_sizes_progress.log: a wait of minutes for Qhull then
-	still shows activity when pytest captures the output."""
+	"""A progress line on stdout and in stated_sizes_progress.log under the run's output folder: a wait of minutes
+	for Qhull then still shows activity when pytest captures the output."""
 	print(msg, flush=True)
 	out = os.path.join(ROOT, 'gpurun_out')
 	os.makedirs(out, exist_ok=True)
