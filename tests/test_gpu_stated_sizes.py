@@ -68,16 +68,19 @@ class Stated:
 		k = max(1, self.B // n)
 		return np.arange(k // 2, self.B, k, dtype=np.int64)[:n]
 
-	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0, indexed=None):
+	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0, indexed=None, lanes=None,
+			 order=None):
 		"""GPU foam_infer over the selected rays (all by default) -> dict of numpy arrays; indexed: the records of
-		ext.index_pack, read in place of the reference records."""
+		ext.index_pack, read in place of the reference records; lanes, order: the ray layout and processing order
+		(vgr_foam_infer_lanes)."""
 		pick = (lambda a: a) if sel is None else (lambda a: a[sel])
 		p = self.pack
 		empty = torch.empty(0, dtype=torch.int32, device=self.dev)
 		out = ext.foam_infer_extension().foam_infer(
 			p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], self.sc.sh_deg, self.t(pick(self.o)),
 			self.t(pick(self.d)), self.t(pick(self.start)), self.t(pick(self.near)), self.t(pick(self.far)),
-			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap, indexed=indexed)
+			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap, indexed=indexed,
+			lanes=lanes, order=order)
 		torch.cuda.synchronize()
 		res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
 		res.setdefault('trace', None)
@@ -134,6 +137,8 @@ def test_foam_full_workload(stated):
 		go = s.foam(diff, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
 		ro = s.oracle(diff, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
 		np.testing.assert_array_equal(go['trace'], ro['trace'])
+	if s.config == 5:  # the bench's layout of this batch
+		check_config5_bench_layout(s, sel, r)
 	caps = {'rays hitting the 8192-cell cap': int((full['stats'][:, 0] > MAX_CELLS).sum()),
 			'rays hitting the 4096-step walk cap': int((full['stats'][:, 2] >= WALK_CAP).sum())}
 	progress(f'[stated sizes] config {s.config} safety caps over all {s.B} rays: {caps}')
@@ -153,6 +158,23 @@ def test_foam_indexed_records_full_workload(stated):
 	np.testing.assert_array_equal(a['stats'], b['stats'])
 	progress(f'[stated sizes] config {s.config}: indexed records bit-identical to the reference records on all '
 			 f'{s.B} rays')
+
+
+def check_config5_bench_layout(s, sel, r):
+	"""Config 5's batch as the bench renders it: 8 lanes per ray in the coherent order of vgr_ray_order (8x8
+	direction bins, 7-bit origins), over the whole batch; against the oracle's rays `sel` (results r), and the same
+	cells and statistics as the one-ray-per-lane kernel with the thresholds off."""
+	order = ext.ray_order(s.t(s.o), s.t(s.d), 8, 7)
+	g = rows(s.foam(lanes=8, order=order), sel)
+	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
+	assert psnr(g['rgb'], r['rgb']) >= 60.0
+	few = sel[::8]
+	g8 = s.foam(few, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1, lanes=8)
+	g1 = s.foam(few, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1, lanes=1)
+	np.testing.assert_array_equal(g8['stats'], g1['stats'])
+	np.testing.assert_array_equal(g8['trace'], g1['trace'])
+	progress(f'[stated sizes] config 5, 8 lanes per ray in coherent order over {s.B} rays: max |rgb| '
+			 f'{np.abs(g["rgb"] - r["rgb"]).max():.2e} on {len(sel)} oracle rays; cells identical to one ray per lane')
 
 
 def test_foam_traces_and_exact_colours(stated):
