@@ -190,3 +190,13 @@ def test_profiles_bind_the_default_workloads_to_these_sources():
 					 ('config5-scale1.0-march-l1-order4x8', bench.source_hash('march.hip', 'order.hip'))):
 		traffic, where = bench.measured_traffic(key, src)
 		assert traffic is not None and traffic > 0, where
+
+
+def test_bench_refuses_more_than_one_gpu():
+	"""bench.py measures one GPU: --gpus N > 1 exits non-zero with a message, before touching a device."""
+	import subprocess
+	import sys
+	root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+	p = subprocess.run([sys.executable, os.path.join(root, 'bench.py'), '--gpus', '2'], capture_output=True, text=True,
+					   cwd=root, timeout=120)
+	assert p.returncode != 0 and 'one GPU' in (p.stdout + p.stderr)
