@@ -4,7 +4,18 @@
 // Semantics follow csrc/vgf.cu of the reference: walk_kernel :51-79 (strict <, so the first closer neighbour
 // in CSR order wins), gauss_local :98-119 and density_forward_kernel :163-177, sh_eval/unit_dir/
 // color_forward_kernel :230-282 (online softmax), conic_local/conic_forward_kernel :350-380.
-// One work item (ray, sample or site) per lane, 256-lane workgroups; all loops are over <= ~60 neighbours.
+//
+// MI355X layouts:
+// - walk: a group of 16 lanes (one DPP row) per ray. The group holds the neighbourhood of the ray's current site in
+//   registers (lane g: entries g, g + 16, g + 32, g + 48) and streams the ray's samples through it: a sample that
+//   stays in the site costs a distance per held entry and a four-step row butterfly, no memory access; only a move
+//   reloads. The first-found rule of the sequential scan is the lexicographic minimum of (distance, CSR position),
+//   which the butterfly computes in any order, so sites and step counts are those of a sequential scan.
+// - density: one sample per lane over per-site Gaussian records built once per call (gauss_pack_kernel).
+// - colour: a group of 4 lanes per sample (16 samples per wave): lane g blends the entries g, g + 4, ... of the
+//   neighbourhood into a partial online softmax (its own running minimum), and the group merges the partials in a
+//   butterfly; four lanes keep four neighbours' SH rows in flight where one lane per sample keeps one.
+// - conic: one site per lane.
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -25,45 +36,114 @@ struct Gauss {
     const float4* __restrict__ quat;      // (N) w x y z, not normalised
 };
 
-__device__ __forceinline__ float dist2(const float* __restrict__ p, int i, float x, float y, float z) {
-    const float dx = x - p[3 * static_cast<int64_t>(i)], dy = y - p[3 * static_cast<int64_t>(i) + 1],
-                dz = z - p[3 * static_cast<int64_t>(i) + 2];
-    return dx * dx + dy * dy + dz * dz;
+// ------------------------------------------------------------------ walk: 16 lanes per ray
+constexpr int kWalkLanes = 16;  // one DPP row per ray, 4 rays per wave
+constexpr int kWalkHeld = 4;    // neighbourhood entries each lane keeps in registers (64 per group)
+
+// Squared distance from x to p, summed in the reference's order (no contraction: bit-exact walks).
+__device__ __forceinline__ float sq_dist(float px, float py, float pz, const float (&x)[3]) {
+    const float a = x[0] - px, b = x[1] - py, c = x[2] - pz;
+    return a * a + b * b + c * c;
 }
 
+// Candidate (d, e, k): keeps the lexicographic minimum of (distance, CSR position), i.e. the entry a sequential scan
+// with a strict < would keep.
+__device__ __forceinline__ void keep_first_closest(float d, int e, int k, float& bd, int& be, int& bk) {
+    if (d < bd || (d == bd && e < be)) bd = d, be = e, bk = k;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void first_closest_step(float& bd, int& be, int& bk) {
+    keep_first_closest(row_perm<CTRL>(bd), row_perm<CTRL>(be), row_perm<CTRL>(bk), bd, be, bk);
+}
+
+// The neighbourhood of one site as a group of 16 lanes holds it: lane g keeps entries g + 16 j (j < kWalkHeld) as
+// (position, site); entries beyond 64 stay in memory and are read by the same lanes in every scan.
+struct HeldCell {
+    int site, e0, e1;
+    float px[kWalkHeld], py[kWalkHeld], pz[kWalkHeld];
+    int k[kWalkHeld];
+};
+
+__device__ __forceinline__ void hold_cell(const Graph& g, int c, int lane, HeldCell& H) {
+    H.site = c;
+    H.e0 = g.offsets[c], H.e1 = g.offsets[c + 1];
+#pragma unroll
+    for (int j = 0; j < kWalkHeld; ++j) {
+        const int e = H.e0 + lane + kWalkLanes * j;
+        H.k[j] = e < H.e1 ? g.adj[e] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kWalkHeld; ++j) {
+        const int64_t q = 3 * static_cast<int64_t>(H.k[j] >= 0 ? H.k[j] : c);
+        H.px[j] = g.points[q], H.py[j] = g.points[q + 1], H.pz[j] = g.points[q + 2];
+    }
+}
+
+// One scan of the held site's neighbourhood for the point x: the site a sequential strict-< scan started from
+// best_d would move to (best_d updated), or the held site itself.
+__device__ __forceinline__ int scan_held(const Graph& g, const HeldCell& H, int lane, const float (&x)[3],
+                                         float& best_d) {
+    float bd = best_d;
+    int be = -1, bk = H.site;  // staying wins ties: a neighbour must be strictly closer
+#pragma unroll
+    for (int j = 0; j < kWalkHeld; ++j)
+        if (H.k[j] >= 0) keep_first_closest(sq_dist(H.px[j], H.py[j], H.pz[j], x), H.e0 + lane + kWalkLanes * j,
+                                            H.k[j], bd, be, bk);
+    for (int e = H.e0 + lane + kWalkLanes * kWalkHeld; e < H.e1; e += kWalkLanes) {  // cells beyond 64 entries
+        const int q = g.adj[e];
+        const int64_t q3 = 3 * static_cast<int64_t>(q);
+        keep_first_closest(sq_dist(g.points[q3], g.points[q3 + 1], g.points[q3 + 2], x), e, q, bd, be, bk);
+    }
+    first_closest_step<kXor1>(bd, be, bk);
+    first_closest_step<kXor2>(bd, be, bk);
+    first_closest_step<kHalfMirror>(bd, be, bk);
+    first_closest_step<kMirror>(bd, be, bk);
+    best_d = bd;
+    return bk;
+}
+
+// Every sample of ray r (S sorted parameters in z) walked from the previous sample's site; the group's lanes hold
+// the same values throughout, lane g stores the sites of samples g, g + 16, ... (16 consecutive ints per store).
 __global__ void __launch_bounds__(kBlock)
-    walk_kernel(Graph g, const float* __restrict__ o, const float* __restrict__ d, const float* __restrict__ z,
-                const int* __restrict__ start, int64_t B, int S, int* __restrict__ site, int* __restrict__ steps) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (r >= B) return;
-    const float ox = o[3 * r], oy = o[3 * r + 1], oz = o[3 * r + 2];
-    const float dx = d[3 * r], dy = d[3 * r + 1], dz = d[3 * r + 2];
-    int cur = start[r];
-    if (cur < 0 || cur >= g.n_sites) {  // invalid start: every sample unresolved
-        for (int s = 0; s < S; ++s) site[r * S + s] = -1;
-        if (steps != nullptr) steps[r] = 0;
+    walk_group_kernel(Graph g, const float* __restrict__ o, const float* __restrict__ d, const float* __restrict__ z,
+                      const int* __restrict__ start, int64_t B, int S, int* __restrict__ site,
+                      int* __restrict__ steps) {
+    const int lane = static_cast<int>(threadIdx.x) % kWalkLanes;
+    const int64_t r = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) / kWalkLanes;
+    if (r >= B) return;  // whole groups leave together
+    int* out = site + r * S;
+    const int first = start[r];
+    if (first < 0 || first >= g.n_sites) {  // invalid start: every sample unresolved
+        for (int s = lane; s < S; s += kWalkLanes) out[s] = -1;
+        if (steps != nullptr && lane == 0) steps[r] = 0;
         return;
     }
-    int total = 0;
+    const float org[3] = {o[3 * r], o[3 * r + 1], o[3 * r + 2]}, dir[3] = {d[3 * r], d[3 * r + 1], d[3 * r + 2]};
+    HeldCell H;
+    hold_cell(g, first, lane, H);
+    int64_t cur3 = 3 * static_cast<int64_t>(first);
+    float cx = g.points[cur3], cy = g.points[cur3 + 1], cz = g.points[cur3 + 2];
+    int moves = 0, mine = -1;
     for (int s = 0; s < S; ++s) {
         const float t = z[r * S + s];
-        const float x = ox + t * dx, y = oy + t * dy, w = oz + t * dz;
-        float best_d = dist2(g.points, cur, x, y, w);
+        const float x[3] = {org[0] + t * dir[0], org[1] + t * dir[1], org[2] + t * dir[2]};
+        float best_d = sq_dist(cx, cy, cz, x);
         for (int it = 0; it < kWalkCap; ++it) {
-            int best = cur;
-            const int e1 = g.offsets[cur + 1];
-            for (int e = g.offsets[cur]; e < e1; ++e) {
-                const int q = g.adj[e];
-                const float dq = dist2(g.points, q, x, y, w);
-                if (dq < best_d) best_d = dq, best = q;
-            }
-            if (best == cur) break;
-            cur = best;
-            ++total;
+            const int next = scan_held(g, H, lane, x, best_d);
+            if (next == H.site) break;
+            ++moves;
+            hold_cell(g, next, lane, H);
+            cur3 = 3 * static_cast<int64_t>(next);
+            cx = g.points[cur3], cy = g.points[cur3 + 1], cz = g.points[cur3 + 2];
         }
-        site[r * S + s] = cur;
+        const int slot = s % kWalkLanes;
+        if (slot == lane) mine = H.site;
+        if (slot == kWalkLanes - 1 || s == S - 1) {
+            if (lane <= slot) out[s - slot + lane] = mine;
+        }
     }
-    if (steps != nullptr) steps[r] = total;
+    if (steps != nullptr && lane == 0) steps[r] = moves;
 }
 
 // Mahalanobis distance of (x, y, z) to Gaussian i, with the inverse variances scaled by inv_mult2.
@@ -180,106 +260,100 @@ __global__ void __launch_bounds__(kBlock)
     sigma[t] = s;
 }
 
-template <int NV>
-__device__ __forceinline__ void sh_eval_n(const float4* __restrict__ sh, int k, const float (&b)[16], int nb,
-                                          float (&c)[3]) {
-    const float4* s = sh + 12 * static_cast<int64_t>(k);
+// ------------------------------------------------------------------ colour: 4 lanes per sample
+constexpr int kColourLanes = 4;
+
+// Partial online softmax of a lane's share of the neighbourhood: running minimum m of the Mahalanobis distances, and
+// sum a of exp(-(m_k - m) / 2) and of those weights times the clamped colours.
+struct Softmax {
+    float m, a, r, g, b;
+};
+
+__device__ __forceinline__ void softmax_add(Softmax& P, float mk, const float (&c)[3]) {
+    if (mk < P.m) {  // rescale to the new minimum (the first term: everything is 0 and exp(-inf) = 0)
+        const float f = fexp(-0.5f * (P.m - mk));
+        P.a *= f, P.r *= f, P.g *= f, P.b *= f;
+        P.m = mk;
+    }
+    const float w = fexp(-0.5f * (mk - P.m));
+    P.a += w;
+    P.r += w * fmaxf(c[0], 0.f), P.g += w * fmaxf(c[1], 0.f), P.b += w * fmaxf(c[2], 0.f);
+}
+
+// Merges the partial of the lane CTRL pairs this one with: both rescaled to the smaller minimum, products rounded
+// separately so that both lanes of a pair compute the same bits.
+template <int CTRL>
+__device__ __forceinline__ void softmax_merge(Softmax& P) {
+    const Softmax Q{row_perm<CTRL>(P.m), row_perm<CTRL>(P.a), row_perm<CTRL>(P.r), row_perm<CTRL>(P.g),
+                    row_perm<CTRL>(P.b)};
+    const float m = fminf(P.m, Q.m);
+    const float fp = fexp(-0.5f * (P.m - m)), fq = fexp(-0.5f * (Q.m - m));
+    const float a1 = P.a * fp, a2 = Q.a * fq, r1 = P.r * fp, r2 = Q.r * fq;
+    const float g1 = P.g * fp, g2 = Q.g * fq, b1 = P.b * fp, b2 = Q.b * fq;
+    P.m = m, P.a = a1 + a2, P.r = r1 + r2, P.g = g1 + g2, P.b = b1 + b2;
+}
+
+// SH_k(d) + 1/2 over the coefficients of degree <= DEG (coefficient j of channel c at 3 j + c of the row).
+template <int DEG>
+__device__ __forceinline__ void sh_colour(const float4* __restrict__ row, const float (&b)[16], float (&c)[3]) {
+    constexpr int nb = (DEG + 1) * (DEG + 1), nv = sh_vec4_f32(DEG);
+    float4 f[nv];
+#pragma unroll
+    for (int q = 0; q < nv; ++q) f[q] = row[q];  // the whole row in flight before the first product
     c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
-    for (int q = 0; q < NV; ++q) {
-        const float4 f = s[q];
-        const float fv[4] = {f.x, f.y, f.z, f.w};
+    for (int q = 0; q < nv; ++q) {
+        const float fv[4] = {f[q].x, f[q].y, f[q].z, f[q].w};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int i = 4 * q + u;
-            if (i / 3 < nb) c[i % 3] += b[i / 3] * fv[u];
+            const int j = 4 * q + u;
+            if (j / 3 < nb) c[j % 3] += b[j / 3] * fv[u];
         }
     }
 }
 
-template <int DEG>
+// Colour at sample t: the normalised blend of max(SH_k(d) + 1/2, 0) over k in {i} U adj(i) with weights
+// exp(-(m_k - m_min) / 2). REC: m_k from the per-site records (gauss_pack_kernel), else from (log_scale, quat).
+template <int DEG, bool REC>
 __global__ void __launch_bounds__(kBlock)
-    color_forward_kernel(Graph g, Gauss H, const float4* __restrict__ sh, const float* __restrict__ x,
-                         const float* __restrict__ dirs, const int* __restrict__ site, int64_t m,
-                         float* __restrict__ rgb) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (t >= m) return;
+    colour_group_kernel(Graph g, Gauss H, const float4* __restrict__ rec, const float4* __restrict__ sh,
+                        const float* __restrict__ x, const float* __restrict__ dirs, const int* __restrict__ site,
+                        int64_t m, float* __restrict__ rgb) {
+    const int lane = static_cast<int>(threadIdx.x) % kColourLanes;
+    const int64_t t = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) / kColourLanes;
+    if (t >= m) return;  // whole groups leave together
     const int i = site[t];
     if (i < 0 || i >= g.n_sites) {
-        rgb[3 * t] = rgb[3 * t + 1] = rgb[3 * t + 2] = 0.f;
+        if (lane < 3) rgb[3 * t + lane] = 0.f;
         return;
     }
-    const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
-    float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
-    const float inv = rsqrtf(fmaxf(dx * dx + dy * dy + dz * dz, 1e-20f));
-    dx *= inv, dy *= inv, dz *= inv;
+    const float px = x[3 * t], py = x[3 * t + 1], pz = x[3 * t + 2];
+    float u[3] = {dirs[3 * t], dirs[3 * t + 1], dirs[3 * t + 2]};
+    const float inv = rsqrtf(fmaxf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2], 1e-20f));
+    u[0] *= inv, u[1] *= inv, u[2] *= inv;
     float b[16];
-    sh_basis(dx, dy, dz, DEG, b);
-    constexpr int nb = (DEG + 1) * (DEG + 1);
-    float mmin = kInf, A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
+    sh_basis(u[0], u[1], u[2], DEG, b);
+    Softmax P{kInf, 0.f, 0.f, 0.f, 0.f};
     const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
-    for (int e = e0 - 1; e < e1; ++e) {
+    for (int e = e0 - 1 + lane; e < e1; e += kColourLanes) {  // position e0 - 1 stands for the site itself
         const int k = e < e0 ? i : g.adj[e];
-        const float mk = gauss_m(g, H, k, qx, qy, qz, 1.f);
-        if (mk < mmin) {
-            const float f = mmin == kInf ? 0.f : fexp(-0.5f * (mmin - mk));
-            A *= f, cr *= f, cg *= f, cb *= f;
-            mmin = mk;
+        float mk;
+        if constexpr (REC) {
+            float raw_c;
+            mk = gauss_m_rec(rec, k, px, py, pz, raw_c);
+        } else {
+            mk = gauss_m(g, H, k, px, py, pz, 1.f);
         }
-        const float a = fexp(-0.5f * (mk - mmin));
         float c[3];
-        sh_eval_n<sh_vec4_f32(DEG)>(sh, k, b, nb, c);
-        A += a;
-        cr += a * fmaxf(c[0], 0.f);
-        cg += a * fmaxf(c[1], 0.f);
-        cb += a * fmaxf(c[2], 0.f);
+        sh_colour<DEG>(sh + 12 * static_cast<int64_t>(k), b, c);
+        softmax_add(P, mk, c);
     }
-    rgb[3 * t] = cr / A;
-    rgb[3 * t + 1] = cg / A;
-    rgb[3 * t + 2] = cb / A;
-}
-
-template <int DEG>
-__global__ void __launch_bounds__(kBlock)
-    color_forward_packed_kernel(Graph g, const float4* __restrict__ rec, const float4* __restrict__ sh,
-                                const float* __restrict__ x, const float* __restrict__ dirs,
-                                const int* __restrict__ site, int64_t m, float* __restrict__ rgb) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (t >= m) return;
-    const int i = site[t];
-    if (i < 0 || i >= g.n_sites) {
-        rgb[3 * t] = rgb[3 * t + 1] = rgb[3 * t + 2] = 0.f;
-        return;
+    softmax_merge<kXor1>(P);
+    softmax_merge<kXor2>(P);
+    if (lane < 3) {
+        const float num = lane == 0 ? P.r : (lane == 1 ? P.g : P.b);
+        rgb[3 * t + lane] = num / P.a;
     }
-    const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
-    float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
-    const float inv = rsqrtf(fmaxf(dx * dx + dy * dy + dz * dz, 1e-20f));
-    dx *= inv, dy *= inv, dz *= inv;
-    float b[16];
-    sh_basis(dx, dy, dz, DEG, b);
-    constexpr int nb = (DEG + 1) * (DEG + 1);
-    float mmin = kInf, A = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
-    const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
-    for (int e = e0 - 1; e < e1; ++e) {
-        const int k = e < e0 ? i : g.adj[e];
-        float raw_c;
-        const float mk = gauss_m_rec(rec, k, qx, qy, qz, raw_c);
-        if (mk < mmin) {
-            const float f = mmin == kInf ? 0.f : fexp(-0.5f * (mmin - mk));
-            A *= f, cr *= f, cg *= f, cb *= f;
-            mmin = mk;
-        }
-        const float a = fexp(-0.5f * (mk - mmin));
-        float c[3];
-        sh_eval_n<sh_vec4_f32(DEG)>(sh, k, b, nb, c);
-        A += a;
-        cr += a * fmaxf(c[0], 0.f);
-        cg += a * fmaxf(c[1], 0.f);
-        cb += a * fmaxf(c[2], 0.f);
-    }
-    rgb[3 * t] = cr / A;
-    rgb[3 * t + 1] = cg / A;
-    rgb[3 * t + 2] = cb / A;
 }
 
 __global__ void __launch_bounds__(kBlock)
@@ -306,6 +380,17 @@ __global__ void __launch_bounds__(kBlock)
         A[6 * i + e] = R[3 * p] * R[3 * q2] * iv[0] + R[3 * p + 1] * R[3 * q2 + 1] * iv[1] +
                        R[3 * p + 2] * R[3 * q2 + 2] * iv[2];
     }
+}
+
+template <int DEG>
+void launch_colour(bool rec, dim3 grid, hipStream_t st, const Graph& g, const Gauss& H, const float4* R,
+                   const float4* sh, const float* x, const float* dirs, const int* site, int64_t m, float* rgb) {
+    if (rec)
+        hipLaunchKernelGGL((colour_group_kernel<DEG, true>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site, m,
+                           rgb);
+    else
+        hipLaunchKernelGGL((colour_group_kernel<DEG, false>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site, m,
+                           rgb);
 }
 
 // The records pay for themselves once a call has about N / 8 samples (their build reads and writes each site once;
@@ -338,9 +423,11 @@ extern "C" int vgr_walk(const float* points, int64_t n_sites, const int32_t* off
     if (n_rays == 0) return VGR_OK;
     if (int rc = check_graph("walk", points, n_sites, offsets, adj, n_adj)) return rc;
     VGR_REQUIRE(o && d && start && site && (z || n_samples == 0), "walk: null pointer");
-    hipLaunchKernelGGL(walk_kernel, dim3(grid_for(n_rays, kBlock)), dim3(kBlock), 0, as_stream(stream),
-                       Graph{points, offsets, adj, int(n_sites)}, o, d, z, start, n_rays, int(n_samples), site, steps);
-    return launch_status("walk_kernel");
+    VGR_REQUIRE(n_rays <= INT64_MAX / kWalkLanes, "walk: n_rays too large");
+    hipLaunchKernelGGL(walk_group_kernel, dim3(grid_for(n_rays * kWalkLanes, kBlock)), dim3(kBlock), 0,
+                       as_stream(stream), Graph{points, offsets, adj, int(n_sites)}, o, d, z, start, n_rays,
+                       int(n_samples), site, steps);
+    return launch_status("walk_group_kernel");
 }
 
 extern "C" int vgr_density_forward(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* adj,
@@ -382,33 +469,20 @@ extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int
     const Graph g{points, offsets, adj, int(n_sites)};
     const Gauss H{log_scale, reinterpret_cast<const float4*>(quat)};
     const float4* s4 = reinterpret_cast<const float4*>(sh);
-    const dim3 grid(grid_for(m, kBlock)), block(kBlock);
+    const dim3 grid(grid_for(m * kColourLanes, kBlock)), block(kBlock);
     const hipStream_t st = as_stream(stream);
-    if (use_records(work, work_bytes, n_sites, m)) {
-        const float4* rec = static_cast<const float4*>(work);
+    const bool rec = use_records(work, work_bytes, n_sites, m);
+    const float4* R = static_cast<const float4*>(work);
+    if (rec)
         hipLaunchKernelGGL(gauss_pack_kernel, dim3(grid_for(n_sites, kBlock)), block, 0, st, g, H, nullptr, 1.f,
                            static_cast<float4*>(work));
-        switch (sh_deg) {
-            case 0: hipLaunchKernelGGL(color_forward_packed_kernel<0>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
-                                       rgb); break;
-            case 1: hipLaunchKernelGGL(color_forward_packed_kernel<1>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
-                                       rgb); break;
-            case 2: hipLaunchKernelGGL(color_forward_packed_kernel<2>, grid, block, 0, st, g, rec, s4, x, dirs, site, m,
-                                       rgb); break;
-            default: hipLaunchKernelGGL(color_forward_packed_kernel<3>, grid, block, 0, st, g, rec, s4, x, dirs, site,
-                                        m, rgb); break;
-        }
-        return launch_status("color_forward_packed_kernel");
-    }
     switch (sh_deg) {
-        case 0: hipLaunchKernelGGL(color_forward_kernel<0>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
-        case 1: hipLaunchKernelGGL(color_forward_kernel<1>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
-        case 2: hipLaunchKernelGGL(color_forward_kernel<2>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb); break;
-        default:
-            hipLaunchKernelGGL(color_forward_kernel<3>, grid, block, 0, st, g, H, s4, x, dirs, site, m, rgb);
-            break;
+        case 0: launch_colour<0>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        case 1: launch_colour<1>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        case 2: launch_colour<2>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        default: launch_colour<3>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
     }
-    return launch_status("color_forward_kernel");
+    return launch_status("colour_group_kernel");
 }
 
 extern "C" int vgr_conic_forward(const float* log_scale, const float* quat, int64_t n, double floor, float* A,

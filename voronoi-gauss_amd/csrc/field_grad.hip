@@ -1,7 +1,8 @@
 // Backward field operators of the NeRF-style path, gfx950: gradients of density_forward, color_forward and
 // conic_forward with respect to the per-site parameters.
 //
-// Semantics follow csrc/vgf.cu of the reference: scatter_gauss_grad :121-148, density_backward_kernel :179-198,
+// Semantics follow csrc/vgf.cu of the reference: scatter_gauss_grad :121-148 (here add_gauss_grad, with dL/dq in
+// the outer-product form derived at quat_grad_of), density_backward_kernel :179-198,
 // color_backward_kernel :284-333, conic_backward_kernel :382-424. With m_k = sum_j y_j^2 / s_j^2, y = R^T (x - p_k):
 //   density  dL/draw_k = g rho_k G_k,  dL/dm_k = -g rho_k G_k / 2       (terms with rho_k G_k |g| <= 1e-12 skipped)
 //   colour   a_k = softmax(-m / 2)_k, C = sum a_k c_k:  dL/dsh_k = a_k b(d) dL/dC (where SH_k + 1/2 > 0),
@@ -45,80 +46,109 @@ struct GaussIn {
     const float4* __restrict__ quat;      // (N) w x y z, not normalised
 };
 
-// Gaussian i seen from (x, y, z): offset v, normalised quaternion qn and the norm it was divided by, rotation R
-// (row-major, columns = axes), y = R^T v, inverse variances is2, and m.
-struct Frame {
-    float v[3], y[3], is2[3], qn[4], qnorm, R[9], m;
+// A site's Gaussian as the gradients need it, built once per (site, use): the unit quaternion (w, u) and the norm
+// |q| it was divided by, the axes of the Gaussian (the columns of R(q / |q|)), the inverse variances 1 / s_j^2 and the
+// position.
+struct SiteGauss {
+    float w, u[3], qnorm;
+    float axis[3][3];  // axis[j] = column j of R
+    float is2[3];
+    float p[3];
 };
 
-__device__ __forceinline__ void rotation(float w, float a, float b, float c, float (&R)[9]) {
-    R[0] = 1.f - 2.f * (b * b + c * c), R[1] = 2.f * (a * b - w * c), R[2] = 2.f * (a * c + w * b);
-    R[3] = 2.f * (a * b + w * c), R[4] = 1.f - 2.f * (a * a + c * c), R[5] = 2.f * (b * c - w * a);
-    R[6] = 2.f * (a * c - w * b), R[7] = 2.f * (b * c + w * a), R[8] = 1.f - 2.f * (a * a + b * b);
+__device__ __forceinline__ void unit_quat(const float4& q, float& w, float (&u)[3], float& qnorm) {
+    qnorm = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
+    w = q.x / qnorm, u[0] = q.y / qnorm, u[1] = q.z / qnorm, u[2] = q.w / qnorm;
 }
 
-__device__ __forceinline__ void frame_of(const GradGraph& g, const GaussIn& G, int i, float x, float y, float z,
-                                         Frame& L) {
+// Columns of the rotation of the unit quaternion (w, u): the images of the coordinate axes.
+__device__ __forceinline__ void quat_axes(float w, const float (&u)[3], float (&axis)[3][3]) {
+    const float xx = u[0] * u[0], yy = u[1] * u[1], zz = u[2] * u[2];
+    const float xy = u[0] * u[1], xz = u[0] * u[2], yz = u[1] * u[2];
+    const float wx = w * u[0], wy = w * u[1], wz = w * u[2];
+    axis[0][0] = 1.f - 2.f * (yy + zz), axis[0][1] = 2.f * (xy + wz), axis[0][2] = 2.f * (xz - wy);
+    axis[1][0] = 2.f * (xy - wz), axis[1][1] = 1.f - 2.f * (xx + zz), axis[1][2] = 2.f * (yz + wx);
+    axis[2][0] = 2.f * (xz + wy), axis[2][1] = 2.f * (yz - wx), axis[2][2] = 1.f - 2.f * (xx + yy);
+}
+
+__device__ __forceinline__ SiteGauss site_gauss(const GradGraph& g, const GaussIn& G, int i) {
+    SiteGauss S;
+    unit_quat(G.quat[i], S.w, S.u, S.qnorm);
+    quat_axes(S.w, S.u, S.axis);
     const int64_t i3 = 3 * static_cast<int64_t>(i);
-    L.v[0] = x - g.points[i3], L.v[1] = y - g.points[i3 + 1], L.v[2] = z - g.points[i3 + 2];
-    const float4 q = G.quat[i];
-    L.qnorm = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
-    L.qn[0] = q.x / L.qnorm, L.qn[1] = q.y / L.qnorm, L.qn[2] = q.z / L.qnorm, L.qn[3] = q.w / L.qnorm;
-    rotation(L.qn[0], L.qn[1], L.qn[2], L.qn[3], L.R);
-    L.m = 0.f;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        L.y[k] = L.R[k] * L.v[0] + L.R[3 + k] * L.v[1] + L.R[6 + k] * L.v[2];
-        const float s = fexp(fminf(fmaxf(G.log_scale[i3 + k], -20.f), 20.f));
-        L.is2[k] = 1.f / (s * s);
-        L.m += L.y[k] * L.y[k] * L.is2[k];
+    for (int j = 0; j < 3; ++j) {
+        const float s = fexp(fminf(fmaxf(G.log_scale[i3 + j], -20.f), 20.f));
+        S.is2[j] = 1.f / (s * s);
+        S.p[j] = g.points[i3 + j];
     }
+    return S;
 }
 
-// m alone (the colour pass's first two sweeps), the same arithmetic as frame_of.
-__device__ __forceinline__ float maha_of(const GradGraph& g, const GaussIn& G, int i, float x, float y, float z) {
-    Frame L;
-    frame_of(g, G, i, x, y, z, L);
-    return L.m;
-}
-
-// dL/dq of R(q / |q|) given dL/dR: the derivative of the rotation in the normalised quaternion, then the tangent
-// projection (dq - (dq . qn) qn) / |q| of the normalisation.
-__device__ __forceinline__ void quat_grad(const float (&qn)[4], float qnorm, const float (&dR)[9], float (&out)[4]) {
-    const float w = qn[0], x = qn[1], y = qn[2], z = qn[3];
-    float dq[4];
-    dq[0] = 2.f * (-z * dR[1] + y * dR[2] + z * dR[3] - x * dR[5] - y * dR[6] + x * dR[7]);
-    dq[1] = 2.f * (y * dR[1] + z * dR[2] + y * dR[3] - 2.f * x * dR[4] - w * dR[5] + z * dR[6] + w * dR[7] -
-                   2.f * x * dR[8]);
-    dq[2] = 2.f * (-2.f * y * dR[0] + x * dR[1] + w * dR[2] + x * dR[3] + z * dR[5] - w * dR[6] + z * dR[7] -
-                   2.f * y * dR[8]);
-    dq[3] = 2.f * (-2.f * z * dR[0] - w * dR[1] + x * dR[2] + w * dR[3] - 2.f * z * dR[4] + y * dR[5] + x * dR[6] +
-                   y * dR[7]);
-    const float proj = dq[0] * w + dq[1] * x + dq[2] * y + dq[3] * z;
+// Offset v = x - p, local coordinates y_j = axis_j . v and the Mahalanobis distance m = sum_j y_j^2 / s_j^2.
+__device__ __forceinline__ float site_local(const SiteGauss& S, float x, float y, float z, float (&v)[3],
+                                            float (&yl)[3]) {
+    v[0] = x - S.p[0], v[1] = y - S.p[1], v[2] = z - S.p[2];
+    float m = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) out[k] = (dq[k] - proj * qn[k]) / qnorm;
-}
-
-// Scatters dL/dlog_scale and dL/dquat of Gaussian i given gm = dL/dm.
-__device__ __forceinline__ void scatter_gauss(const Frame& L, float gm, int i, float* __restrict__ g_ls,
-                                              float* __restrict__ g_quat) {
-    float yk[3];
-    float* gl = g_ls + 3 * static_cast<int64_t>(i);
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        yk[k] = 2.f * gm * L.y[k] * L.is2[k];
-        unsafeAtomicAdd(gl + k, -2.f * gm * L.y[k] * L.y[k] * L.is2[k]);
+    for (int j = 0; j < 3; ++j) {
+        yl[j] = S.axis[j][0] * v[0] + S.axis[j][1] * v[1] + S.axis[j][2] * v[2];
+        m += yl[j] * yl[j] * S.is2[j];
     }
-    float dR[9];  // dL/dR_ab = v_a dL/dy_b
+    return m;
+}
+
+// m of site i at x (the colour gradient's first sweeps), site_local's arithmetic.
+__device__ __forceinline__ float site_m(const GradGraph& g, const GaussIn& G, int i, float x, float y, float z) {
+    const SiteGauss S = site_gauss(g, G, i);
+    float v[3], yl[3];
+    return site_local(S, x, y, z, v, yl);
+}
+
+// dL/dq for a loss that depends on q through R(q / |q|), given M = dL/dR (row-major, M[3a + b] = dL/dR_ab). With
+// R^T v = v - 2 w (u x v) + 2 u (u . v) - 2 v |u|^2 (Rodrigues' form of the rotation of the unit quaternion (w, u),
+// treated as a polynomial in (w, u)), and ax(M) = (M_12 - M_21, M_20 - M_02, M_01 - M_10):
+//   dL/dw = -2 u . ax(M),    dL/du = -2 w ax(M) + 2 (M u + M^T u) - 4 tr(M) u,
+// then the tangent projection of the normalisation: (d - (d . q^) q^) / |q|.
+__device__ __forceinline__ void quat_grad_of(float w, const float (&u)[3], float qnorm, const float (&M)[9],
+                                             float (&out)[4]) {
+    const float ax[3] = {M[5] - M[7], M[6] - M[2], M[1] - M[3]};
+    const float tr = M[0] + M[4] + M[8];
+    float d[4];
+    d[0] = -2.f * (u[0] * ax[0] + u[1] * ax[1] + u[2] * ax[2]);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float Mu = M[3 * a] * u[0] + M[3 * a + 1] * u[1] + M[3 * a + 2] * u[2];
+        const float MTu = M[a] * u[0] + M[3 + a] * u[1] + M[6 + a] * u[2];
+        d[1 + a] = -2.f * w * ax[a] + 2.f * (Mu + MTu) - 4.f * tr * u[a];
+    }
+    const float radial = d[0] * w + d[1] * u[0] + d[2] * u[1] + d[3] * u[2];
+    out[0] = (d[0] - radial * w) / qnorm;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) out[1 + a] = (d[1 + a] - radial * u[a]) / qnorm;
+}
+
+// Adds the log-scale and quaternion gradients of site k for dL/dm = gm at offset v (local coordinates yl):
+// dm/dlog_s_j = -2 y_j^2 / s_j^2, and dL/dR_ab = v_a dL/dy_b with dL/dy_b = 2 gm y_b / s_b^2.
+__device__ __forceinline__ void add_gauss_grad(const SiteGauss& S, float gm, const float (&v)[3],
+                                               const float (&yl)[3], int k, float* __restrict__ g_ls,
+                                               float* __restrict__ g_quat) {
+    float gy[3], M[9];
+    float* gl = g_ls + 3 * static_cast<int64_t>(k);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        gy[j] = 2.f * gm * yl[j] * S.is2[j];
+        unsafeAtomicAdd(gl + j, -gy[j] * yl[j]);
+    }
 #pragma unroll
     for (int a = 0; a < 3; ++a)
 #pragma unroll
-        for (int b = 0; b < 3; ++b) dR[3 * a + b] = L.v[a] * yk[b];
+        for (int b = 0; b < 3; ++b) M[3 * a + b] = v[a] * gy[b];
     float gq[4];
-    quat_grad(L.qn, L.qnorm, dR, gq);
-    float* gqp = g_quat + 4 * static_cast<int64_t>(i);
+    quat_grad_of(S.w, S.u, S.qnorm, M, gq);
+    float* gqp = g_quat + 4 * static_cast<int64_t>(k);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) unsafeAtomicAdd(gqp + k, gq[k]);
+    for (int j = 0; j < 4; ++j) unsafeAtomicAdd(gqp + j, gq[j]);
 }
 
 __global__ void __launch_bounds__(kBlock)
@@ -134,12 +164,12 @@ __global__ void __launch_bounds__(kBlock)
     const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
     for (int e = e0 - 1; e < e1; ++e) {
         const int k = e < e0 ? i : g.adj[e];
-        Frame L;
-        frame_of(g, G, k, qx, qy, qz, L);
-        const float c = fexp(fminf(raw[k], 30.f) - 0.5f * L.m);  // rho_k G_k
+        const SiteGauss S = site_gauss(g, G, k);
+        float v[3], yl[3];
+        const float c = fexp(fminf(raw[k], 30.f) - 0.5f * site_local(S, qx, qy, qz, v, yl));  // rho_k G_k
         if (c * fabsf(gs) > 1e-12f) {
             unsafeAtomicAdd(g_raw + k, gs * c);
-            scatter_gauss(L, -0.5f * gs * c, k, g_ls, g_quat);
+            add_gauss_grad(S, -0.5f * gs * c, v, yl, k, g_ls, g_quat);
         }
     }
 }
@@ -174,32 +204,19 @@ __device__ __forceinline__ void sums_add(GaussSums& A, float gm, const float (&v
 }
 
 // Adds site k's log-scale and quaternion gradients from its sums (F: the site's frame).
-__device__ __forceinline__ void sums_write(const GaussSums& A, const Frame& F, int64_t k, float* __restrict__ g_ls,
-                                           float* __restrict__ g_quat) {
-    float dR[9];
+__device__ __forceinline__ void sums_write(const GaussSums& A, const SiteGauss& F, int64_t k,
+                                           float* __restrict__ g_ls, float* __restrict__ g_quat) {
+    float M[9];  // dL/dR
 #pragma unroll
     for (int a = 0; a < 3; ++a)
 #pragma unroll
-        for (int b = 0; b < 3; ++b) dR[3 * a + b] = 2.f * F.is2[b] * A.G[3 * a + b];
+        for (int b = 0; b < 3; ++b) M[3 * a + b] = 2.f * F.is2[b] * A.G[3 * a + b];
     float gq[4];
-    quat_grad(F.qn, F.qnorm, dR, gq);
+    quat_grad_of(F.w, F.u, F.qnorm, M, gq);
 #pragma unroll
     for (int j = 0; j < 3; ++j) g_ls[3 * k + j] += -2.f * F.is2[j] * A.S[j];
 #pragma unroll
     for (int j = 0; j < 4; ++j) g_quat[4 * k + j] += gq[j];
-}
-
-// Offset v = x - p and y = R^T v of a sample at site k from the site's frame, and m: frame_of's arithmetic.
-__device__ __forceinline__ float site_maha(const Frame& F, const float (&p)[3], float x, float y, float z,
-                                           float (&v)[3], float (&yy)[3]) {
-    v[0] = x - p[0], v[1] = y - p[1], v[2] = z - p[2];
-    float m = 0.f;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        yy[j] = F.R[j] * v[0] + F.R[3 + j] * v[1] + F.R[6 + j] * v[2];
-        m += yy[j] * yy[j] * F.is2[j];
-    }
-    return m;
 }
 
 // SH_k(d) + 1/2 over the coefficients of degree <= DEG (storage order: coefficient j, channel c at 3 j + c).
@@ -237,9 +254,9 @@ __global__ void __launch_bounds__(kBlock)
     const float qx = x[3 * t], qy = x[3 * t + 1], qz = x[3 * t + 2];
     const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
     float mmin = kInf;
-    for (int e = e0 - 1; e < e1; ++e) mmin = fminf(mmin, maha_of(g, H, e < e0 ? i : g.adj[e], qx, qy, qz));
+    for (int e = e0 - 1; e < e1; ++e) mmin = fminf(mmin, site_m(g, H, e < e0 ? i : g.adj[e], qx, qy, qz));
     float A = 0.f;
-    for (int e = e0 - 1; e < e1; ++e) A += fexp(-0.5f * (maha_of(g, H, e < e0 ? i : g.adj[e], qx, qy, qz) - mmin));
+    for (int e = e0 - 1; e < e1; ++e) A += fexp(-0.5f * (site_m(g, H, e < e0 ? i : g.adj[e], qx, qy, qz) - mmin));
     const float inv_a = 1.f / A;
     const float gCC = gr * rgb[3 * t] + gg * rgb[3 * t + 1] + gb * rgb[3 * t + 2];
     float dx = dirs[3 * t], dy = dirs[3 * t + 1], dz = dirs[3 * t + 2];
@@ -255,9 +272,9 @@ __global__ void __launch_bounds__(kBlock)
     }
     for (int e = e0 - 1; e < e1; ++e) {
         const int k = e < e0 ? i : g.adj[e];
-        Frame L;
-        frame_of(g, H, k, qx, qy, qz, L);
-        const float a = fexp(-0.5f * (L.m - mmin)) * inv_a;
+        const SiteGauss S = site_gauss(g, H, k);
+        float v[3], yl[3];
+        const float a = fexp(-0.5f * (site_local(S, qx, qy, qz, v, yl) - mmin)) * inv_a;
         if (a < kMinWeight) continue;
         float c[3];
         sh_colour<DEG>(sh + 12 * static_cast<int64_t>(k), b, c);
@@ -271,7 +288,7 @@ __global__ void __launch_bounds__(kBlock)
         }
         const float ga = gr * fmaxf(c[0], 0.f) + gg * fmaxf(c[1], 0.f) + gb * fmaxf(c[2], 0.f);
         const float gm = -0.5f * a * (ga - gCC);
-        if (gm != 0.f) scatter_gauss(L, gm, k, g_ls, g_quat);
+        if (gm != 0.f) add_gauss_grad(S, gm, v, yl, k, g_ls, g_quat);
     }
 }
 
@@ -332,9 +349,7 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t kk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (kk >= g.n_sites) return;
     const int k = static_cast<int>(kk);
-    const float p[3] = {g.points[3 * kk], g.points[3 * kk + 1], g.points[3 * kk + 2]};
-    Frame F;  // the site's rotation, variances and quaternion (frame_of at the site itself)
-    frame_of(g, G, k, p[0], p[1], p[2], F);
+    const SiteGauss F = site_gauss(g, G, k);
     const float raw_c = fminf(raw[k], 30.f);
     GaussSums A;
     sums_init(A);
@@ -347,7 +362,7 @@ __global__ void __launch_bounds__(kBlock)
         for (int r = start[i]; r < r1; ++r) {
             const float4 rec = recs[r];
             float v[3], y[3];
-            const float m_k = site_maha(F, p, rec.x, rec.y, rec.z, v, y);
+            const float m_k = site_local(F, rec.x, rec.y, rec.z, v, y);
             const float c = fexp(raw_c - 0.5f * m_k);  // rho_k G_k
             if (c * fabsf(rec.w) > 1e-12f) {
                 acc_raw += rec.w * c;
@@ -380,9 +395,7 @@ __global__ void __launch_bounds__(kBlock)
     for (int j = 0; j < nb; ++j) acc[j][0] = acc[j][1] = acc[j][2] = 0.f;
     bool any = false;
     const float4* sk = sh + 12 * kk;
-    const float p[3] = {g.points[3 * kk], g.points[3 * kk + 1], g.points[3 * kk + 2]};
-    Frame F;  // the site's rotation, variances and quaternion (frame_of at the site itself)
-    frame_of(g, H, k, p[0], p[1], p[2], F);
+    const SiteGauss F = site_gauss(g, H, k);
     GaussSums A;
     sums_init(A);
     for (int e = e0 - 1; e < e1; ++e) {
@@ -391,7 +404,7 @@ __global__ void __launch_bounds__(kBlock)
         for (int r = r0; r < r1; ++r) {
             const SampleRec rec = recs[r];
             float v[3], y[3];
-            const float m_k = site_maha(F, p, rec.a.x, rec.a.y, rec.a.z, v, y);
+            const float m_k = site_local(F, rec.a.x, rec.a.y, rec.a.z, v, y);
             const float a = fexp(-0.5f * (m_k - rec.a.w)) * rec.b.w;
             if (a < kMinWeight) continue;
             float b[16];
@@ -434,38 +447,30 @@ __global__ void __launch_bounds__(kBlock)
                           float* __restrict__ g_quat) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n) return;
-    const float4 q = quat[i];
-    const float qnorm = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
-    const float qn[4] = {q.x / qnorm, q.y / qnorm, q.z / qnorm, q.w / qnorm};
-    float R[9];
-    rotation(qn[0], qn[1], qn[2], qn[3], R);
-    float iv[3], s2[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        s2[k] = fexp(2.f * fminf(fmaxf(log_scale[3 * i + k], -20.f), 20.f));
-        iv[k] = 1.f / (s2[k] + floor2);
-    }
-    // the off-diagonal entries of A stand for A_ab and A_ba: dL/dA is symmetric with half of them off the diagonal
+    // A = sum_j iv_j a_j a_j^T over the axes a_j (columns of R), iv_j = 1 / (s_j^2 + floor^2); dL/dA is symmetric,
+    // its off-diagonal storage entries standing for both A_ab and A_ba
+    float w, u[3], qnorm, axis[3][3];
+    unit_quat(quat[i], w, u, qnorm);
+    quat_axes(w, u, axis);
     const float* ga = gA + 6 * i;
-    const float G[9] = {ga[0],        0.5f * ga[1], 0.5f * ga[2], 0.5f * ga[1], ga[3],
-                        0.5f * ga[4], 0.5f * ga[2], 0.5f * ga[4], ga[5]};
-    float GR[9];
+    const float G[3][3] = {{ga[0], 0.5f * ga[1], 0.5f * ga[2]},
+                           {0.5f * ga[1], ga[3], 0.5f * ga[4]},
+                           {0.5f * ga[2], 0.5f * ga[4], ga[5]}};
+    float M[9];  // dL/dR: column j is 2 iv_j G a_j
 #pragma unroll
-    for (int r = 0; r < 3; ++r)
+    for (int j = 0; j < 3; ++j) {
+        const float s2 = fexp(2.f * fminf(fmaxf(log_scale[3 * i + j], -20.f), 20.f));
+        const float iv = 1.f / (s2 + floor2);
+        float Ga[3];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) GR[3 * r + k] = G[3 * r] * R[k] + G[3 * r + 1] * R[3 + k] + G[3 * r + 2] * R[6 + k];
+        for (int a = 0; a < 3; ++a) Ga[a] = G[a][0] * axis[j][0] + G[a][1] * axis[j][1] + G[a][2] * axis[j][2];
+        const float aGa = axis[j][0] * Ga[0] + axis[j][1] * Ga[1] + axis[j][2] * Ga[2];  // dL/div_j
+        g_ls[3 * i + j] = aGa * (-2.f * s2 * iv * iv);                                   // div_j/dlog_s_j
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const float g_iv = R[k] * GR[k] + R[3 + k] * GR[3 + k] + R[6 + k] * GR[6 + k];  // (R^T G R)_kk
-        g_ls[3 * i + k] = g_iv * (-2.f * s2[k] * iv[k] * iv[k]);
+        for (int a = 0; a < 3; ++a) M[3 * a + j] = 2.f * iv * Ga[a];
     }
-    float dR[9];  // dL/dR = 2 G R diag(iv)
-#pragma unroll
-    for (int r = 0; r < 3; ++r)
-#pragma unroll
-        for (int k = 0; k < 3; ++k) dR[3 * r + k] = 2.f * GR[3 * r + k] * iv[k];
     float gq[4];
-    quat_grad(qn, qnorm, dR, gq);
+    quat_grad_of(w, u, qnorm, M, gq);
 #pragma unroll
     for (int k = 0; k < 4; ++k) g_quat[4 * i + k] = gq[k];
 }

@@ -97,6 +97,51 @@ def normalization_of(xyz, radius=0.95, keep_quantile=0.98):
 	return center, scale
 
 
+def split_views(images, split, test_every):
+	"""Image ids of one split, in name order: the test split is every `test_every`-th image by name starting with the
+	first, the train split the others (colmap.py:84-89)."""
+	if split not in ('train', 'test'):
+		raise ValueError(f"split must be 'train' or 'test' (got {split!r})")
+	by_name = sorted(images, key=lambda iid: images[iid][0])
+	is_test = [rank % test_every == 0 for rank in range(len(by_name))]
+	return [iid for iid, t in zip(by_name, is_test) if t == (split == 'test')]
+
+
+def image_size(root, downsample, first_name, camera):
+	"""(W, H) of the split's images: read from the first downsampled image file when present, else the camera's
+	resolution divided by `downsample` (the size the downsampled images have)."""
+	img_dir = os.path.join(root, 'images' if downsample == 1 else f'images_{downsample}')
+	path = os.path.join(img_dir, first_name)
+	if os.path.exists(path):
+		from PIL import Image
+		with Image.open(path) as im:
+			return im.size
+	_, w, h, _ = camera
+	return int(round(w / downsample)), int(round(h / downsample))
+
+
+def view_matrices(cams, images, ids, width, height, center, scale):
+	"""Per view: K (n, 3, 3) scaled from the camera's resolution to width x height, and camera-to-world c2w (n, 4, 4)
+	in normalised coordinates (rotation R^T of the world-to-camera rotation R, camera centre (-R^T t - center) /
+	scale), as colmap.py:100-118 defines them; all views at once."""
+	R = np.stack([images[i][1] for i in ids])                  # (n, 3, 3) world -> camera
+	t = np.stack([images[i][2] for i in ids])                  # (n, 3)
+	cam = [cams[images[i][3]] for i in ids]
+	fxfycxcy = np.array([intrinsics(c[0], c[3]) for c in cam], np.float64)  # (n, 4)
+	res = np.array([(c[1], c[2]) for c in cam], np.float64)    # (n, 2) native width, height
+	sx, sy = width / res[:, 0], height / res[:, 1]
+	n = len(ids)
+	K = np.zeros((n, 3, 3))
+	K[:, 0, 0], K[:, 1, 1] = fxfycxcy[:, 0] * sx, fxfycxcy[:, 1] * sy
+	K[:, 0, 2], K[:, 1, 2] = fxfycxcy[:, 2] * sx, fxfycxcy[:, 3] * sy
+	K[:, 2, 2] = 1.0
+	Rt = np.transpose(R, (0, 2, 1))
+	c2w = np.tile(np.eye(4), (n, 1, 1))
+	c2w[:, :3, :3] = Rt
+	c2w[:, :3, 3] = (-np.einsum('nij,nj->ni', Rt, t) - center) / scale
+	return K, c2w
+
+
 class ColmapCameras:
 	"""The views of one split (every `test_every`-th image by name is a test view, colmap.py:84-89) in normalised
 	coordinates: K (n, 3, 3) at the downsampled resolution, c2w (n, 4, 4) camera-to-world with OpenCV axes,
@@ -105,58 +150,36 @@ class ColmapCameras:
 
 	def __init__(self, root, split='test', downsample=4, device='cuda', test_every=8, radius=0.95,
 				 keep_quantile=0.98, normalization=None, load_images=False):
-		if split not in ('train', 'test'):
-			raise ValueError(f"split must be 'train' or 'test' (got {split!r})")
 		self.root, self.device = root, torch.device(device)
 		sparse = os.path.join(root, 'sparse', '0')
 		cams = read_cameras(os.path.join(sparse, 'cameras.bin'))
 		images = read_images(os.path.join(sparse, 'images.bin'))
-		order = sorted(images, key=lambda i: images[i][0])
-		idx = np.arange(len(order))
-		keep = idx % test_every != 0 if split == 'train' else idx % test_every == 0
-		self.image_ids = [order[i] for i in idx[keep]]
+		self.image_ids = split_views(images, split, test_every)
+		if not self.image_ids:
+			raise ValueError(f'{root}: no {split} images')
 		self.names = [images[i][0] for i in self.image_ids]
 		self.n = len(self.names)
-		if self.n == 0:
-			raise ValueError(f'{root}: no {split} images')
-
-		img_dir = os.path.join(root, 'images' if downsample == 1 else f'images_{downsample}')
-		first = os.path.join(img_dir, self.names[0])
-		if os.path.exists(first):
-			from PIL import Image
-			with Image.open(first) as im:
-				self.W, self.H = im.size
-		else:  # no image files: the resolution the downsampled images would have
-			_, w, h, _ = cams[images[self.image_ids[0]][3]]
-			self.W, self.H = int(round(w / downsample)), int(round(h / downsample))
-		self.images = None
-		if load_images:
-			from PIL import Image
-			rgb = [np.asarray(Image.open(os.path.join(img_dir, n)).convert('RGB')) for n in self.names]
-			self.images = torch.from_numpy(np.stack(rgb)).to(self.device)
+		self.W, self.H = image_size(root, downsample, self.names[0], cams[images[self.image_ids[0]][3]])
+		self.images = self._read_images(downsample) if load_images else None
 
 		if normalization is None:
-			xyz = read_points(os.path.join(sparse, 'points3D.bin'))[0]
-			normalization = normalization_of(xyz, radius, keep_quantile)
-		center, scale = normalization
-		center, scale = np.asarray(center, np.float64).reshape(3), float(scale)
+			normalization = normalization_of(read_points(os.path.join(sparse, 'points3D.bin'))[0], radius,
+											 keep_quantile)
+		center = np.asarray(normalization[0], np.float64).reshape(3)
+		scale = float(normalization[1])
 		self.normalization = (center, scale)
 
-		Ks, c2ws = [], []
-		for iid in self.image_ids:
-			_, R, t, cid = images[iid]
-			model, w, h, params = cams[cid]
-			fx, fy, cx, cy = intrinsics(model, params)
-			sx, sy = self.W / w, self.H / h
-			Ks.append(np.array([[fx * sx, 0, cx * sx], [0, fy * sy, cy * sy], [0, 0, 1]]))
-			c2w = np.eye(4)
-			c2w[:3, :3] = R.T
-			c2w[:3, 3] = (-R.T @ t - center) / scale
-			c2ws.append(c2w)
-		self.K = torch.tensor(np.stack(Ks), dtype=torch.float32, device=self.device)
+		K, c2w = view_matrices(cams, images, self.image_ids, self.W, self.H, center, scale)
+		self.K = torch.tensor(K, dtype=torch.float32, device=self.device)
 		self.K_inv = torch.linalg.inv(self.K)
-		self.c2w = torch.tensor(np.stack(c2ws), dtype=torch.float32, device=self.device)
+		self.c2w = torch.tensor(c2w, dtype=torch.float32, device=self.device)
 		self.centers = self.c2w[:, :3, 3].contiguous()
+
+	def _read_images(self, downsample):
+		from PIL import Image
+		img_dir = os.path.join(self.root, 'images' if downsample == 1 else f'images_{downsample}')
+		rgb = [np.asarray(Image.open(os.path.join(img_dir, n)).convert('RGB')) for n in self.names]
+		return torch.from_numpy(np.stack(rgb)).to(self.device)
 
 	def rays(self, img, px, py):
 		"""Rays through pixel centres (px + 0.5, py + 0.5) of views `img` (colmap.py:126-131) -> o, d (m, 3)."""
