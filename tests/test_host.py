@@ -200,3 +200,60 @@ def test_bench_refuses_more_than_one_gpu():
 	p = subprocess.run([sys.executable, os.path.join(root, 'bench.py'), '--gpus', '2'], capture_output=True, text=True,
 					   cwd=root, timeout=120)
 	assert p.returncode != 0 and 'one GPU' in (p.stdout + p.stderr)
+
+
+def test_s_to_t_rounds_like_the_reference():
+	"""render.s_to_t bit for bit against render.py:28-33 restated in numpy float32, operation by operation
+	(lin = n + (m - n) min(2 s, 1); disparity 1 / (1/m + u (1/f - 1/m)), u = max(2 s - 1, 0)), on 4096 rays x 64
+	coordinates including s = 0, 1/2 and 1."""
+	from vgr.render import s_to_t
+	rng = np.random.default_rng(5)
+	B, S = 4096, 64
+	n = np.full(B, 0.02, np.float32)
+	m = rng.uniform(0.5, 3.0, B).astype(np.float32)
+	f = (m + rng.uniform(1e-3, 50.0, B)).astype(np.float32)
+	s = np.sort(rng.uniform(0, 1, (B, S)).astype(np.float32), 1)
+	s[:, 0], s[:, S // 2], s[:, -1] = 0.0, 0.5, 1.0
+	got = s_to_t(torch.from_numpy(s), torch.from_numpy(n), torch.from_numpy(m), torch.from_numpy(f)).numpy()
+	one, two = np.float32(1), np.float32(2)
+	nn, mm, ff = n[:, None], m[:, None], f[:, None]
+	lin = nn + (mm - nn) * np.minimum(two * s, one)
+	u = np.maximum(two * s - one, np.float32(0))
+	disp = one / (one / mm + u * (one / ff - one / mm))
+	want = np.where(s < np.float32(0.5), lin, disp)
+	assert got.dtype == np.float32
+	np.testing.assert_array_equal(got, want)
+	np.testing.assert_allclose(got[:, 0], n, rtol=0)
+	np.testing.assert_allclose(got[:, -1], f, rtol=1e-5)  # three reciprocals: a few ulps
+
+
+def test_sample_pdf_inverts_the_cdf():
+	"""render.sample_pdf (render.py:36-50): bit for bit against the reference's sequence of torch operations
+	restated here (pdf, cumsum, linspace levels, searchsorted right, clamped gathers, the 1e-5 span guard); and the
+	closed form: each sample is the float64 inverse of the piecewise-linear CDF of weights + 1e-5 at its level."""
+	from vgr.render import sample_pdf
+	rng = np.random.default_rng(6)
+	B, S, n = 512, 63, 64
+	bins = torch.from_numpy(np.sort(rng.uniform(0, 1, (B, S + 1)).astype(np.float32), 1))
+	w = rng.exponential(1.0, (B, S)).astype(np.float32)
+	w[::7] = 0.0  # all-zero rows: the 1e-5 floor makes the pdf uniform
+	w[1::5, 10:20] = 0.0
+	weights = torch.from_numpy(w)
+	got = sample_pdf(bins, weights, n, det=True)
+	ww = weights + 1e-5
+	pdf = ww / ww.sum(-1, keepdim=True)
+	cdf = torch.cat([torch.zeros_like(pdf[:, :1]), torch.cumsum(pdf, -1)], -1)
+	u = torch.linspace(0.5 / n, 1 - 0.5 / n, n).expand(B, n).contiguous()
+	inds = torch.searchsorted(cdf, u, right=True)
+	below, above = (inds - 1).clamp_min(0), inds.clamp_max(cdf.shape[-1] - 1)
+	cb, ca = cdf.gather(1, below), cdf.gather(1, above)
+	bb, ba = bins.gather(1, below), bins.gather(1, above)
+	denom = torch.where(ca - cb < 1e-5, torch.ones_like(ca), ca - cb)
+	want = bb + (u - cb) / denom * (ba - bb)
+	assert torch.equal(got, want)
+	# closed form in float64
+	c64 = np.concatenate([np.zeros((B, 1)), np.cumsum((w + 1e-5) / (w + 1e-5).sum(1, keepdims=True), 1)], 1)
+	lev = (np.arange(n) + 0.5) / n
+	b64 = bins.numpy().astype(np.float64)
+	for r in range(0, B, 37):
+		np.testing.assert_allclose(got[r].numpy(), np.interp(lev, c64[r], b64[r]), atol=2e-5)

@@ -89,3 +89,50 @@ def test_noalloc_grid_rejects_builds_beyond_its_scratch(gpu):
 	res = (ctypes.c_int32 * 3)(200, 200, 200)
 	rc = lib.vgr_grid_build_noalloc(None, n, 3, lo, cell, res, None, None, _lib.stream_of(gpu))
 	assert rc != 0 and b'beyond the static' in lib.vgr_last_error()
+
+
+def test_noalloc_grid_allocates_nothing_and_replays_in_a_graph(gpu):
+	"""After one warm call on the device (which looks up the scratch array's address), repeated calls leave the
+	device's free memory unchanged; and a call captured in a HIP graph (torch.cuda.graph), replayed three times with
+	eager work between the replays, gives the workspace build's cells every time."""
+	lib = _lib.load()
+	rng = np.random.default_rng(22)
+	n = 100000
+	pts = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+	pts_t = torch.as_tensor(pts, device=gpu)
+	geom = geometry(pts)
+	lo, cell, res, n_cells = geom
+	ref = build(gpu, pts_t, geom, noalloc=False)
+	cs_ref, s_ref = ref[0].cpu().numpy(), ref[1].cpu().numpy()
+	cell_of = np.repeat(np.arange(len(cs_ref) - 1), np.diff(cs_ref))
+	sorted_ref = s_ref[np.lexsort((s_ref, cell_of))]
+	cs = torch.full((n_cells + 1,), -7, dtype=torch.int32, device=gpu)
+	sites = torch.full((n,), -7, dtype=torch.int32, device=gpu)
+
+	def call():
+		return lib.vgr_grid_build_noalloc(_lib.ptr(pts_t), n, 3, lo, cell, res, _lib.ptr(cs), _lib.ptr(sites),
+										  _lib.stream_of(gpu))
+
+	assert call() == 0, lib.vgr_last_error()  # the warm call
+	torch.cuda.synchronize()
+	free0 = torch.cuda.mem_get_info(gpu)[0]
+	for _ in range(3):
+		assert call() == 0, lib.vgr_last_error()
+	torch.cuda.synchronize()
+	assert torch.cuda.mem_get_info(gpu)[0] == free0
+	np.testing.assert_array_equal(cs.cpu().numpy(), cs_ref)
+
+	graph = torch.cuda.CUDAGraph()
+	with torch.cuda.graph(graph):
+		rc = call()
+	assert rc == 0, lib.vgr_last_error()
+	for rep in range(3):
+		cs.fill_(-7)
+		sites.fill_(-7)
+		torch.cuda.synchronize()
+		graph.replay()
+		torch.cuda.synchronize()
+		got_cs, got_s = cs.cpu().numpy(), sites.cpu().numpy()
+		print(f'[no-alloc grid] graph replay {rep}', flush=True)
+		np.testing.assert_array_equal(got_cs, cs_ref)
+		np.testing.assert_array_equal(got_s[np.lexsort((got_s, cell_of))], sorted_ref)

@@ -42,8 +42,10 @@ def s_to_t(s, t_near, t_mid, t_far):
 	"""Ray parameter of the normalised coordinate s in [0, 1]: s in [0, 1/2] maps linearly onto [near, mid], s in
 	[1/2, 1] linearly in disparity 1/t onto [mid, far] (render.py:28-33)."""
 	n, m, f = t_near.unsqueeze(-1), t_mid.unsqueeze(-1), t_far.unsqueeze(-1)
-	inside = torch.lerp(n.expand_as(s), m.expand_as(s), (2 * s).clamp(max=1.0))
-	beyond = 1.0 / torch.lerp((1.0 / m).expand_as(s), (1.0 / f).expand_as(s), (2 * s - 1).clamp(min=0.0))
+	# the reference's operation order (a + (b - a) w, not torch.lerp, which rounds differently for w >= 1/2)
+	inside = n + (m - n) * (2 * s).clamp(max=1.0)
+	inv_m = 1.0 / m
+	beyond = 1.0 / (inv_m + (2 * s - 1).clamp(min=0.0) * (1.0 / f - inv_m))
 	return torch.where(s < 0.5, inside, beyond)
 
 
@@ -54,7 +56,7 @@ def sample_pdf(bins, weights, n, det=True):
 	cdf = F.pad(torch.cumsum(w / w.sum(-1, keepdim=True), -1), (1, 0), value=0.0)
 	B = bins.shape[0]
 	if det:
-		levels = ((torch.arange(n, device=bins.device, dtype=bins.dtype) + 0.5) / n).expand(B, n).contiguous()
+		levels = torch.linspace(0.5 / n, 1 - 0.5 / n, n, device=bins.device, dtype=bins.dtype).expand(B, n).contiguous()
 	else:
 		levels = torch.rand(B, n, device=bins.device, dtype=bins.dtype)
 	hi = torch.searchsorted(cdf, levels, right=True)
@@ -77,7 +79,7 @@ def composite(sigma, t, t_far):
 
 def _points(o, d, t):
 	"""(B * S, 3) sample points o + t d for t (B, S)."""
-	return torch.addcmul(o.unsqueeze(1), d.unsqueeze(1), t.unsqueeze(-1)).reshape(-1, 3)
+	return (o.unsqueeze(1) + d.unsqueeze(1) * t.unsqueeze(-1)).reshape(-1, 3)
 
 
 def proposal_weights(model, o, d, s, bounds, start, scale_mult):
@@ -314,10 +316,12 @@ def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=Fa
 
 @torch.no_grad()
 def index_pack(pack):
-	"""Adds the indexed edge records (ext.index_pack: edge_i, attr_i) to a GPU pack; render_rays_foam_infer then
-	renders fused colours with one record stream per neighbourhood entry, bit-identical to the reference records.
-	A snapshot: call again after changing the pack."""
+	"""Adds the indexed edge records (ext.index_pack: edge_i, attr_i) and the slot table of the reference's colour
+	cache (ext.slot_table: slots) to a GPU pack; render_rays_foam_infer then renders fused colours with one record
+	stream per neighbourhood entry, bit-identical to the reference records, and counts the cache misses of
+	stats[:, 4] once per neighbourhood pass. A snapshot: call again after changing the pack."""
 	pack['edge_i'], pack['attr_i'] = ext.index_pack(pack['offsets'], pack['nbr'], pack['edge'], pack['attr'])
+	pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
 	return pack
 
 
@@ -359,7 +363,8 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 		o.float().contiguous(), d.float().contiguous(), start.int().contiguous(), t_near.contiguous(),
 		t_far.contiguous(), float(t_thresh), float(w_thresh), 2 * math.log(1 / eps_color) if eps_color > 0 else math.inf,
 		_COLOR_MODES[colors], int(stage), empty if cap is None else cap.int().contiguous(), pack['orig'],
-		trace_cap=trace_cap, indexed=(pack['edge_i'], pack['attr_i']) if 'edge_i' in pack else None)
+		trace_cap=trace_cap, indexed=(pack['edge_i'], pack['attr_i']) if 'edge_i' in pack else None,
+		slots=pack.get('slots'))
 	fg, T, depth, stats = out[:4]
 	res = {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth, 'stats': stats}
 	if trace_cap > 0:
