@@ -284,14 +284,17 @@ def bench_foam(args):
 	# fused colours with one ray per lane read the indexed edge records (built once with the pack, untimed)
 	indexed = not args.no_indexed and mode == 2 and lanes == 1
 	if indexed:
-		render.index_pack(pack)
+		render.index_pack(pack)  # also the slot table
+	elif args.colors != 'baked':  # the reference's colour-cache misses counted once per neighbourhood pass
+		pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
 
 	def launch(p, sel, m=mode, cut=color_cut):
 		order = ext.ray_order(o[sel], d[sel], dir_res, pos_bits) if ordered else None
 		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
 							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'],
 							 lanes=lanes, order=order,
-							 indexed=(p['edge_i'], p['attr_i']) if 'edge_i' in p and m == 2 else None)
+							 indexed=(p['edge_i'], p['attr_i']) if 'edge_i' in p and m == 2 else None,
+							 slots=p.get('slots'))
 
 	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
 		per = B // frames

@@ -48,7 +48,9 @@ int vgr_abi_version(void);
  *   cap     i32 (B) per-ray sample budget, or NULL (unbounded)
  *   orig    i32 (N) original site index for tie-breaking after a renumbering, or NULL
  *   outputs rgb f32 (B, 3) foreground (no background), T f32 (B), depth f32 (B),
- *           stats i32 (B, 5) = samples, segments with colour, walk steps, density terms, SH evaluations
+ *           stats i32 (B, 5) = samples, segments with colour, walk steps, density terms, SH evaluations (the colour
+ *           lookups that miss the reference's per-ray cache of 8 direct-mapped slots keyed by site & 7,
+ *           csrc/foam_infer.cu:151-168; kept here as 8 tags per ray in LDS, checked at every lookup)
  * color_mode: VGR_COLOR_*; stage: 0 exit faces only, 1 + density, 2 full rendering.
  * Rays whose start index is outside [0, N) are not traced: rgb = depth = 0, T = 1, stats = 0.
  */
@@ -80,8 +82,10 @@ int vgr_foam_infer_traced(const float* points, int64_t n_sites, const int32_t* o
  * baked colours with a finite color_cut always run one ray per lane (their neighbour skipping follows the edge
  * order). trace may be NULL (then trace_cap is ignored). order (NULL = the batch order): a permutation of
  * 0 .. B - 1 giving the order in which the rays are traced (vgr_ray_order); results are the same in any order, an
- * entry outside [0, B) is skipped. No counterpart in the reference: the layout comparison for vgr_foam_infer, whose
- * arguments and outputs it otherwise shares.
+ * entry outside [0, B) is skipped. slots (NULL = none): the slot table of vgr_foam_slot_table for this pack; with
+ * color_cut = +inf the reference's cache misses (stats[:, 4]) then come from it once per neighbourhood pass instead
+ * of from per-lookup tags in LDS (same counts, less work). No counterpart in the reference: the layout comparison
+ * for vgr_foam_infer, whose arguments and outputs it otherwise shares.
  */
 int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                          const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
@@ -89,7 +93,7 @@ int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const int32_t* of
                          const float* far_t, int64_t n_rays, double t_thresh, double w_thresh, double color_cut,
                          int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
                          float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
-                         const int32_t* order, int64_t lanes_per_ray, void* stream);
+                         const int32_t* order, int64_t lanes_per_ray, const int32_t* slots, void* stream);
 
 /*
  * Cell traversal alone (foam_infer with stage 0: walk to the start cell, then exit faces up to far or cap) with a
@@ -347,7 +351,8 @@ int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float*
  * VGR_COLOR_FUSED) with one ray per lane (lanes_per_ray 0 or 1) reads edge_i and attr_i in place of nbr, edge and
  * attr, one record stream per neighbourhood entry instead of two. The outputs are bit-identical to
  * vgr_foam_infer_lanes on the same pack; every other stage, colour mode or layout runs vgr_foam_infer_lanes on the
- * reference records unchanged. No counterpart in the reference (same function as vgr_foam_infer).
+ * reference records unchanged. slots as for vgr_foam_infer_lanes. No counterpart in the reference (same function as
+ * vgr_foam_infer).
  */
 int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                            const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
@@ -356,7 +361,21 @@ int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* 
                            int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
                            float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                            const int32_t* order, int64_t lanes_per_ray, const float* edge_i, const float* attr_i,
-                           void* stream);
+                           const int32_t* slots, void* stream);
+
+/*
+ * Slot table of a foam pack, for the `slots` argument of vgr_foam_infer_lanes and vgr_foam_infer_indexed. No
+ * counterpart in the reference, which keeps its per-ray colour cache of 8 direct-mapped slots (site & 7) in shared
+ * memory and counts the lookups that miss it (csrc/foam_infer.cu:151-168, 359-360). A neighbourhood pass that looks
+ * up every entry of cell c (colour cut-off +inf) hits that cache only at the first entry of a slot, and leaves the
+ * slot's last entry in it; the table holds both per site:
+ *   offsets i32 (N + 1), nbr i32 (E) as for vgr_foam_infer
+ *   -> slots i32 (N, 16), 16-byte aligned: for slots s = 0..7 of site k's self-first neighbourhood in CSR order, the
+ *      first and the last entry (F_s, L_s) at columns 2s, 2s + 1, -2 for a slot without entries; a snapshot: rebuild
+ *      after changing the pack.
+ */
+int vgr_foam_slot_table(const int32_t* offsets, const int32_t* nbr, int64_t n_sites, int64_t n_edges, int32_t* slots,
+                        void* stream);
 
 /*
  * vgr_grid_build without a workspace argument, for callers that cannot allocate device memory (code under HIP
@@ -366,7 +385,9 @@ int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* 
  * that (vgr_grid_work_size(N, G) > VGR_GRID_NOALLOC_MAX_WORK) is rejected with VGR_ERR_INVALID. It calls no
  * hipMalloc/hipFree and clears its counters with a kernel. Every call on one GPU uses that GPU's one array: calls
  * that overlap on a GPU (other streams, other host threads) race and must be serialised by the caller. The device
- * current on the calling thread must be the stream's. Same arguments and outputs as vgr_grid_build otherwise.
+ * current on the calling thread must be the stream's. The first call on each device looks the array's address up
+ * (hipGetSymbolAddress): make it outside graph capture (a warm call); every later call only launches kernels on
+ * `stream`, so it can be captured and replayed. Same arguments and outputs as vgr_grid_build otherwise.
  */
 #define VGR_GRID_NOALLOC_MAX_WORK (1LL << 24)
 int vgr_grid_build_noalloc(const float* points, int64_t n_sites, int32_t stride, const float* lo, const float* cell,

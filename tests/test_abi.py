@@ -31,7 +31,8 @@ def test_header_declares_the_entry_points():
 			  'vgr_color_backward', 'vgr_color_backward_work_size', 'vgr_conic_backward', 'vgr_pack_work_size',
 			  'vgr_pack_foam', 'vgr_morton_work_size', 'vgr_morton_codes', 'vgr_bake_colors', 'vgr_grid_work_size',
 			  'vgr_grid_build', 'vgr_grid_nearest', 'vgr_ray_order_work_size', 'vgr_ray_order', 'vgr_last_error',
-			  'vgr_abi_version', 'vgr_foam_index_pack', 'vgr_foam_infer_indexed'):
+			  'vgr_abi_version', 'vgr_foam_index_pack', 'vgr_foam_infer_indexed', 'vgr_grid_build_noalloc',
+			  'vgr_foam_slot_table'):
 		assert n in names
 
 
@@ -109,10 +110,22 @@ def test_indexed_records_arguments_without_a_gpu():
 	assert pack(10, 20) == 1 and b'null pointer' in lib.vgr_last_error()
 	assert pack(0, 0) == 0
 	args = [None, 10, None, None, None, 10, None, None, 0, 3, None, None, None, None, None, 5, 1e-4, 1e-4, 1e30, 2, 2,
-			None, None, None, None, None, None, None, 0, None, 0, None, None, None]
+			None, None, None, None, None, None, None, 0, None, 0, None, None, None, None]
 	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'edge_i and attr_i' in lib.vgr_last_error()
 	args[27], args[28] = 1, 0  # a trace sink without a capacity
 	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'trace_cap' in lib.vgr_last_error()
+
+
+def test_slot_table_arguments_without_a_gpu():
+	"""vgr_foam_slot_table validates its sizes, pointers and the table's alignment on the host; an empty pack
+	launches nothing."""
+	from vgr import _lib
+	lib = _lib.load()
+	assert lib.vgr_foam_slot_table(None, None, -1, 0, None, None) == 1 and b'n_sites' in lib.vgr_last_error()
+	assert lib.vgr_foam_slot_table(None, None, 10, 5, None, None) == 1 and b'n_edges' in lib.vgr_last_error()
+	assert lib.vgr_foam_slot_table(None, None, 10, 20, None, None) == 1 and b'null pointer' in lib.vgr_last_error()
+	assert lib.vgr_foam_slot_table(8, 8, 10, 20, 4, None) == 1 and b'aligned' in lib.vgr_last_error()
+	assert lib.vgr_foam_slot_table(None, None, 0, 0, None, None) == 0
 
 
 def test_ray_order_arguments_without_a_gpu():

@@ -17,15 +17,14 @@ TOL = 1e-4  # absolute, fp32 rgb / T / depth (north-star parity bar)
 
 
 def ref_foam(*args, **kw):
-	"""The oracle with its per-ray colour cache off: the HIP kernel caches SH coefficient blocks per wave instead
-	of colours per ray and evaluates the SH polynomial at every colour lookup, so its SH-evaluation counter
-	(stats[:, 4]) equals the oracle's count without a colour cache; colours are identical either way."""
-	kw.setdefault('use_cache', False)
+	"""The oracle with the reference's per-ray colour cache (foam_infer.cu:151-168), so stats[:, 4] on both sides
+	is the number of colour lookups that miss that 8-slot cache; colours are identical with the cache on or off."""
+	kw.setdefault('use_cache', True)
 	return oracle.foam_infer(*args, **kw)
 
 
 def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, color_cut=math.inf,
-			 color_mode=0, stage=2, cap=None, trace_cap=0, lanes=None):
+			 color_mode=0, stage=2, cap=None, trace_cap=0, lanes=None, slots=False):
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)  # noqa: E731
 	empty = torch.empty(0, dtype=torch.int32, device=dev)
 	orig = pk.get('orig')
@@ -33,7 +32,7 @@ def gpu_foam(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e
 		t(pk['points']), t(pk['offsets']), t(pk['nbr']), t(pk['edge']), t(pk['attr']), t(pk['sh']), sh_deg, t(o),
 		t(d), t(start), t(near), t(far), t_thresh, w_thresh, color_cut, color_mode, stage,
 		empty if cap is None else t(cap.astype(np.int32)), t(orig) if orig is not None and len(orig) else empty,
-		trace_cap=trace_cap, lanes=lanes)
+		trace_cap=trace_cap, lanes=lanes, slots=ext.slot_table(t(pk['offsets']), t(pk['nbr'])) if slots else None)
 	torch.cuda.synchronize()
 	res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
 	res.setdefault('trace', None)
@@ -193,6 +192,49 @@ def test_layouts_small_field(gpu, small, lanes):
 	bad[:4] = -1
 	g = gpu_foam(gpu, pk, 3, o, d, bad, near, far, lanes=lanes)
 	assert (g['T'][:4] == 1).all() and (g['rgb'][:4] == 0).all() and (g['stats'][:4] == 0).all()
+
+
+@pytest.mark.parametrize('lanes', [1, 2, 4, 8])
+def test_sh_miss_count_every_layout(gpu, small, lanes):
+	"""stats[:, 4] is the reference's count of colour lookups that miss its per-ray 8-slot cache (foam_infer.cu:
+	151-168, 359-360), in every ray layout, exact and fused colours, with and without a colour cut-off, with the
+	thresholds off (every statistic of every ray equal to the oracle's with its cache on), with the tags per lookup
+	in LDS and from the slot table once per pass (colour cut-off +inf). The count is below the number of lookups
+	(the oracle without the cache), so the cache is exercised."""
+	f, (o, d, start, near, _, far) = small
+	pk = f.pack(reorder=True)
+	st = pk['inv'][start].astype(np.int32)
+	for mode, cut, table in ((0, math.inf, False), (0, math.inf, True), (2, math.inf, False), (2, math.inf, True),
+							 (0, 2 * math.log(1e3), False), (2, 2 * math.log(1e3), True)):
+		if cut != math.inf and mode == 2 and lanes != 1:
+			continue  # a finite cut-off in fused mode always runs one ray per lane
+		# (a finite cut-off with the table given keeps per-lookup tags: the table only applies to full passes)
+		g = gpu_foam(gpu, pk, 3, o, d, st, near, far, 0.0, -1.0, color_cut=cut, color_mode=mode, trace_cap=512,
+					 lanes=lanes, slots=table)
+		r = ref_foam(pk, 3, o, d, st, near, far, 0.0, -1.0, color_cut=cut, color_mode=mode, trace_cap=512)
+		compare(g, r)
+		every = ref_foam(pk, 3, o, d, st, near, far, 0.0, -1.0, color_cut=cut, color_mode=mode, use_cache=False)
+		assert (g['stats'][:, 4] <= every['stats'][:, 4]).all()
+		assert g['stats'][:, 4].sum() < every['stats'][:, 4].sum()
+
+
+def test_slot_table_layout(gpu, small):
+	"""ext.slot_table (vgr_foam_slot_table) against a restatement on the host: per site and slot s (site & 7) of
+	its self-first neighbourhood in CSR order, the first and the last entry at columns 2s and 2s + 1, -2 for an empty
+	slot."""
+	f, _ = small
+	for reorder in (False, True):
+		pk = f.pack(reorder=reorder)
+		t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=gpu)  # noqa: E731
+		got = ext.slot_table(t(pk['offsets']), t(pk['nbr'])).cpu().numpy()
+		want = np.full((f.n, 16), -2, np.int32)
+		for k in range(f.n):
+			for j in pk['nbr'][pk['offsets'][k]:pk['offsets'][k + 1]]:
+				s = int(j) & 7
+				if want[k, 2 * s] == -2:
+					want[k, 2 * s] = j
+				want[k, 2 * s + 1] = j
+		np.testing.assert_array_equal(got, want)
 
 
 @pytest.mark.parametrize('lanes', [1, 2, 4, 8])

@@ -19,8 +19,9 @@ FIELDS = ('rgb', 'T', 'depth', 'stats', 'trace')
 
 
 def run(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, color_cut=math.inf, color_mode=2,
-		stage=2, cap=None, trace_cap=0, lanes=1, indexed=False):
-	"""One foam_infer launch on numpy inputs -> dict of numpy outputs; indexed: through index_pack's records."""
+		stage=2, cap=None, trace_cap=0, lanes=1, indexed=False, slots=False):
+	"""One foam_infer launch on numpy inputs -> dict of numpy outputs; indexed: through index_pack's records;
+	slots: with the pack's slot table (the reference's cache misses counted once per pass)."""
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)  # noqa: E731
 	empty = torch.empty(0, dtype=torch.int32, device=dev)
 	orig = pk.get('orig')
@@ -30,7 +31,8 @@ def run(dev, pk, sh_deg, o, d, start, near, far, t_thresh=1e-4, w_thresh=1e-4, c
 		tens['points'], tens['offsets'], tens['nbr'], tens['edge'], tens['attr'], tens['sh'], sh_deg, t(o), t(d),
 		t(start), t(near), t(far), t_thresh, w_thresh, color_cut, color_mode, stage,
 		empty if cap is None else t(cap.astype(np.int32)), t(orig) if orig is not None and len(orig) else empty,
-		trace_cap=trace_cap, lanes=lanes, indexed=idx)
+		trace_cap=trace_cap, lanes=lanes, indexed=idx,
+		slots=ext.slot_table(tens['offsets'], tens['nbr']) if slots else None)
 	torch.cuda.synchronize()
 	res = dict(zip(FIELDS, [x.cpu().numpy() for x in out]))
 	res.setdefault('trace', None)
@@ -86,6 +88,7 @@ def test_indexed_identical_small_field(gpu, small, sh_deg, sh_half):
 			a = run(gpu, pk, sh_deg, o, d, st, near, far, **kw)
 			b = run(gpu, pk, sh_deg, o, d, st, near, far, indexed=True, **kw)
 			assert_identical(a, b)
+			assert_identical(a, run(gpu, pk, sh_deg, o, d, st, near, far, indexed=True, slots=True, **kw))
 			if cut == math.inf and not sh_half:
 				r = ref_foam(pk, sh_deg, o, d, st, near, far, tt, wt, color_mode=2, trace_cap=512)
 				compare(b, r, exact_trace=tt == 0.0, stats_frac=1.0 if tt == 0.0 else 0.98)

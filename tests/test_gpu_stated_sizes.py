@@ -69,7 +69,7 @@ class Stated:
 		return np.arange(k // 2, self.B, k, dtype=np.int64)[:n]
 
 	def foam(self, sel=None, mode=2, t_thresh=1e-4, w_thresh=1e-4, stage=2, trace_cap=0, indexed=None, lanes=None,
-			 order=None):
+			 order=None, slots=None):
 		"""GPU foam_infer over the selected rays (all by default) -> dict of numpy arrays; indexed: the records of
 		ext.index_pack, read in place of the reference records; lanes, order: the ray layout and processing order
 		(vgr_foam_infer_lanes)."""
@@ -80,7 +80,7 @@ class Stated:
 			p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], self.sc.sh_deg, self.t(pick(self.o)),
 			self.t(pick(self.d)), self.t(pick(self.start)), self.t(pick(self.near)), self.t(pick(self.far)),
 			t_thresh, w_thresh, math.inf, mode, stage, empty, p['orig'], trace_cap=trace_cap, indexed=indexed,
-			lanes=lanes, order=order)
+			lanes=lanes, order=order, slots=slots)
 		torch.cuda.synchronize()
 		res = dict(zip(('rgb', 'T', 'depth', 'stats', 'trace'), [x.cpu().numpy() for x in out]))
 		res.setdefault('trace', None)
@@ -146,13 +146,15 @@ def test_foam_full_workload(stated):
 
 
 def test_foam_indexed_records_full_workload(stated):
-	"""The bench's default path at the stated size: fused colours through the indexed edge records over the whole
-	workload, bit-identical on every ray to the reference records (which the oracle checks above)."""
+	"""The bench's default path at the stated size: fused colours through the indexed edge records, with the
+	reference's cache misses from the slot table, over the whole workload, bit-identical on every ray to the
+	reference records with per-lookup tags (which the oracle checks above)."""
 	s = stated
 	p = s.pack
 	idx = ext.index_pack(p['offsets'], p['nbr'], p['edge'], p['attr'])
-	a, b = s.foam(), s.foam(indexed=idx)
-	del idx
+	slots = ext.slot_table(p['offsets'], p['nbr'])
+	a, b = s.foam(), s.foam(indexed=idx, slots=slots)  # b: the bench's path; a: per-lookup cache tags
+	del idx, slots
 	for k in ('rgb', 'T', 'depth'):
 		np.testing.assert_array_equal(a[k].view(np.int32), b[k].view(np.int32), err_msg=k)
 	np.testing.assert_array_equal(a['stats'], b['stats'])
@@ -165,7 +167,7 @@ def check_config5_bench_layout(s, sel, r):
 	direction bins, 7-bit origins), over the whole batch; against the oracle's rays `sel` (results r), and the same
 	cells and statistics as the one-ray-per-lane kernel with the thresholds off."""
 	order = ext.ray_order(s.t(s.o), s.t(s.d), 8, 7)
-	g = rows(s.foam(lanes=8, order=order), sel)
+	g = rows(s.foam(lanes=8, order=order, slots=ext.slot_table(s.pack['offsets'], s.pack['nbr'])), sel)
 	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
 	assert psnr(g['rgb'], r['rgb']) >= 60.0
 	few = sel[::8]

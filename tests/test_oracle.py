@@ -107,6 +107,41 @@ def test_foam_lazy_equals_fused_and_cache_is_transparent(foam_case):
 	assert nocache['stats'][:, 4].sum() > lazy['stats'][:, 4].sum()
 
 
+def direct_mapped_misses(keys, slots=8):
+	"""Misses of a direct-mapped cache of `slots` slots keyed by k mod slots that holds the last key of each slot."""
+	held = [-1] * slots
+	miss = 0
+	for k in keys:
+		s = k % slots
+		miss += held[s] != k
+		held[s] = k
+	return miss
+
+
+@pytest.mark.parametrize('mode', [0, 2])
+@pytest.mark.parametrize('reorder', [False, True])
+def test_foam_cache_miss_count_is_a_direct_mapped_cache(foam_case, mode, reorder):
+	"""stats[:, 4] with the cache on is the miss count of an 8-slot direct-mapped cache keyed by k & 7
+	(foam_infer.cu:151-168) over the ray's colour lookups. With the thresholds off and no colour cut-off the
+	lookups are, in both colour modes, every neighbourhood entry (self first, CSR order) of every sample's cell in
+	sample order, so the count follows from the cell trace alone; without the cache every lookup counts."""
+	f, _, rays = foam_case
+	pk = f.pack(reorder=reorder)
+	o, d, start, near, _, far = rays
+	st = pk['inv'][start].astype(np.int32) if reorder else start
+	out = oracle.foam_infer(pk, f.sh_deg, o, d, st, near, far, 0.0, -1.0, color_mode=mode, trace_cap=4096)
+	every = oracle.foam_infer(pk, f.sh_deg, o, d, st, near, far, 0.0, -1.0, color_mode=mode, use_cache=False)
+	inv = pk['inv'] if reorder else np.arange(f.n)
+	offsets, nbr = pk['offsets'], pk['nbr']
+	for r in range(len(o)):
+		n = out['stats'][r, 0]
+		cells = inv[out['trace'][r, :n]]  # trace in original numbering -> the pack's numbering
+		keys = [int(k) for c in cells for k in nbr[offsets[c]:offsets[c + 1]]]
+		assert every['stats'][r, 4] == len(keys)
+		assert out['stats'][r, 4] == direct_mapped_misses(keys), f'ray {r}'
+	assert out['stats'][:, 4].sum() < every['stats'][:, 4].sum()
+
+
 def test_foam_morton_reorder_is_invariant(foam_case):
 	"""Renumbering the sites (Z-order, render.py:213-222) changes nothing but the cache statistics: same values
 	bit for bit and the same cell sequences in original numbering."""

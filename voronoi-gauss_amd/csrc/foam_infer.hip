@@ -12,6 +12,8 @@
 // A second layout, a group of 2, 4 or 8 lanes per ray (foam_group_kernel below), splits each cell's
 // neighbourhood over the group's lanes; it is the faster one for traversal, density and lazy colours, one ray per
 // lane for fused and baked colours (default_lanes).
+#include <cmath>
+
 #include "vgr_abi.h"
 #include "vgr_device.h"
 
@@ -33,6 +35,7 @@ struct FoamScene {
     const float4* __restrict__ attr;    // (N, 5)
     const float4* __restrict__ sh;      // (N, 12) fp32 or (N, 6) fp16
     const int* __restrict__ orig;       // (N) or null
+    const int4* __restrict__ slots;     // (N, 4) slot table (vgr_foam_slot_table) or null
     int n_sites;
 };
 
@@ -158,8 +161,18 @@ __device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int 
 // direct-mapped slots (site k mod SLOTS) plus `overflow` blocks used within one lookup, stored [12][blocks] float4
 // so that lanes reading different slots hit different banks. The 64 rays of a tile read overlapping sets of sites
 // (45 % of the lookups find their block in LDS on the config-3 scene); the colour itself, max(SH_k(d) + 1/2, 0), is
-// evaluated per lane since it depends on the ray direction. n_sh counts the SH evaluations, i.e. every colour
-// lookup.
+// evaluated per lane since it depends on the ray direction.
+//
+// n_sh (stats[:, 4]) is the reference's count: the colour lookups that miss its per-ray cache of 8 direct-mapped
+// slots keyed by k & 7, each holding the last site looked up in it (foam_infer.cu:151-168). A hit there returns the
+// colour computed at the earlier lookup, the same bits the SH evaluation gives, so only the tags are kept, in one of
+// two ways:
+// - with a slot table (TABLE; the colour cut-off is +inf, so a pass looks up every entry of the cell's
+//   neighbourhood in CSR order): within one pass the sites are distinct, so a lookup can hit only as the first
+//   entry of its slot in the pass, and only if the ray's tag of that slot is that site; after the pass the slot
+//   holds its last entry. The table gives each site's first and last entry of every slot, so the 8 tags live in
+//   registers and are checked and replaced once per pass, with static slot indices;
+// - otherwise 8 tags per ray in the wave's LDS, checked and replaced at every lookup in the reference's order.
 //
 // Tuning per colour mode, measured on config 3. Fused and baked colours: 24 slots and 4 overflow blocks (5.8 KB of
 // LDS per wave), so that 24 waves (6 per SIMD) fit in a CU's 160 KB, and no software pipelining: the registers that
@@ -180,11 +193,17 @@ __device__ __forceinline__ int slot_of(int k) {
     return static_cast<int>(static_cast<uint32_t>(k) % SLOTS);
 }
 
+// Entry e of a neighbourhood [e0, e1) for a load issued ahead of the loop that may not run: clamped into the cell,
+// and for an empty cell (no self entry, which no pack_foam pack has) to the entry before it, so the load stays in
+// bounds whatever the offsets.
+__device__ __forceinline__ int entry_in(int e, int e1) { return max(min(e, e1 - 1), 0); }
+
 // Volatile ints typed as LDS: the election and tag accesses stay ds_read / ds_write. Through a generic pointer
 // they would be flat accesses, after each of which the wave waits for all of its outstanding global loads.
 typedef __attribute__((address_space(3))) volatile int lds_int;
 
-// The cache of one wave for colour mode COLOR (Tune<COLOR>: `slots` cached slots and `overflow` blocks).
+// The cache of one wave for colour mode COLOR (Tune<COLOR>: `slots` cached slots and `overflow` blocks), and the
+// reference's per-ray colour-cache tags of the wave's rays.
 template <int COLOR>
 struct ColorCache {
     float4* data;    // [12][slots + overflow] coefficient blocks: the cached slots, then the overflow blocks
@@ -194,17 +213,32 @@ struct ColorCache {
     lds_int* ovf_b;  // ... and that block (-1: none)
     lds_int* req_k;  // sites fetched by the current fill ...
     lds_int* req_b;  // ... and their blocks
+    lds_int* rtag;   // this ray's tag of slot 0 of the reference's per-ray cache; slot s at rtag[s * rays]
+    int rays;        // rays per wave (the tags are stored [8][rays], conflict-free across the wave's rays)
 };
 
-// LDS footprint per block of the colour cache, in float4 units (the words follow the coefficient blocks).
-template <int COLOR>
+constexpr int kRayTagSlots = 8;  // the reference's per-ray colour cache: 8 direct-mapped slots (k & 7)
+
+// LDS footprint of the colour cache of a wave rendering RAYS rays, in float4 units (the words follow the coefficient
+// blocks, then the per-ray tags).
+template <int COLOR, int RAYS, bool TABLE>
 constexpr int cache_vec4(bool sh) {
-    constexpr int S = Tune<COLOR>::slots, O = Tune<COLOR>::overflow;
-    return sh ? 12 * (S + O) + (2 * S + (O > 0 ? 2 * S : 0) + 2 * (S + O) + 3) / 4 : 1;
+    constexpr int S = Tune<COLOR>::slots, O = Tune<COLOR>::overflow, TAGS = TABLE ? 0 : kRayTagSlots * RAYS;
+    return sh ? 12 * (S + O) + (2 * S + (O > 0 ? 2 * S : 0) + 2 * (S + O) + TAGS + 3) / 4 : 1;
 }
 
-template <int COLOR>
-__device__ __forceinline__ ColorCache<COLOR> make_cache(float4* lds) {
+// Waves per SIMD a kernel is compiled for: Tune's count, or fewer when its LDS (the colour cache and, without the
+// slot table, the per-ray tags) does not fit that many workgroups of one wave in a CU's 160 KB.
+template <int COLOR, int RAYS, bool TABLE>
+constexpr int waves_for(bool sh) {
+    constexpr int kCuLds = 160 * 1024, kSimds = 4;
+    const int fit = kCuLds / (16 * cache_vec4<COLOR, RAYS, TABLE>(sh)) / kSimds;
+    return fit < Tune<COLOR>::waves ? (fit < 1 ? 1 : fit) : Tune<COLOR>::waves;
+}
+
+// Sets up the wave's cache; `ray` is the lane's ray within the wave (0 .. RAYS - 1). TABLE: no LDS tags.
+template <int COLOR, int RAYS, bool TABLE>
+__device__ __forceinline__ ColorCache<COLOR> make_cache(float4* lds, int ray) {
     constexpr int S = Tune<COLOR>::slots, O = Tune<COLOR>::overflow;
     ColorCache<COLOR> C;
     C.data = lds;
@@ -214,9 +248,38 @@ __device__ __forceinline__ ColorCache<COLOR> make_cache(float4* lds) {
     C.ovf_b = C.ovf_k + (O > 0 ? S : 0);
     C.req_k = C.ovf_b + (O > 0 ? S : 0);
     C.req_b = C.req_k + S + O;
+    C.rays = RAYS;
+    C.rtag = C.req_b + S + O + ray;
     for (int i = threadIdx.x; i < S; i += kBlock) C.tag[i] = -1, C.claim[i] = -1;
+    if (!TABLE)
+        for (int i = threadIdx.x; i < kRayTagSlots * RAYS; i += kBlock) C.req_b[S + O + i] = -1;
     __syncthreads();
     return C;
+}
+
+// 1 if site k misses this ray's slot k & 7 of the reference's colour cache, which then holds k; a lane alone on its
+// ray (one ray per lane).
+template <int COLOR>
+__device__ __forceinline__ int ray_tag_miss(ColorCache<COLOR>& C, int k) {
+    lds_int* p = C.rtag + (k & (kRayTagSlots - 1)) * C.rays;
+    const int held = *p;
+    *p = k;
+    return held != k ? 1 : 0;
+}
+
+// The same for a group of G lanes per ray whose lane g looks up site k when `look` is set, in one round of a
+// neighbourhood pass: the reference's order of these lookups is lane 0, 1, ..., G - 1 (lane g takes the edges
+// g, g + G, ... of the cell), so the lanes check and replace their tags in G steps of that order, one lane of every
+// group per step. Called with the group's lanes converged (each lane's `look` says whether it looks up).
+template <int G, int COLOR>
+__device__ __forceinline__ int group_tag_miss(ColorCache<COLOR>& C, int g, bool look, int k) {
+    lds_int* p = C.rtag + (k & (kRayTagSlots - 1)) * C.rays;
+    int held = k;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        if (look && g == j) held = *p, *p = k;
+    }
+    return held != k ? 1 : 0;
 }
 
 // Number of set bits of `mask` below this lane.
@@ -318,6 +381,52 @@ __device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4
     }
 }
 
+// The ray's tags of the slots a lane keeps (all 8 with one ray per lane; g, g + G, ... in a group of G lanes), for
+// the slot-table accounting.
+// The tags stay in the lane's private (scratch) memory between passes: they are read and written once per pass, and
+// kept in registers they would push more of the neighbourhood loop's state out to scratch.
+template <int G>
+struct SlotTags {
+    static constexpr int n = kRayTagSlots / G;
+    volatile int t[n];
+};
+
+template <int G>
+__device__ __forceinline__ void tags_init(SlotTags<G>& T) {
+#pragma unroll
+    for (int i = 0; i < SlotTags<G>::n; ++i) T.t[i] = -1;
+}
+
+// One pass over the neighbourhood of cell c looked up every entry: returns the lookups of the lane's slots that hit
+// the ray's cache (their first entry in the pass is the site the tag holds) and replaces those tags with the slots'
+// last entries. Slot table row of site c: (F0, L0, F1, L1), ..., (F6, L6, F7, L7), first and last entry of each
+// slot, -2 for a slot without entries.
+template <int G>
+__device__ __forceinline__ int table_hits(const FoamScene& S, int c, int g, SlotTags<G>& T) {
+    const int4* row = S.slots + 4 * static_cast<int64_t>(c);
+    int hits = 0;
+    if constexpr (G == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // slots 2q and 2q + 1
+            const int4 v = row[q];
+            hits += v.x == T.t[2 * q] ? 1 : 0;
+            T.t[2 * q] = v.y >= 0 ? v.y : T.t[2 * q];
+            hits += v.z == T.t[2 * q + 1] ? 1 : 0;
+            T.t[2 * q + 1] = v.w >= 0 ? v.w : T.t[2 * q + 1];
+            __builtin_amdgcn_sched_barrier(0);  // one int4 of the row in registers at a time
+        }
+    } else {
+        const int2* fl = reinterpret_cast<const int2*>(row);
+#pragma unroll
+        for (int i = 0; i < SlotTags<G>::n; ++i) {
+            const int2 v = fl[g + G * i];
+            hits += v.x == T.t[i] ? 1 : 0;
+            T.t[i] = v.y >= 0 ? v.y : T.t[i];
+        }
+    }
+    return hits;
+}
+
 // Number of float4 a colour fetch reads: the blocks holding coefficients of degree <= DEG (the others multiply a
 // zero basis value, so leaving them out changes no finite colour).
 template <bool HALF, int DEG>
@@ -387,7 +496,7 @@ __device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
 // Mahalanobis distance (lazy) or running colour blend (fused, baked), and, when want_exit, the exit face.
 // Pipelined (Tune): the edge record of e + 2 and the site records of e + 1 are loaded while edge e is evaluated,
 // indices clamped to the cell so every load stays in bounds.
-template <int STAGE, int COLOR, bool HALF, int DEG>
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TABLE>
 __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float t, const float (&o)[3],
                           const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
                           bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
@@ -405,8 +514,8 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
     float4 edn;
     int kn = 0;
     if constexpr (PREF) {
-        edn = S.edge[e0];
-        if constexpr (!IDX) kn = S.nbr[e0];
+        edn = S.edge[entry_in(e0, e1)];
+        if constexpr (!IDX) kn = S.nbr[entry_in(e0, e1)];
     }
     const float4 pc = PREF && !IDX ? edn : S.points[c];
     float x[3];
@@ -419,8 +528,8 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
     int k, k1;
     SiteRec q;
     if constexpr (PIPE) {
-        ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
-        k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+        ed = S.edge[entry_in(e0, e1)], ed1 = S.edge[entry_in(e0 + 1, e1)];
+        k = S.nbr[entry_in(e0, e1)], k1 = S.nbr[entry_in(e0 + 1, e1)];
         q = site_rec<STAGE>(S, k);
     }
     for (int e = e0; e < e1; ++e) {
@@ -464,7 +573,8 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                                 const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
                                 c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
                             } else {
-                                ++n_sh;
+                                if constexpr (TABLE) ++n_sh;  // the pass's hits come off in table_hits
+                                else n_sh += ray_tag_miss(cache, k);
                                 cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
                             }
                             blend_add(R.B, m, c3[0], c3[1], c3[2]);
@@ -481,7 +591,7 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
 
 // Lazy colour of the sample o + t d in cell c, given its smallest colour Mahalanobis distance mmin (lazy mode only,
 // pipelined as eval_cell is).
-template <bool HALF, int DEG>
+template <bool HALF, int DEG, bool TABLE>
 __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float t, float mmin, const float (&o)[3],
                            const float (&d)[3], const float (&b)[16], ColorCache<kLazy>& cache,
                            float (&C)[3], int& n_sh) {
@@ -495,8 +605,8 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
     float4 ed, ed1, q2, q3;
     int k, k1;
     if constexpr (PIPE) {
-        ed = S.edge[e0], ed1 = S.edge[min(e0 + 1, last)];
-        k = S.nbr[e0], k1 = S.nbr[min(e0 + 1, last)];
+        ed = S.edge[entry_in(e0, e1)], ed1 = S.edge[entry_in(e0 + 1, e1)];
+        k = S.nbr[entry_in(e0, e1)], k1 = S.nbr[entry_in(e0 + 1, e1)];
         q2 = S.attr[5 * static_cast<int64_t>(k) + 2], q3 = S.attr[5 * static_cast<int64_t>(k) + 3];
     }
     for (int e = e0; e < e1; ++e) {
@@ -518,7 +628,8 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
             const float m = maha_f(q2, q3, v0, v1, v2);
             if (m <= cut) {
                 float c3[3];
-                ++n_sh;
+                if constexpr (TABLE) ++n_sh;
+                else n_sh += ray_tag_miss(cache, k);
                 cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
                 accumulate(A, r, g, bl, weight_of(m, mmin), c3);
             }
@@ -534,17 +645,20 @@ __device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O,
     if (TRACE && s < O.trace_cap) O.trace[r * O.trace_cap + s] = S.orig != nullptr ? S.orig[c] : c;
 }
 
-// The register allocation is bounded for Tune<COLOR>::waves waves per SIMD. At 6 the fused fp32 degree-3 kernel
-// spills 12 VGPRs and is the fastest measured (207 ms on config 3); at 4 it takes 114 VGPRs and 233 ms, at 7 it
-// spills 45 and takes 257 ms.
-template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
-__global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
+// The register allocation is bounded for waves_for waves per SIMD (Tune<COLOR>::waves unless the LDS allows fewer).
+// Six waves per SIMD is the fastest occupancy measured for the fused fp32 degree-3 kernel on config 3 although it
+// spills: 80 VGPRs, the rest of the ray's state (accumulated colour and depth, the basis) stored to scratch once
+// per sample, outside the neighbourhood loop; at 4 waves it needs no spills and ran 27 % slower, at 7 it spills
+// inside the loop.
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, bool TABLE>
+__global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE >= 2 && COLOR != kBaked)))
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    __shared__ float4 cache_lds[cache_vec4<COLOR>(kSH)];
+    constexpr bool FUSED_SH = BLEND && COLOR != kBaked;
+    __shared__ float4 cache_lds[cache_vec4<COLOR, kBlock, TABLE>(kSH)];
     ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache<COLOR>(cache_lds);
+    if (kSH) cache = make_cache<COLOR, kBlock, TABLE>(cache_lds, static_cast<int>(threadIdx.x));
     const int64_t i = xcd_block_id() * kBlock + threadIdx.x;
     if (i >= R.n) return;
     const int64_t r = R.order != nullptr ? R.order[i] : i;
@@ -567,10 +681,13 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
+    SlotTags<1> tags;
+    tags_init(tags);
     int c = walk_to<COLOR == kFusedIdx>(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2],
                                         walk_steps);
     CellEval E;
-    eval_cell<STAGE, COLOR, HALF, DEG>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    if (TABLE && FUSED_SH) n_sh -= table_hits<1>(S, c, 0, tags);
     trace_cell<TRACE>(S, O, r, 0, c);
     float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
     bool hasP = false;
@@ -585,7 +702,8 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
         const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
         const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
         const int cQ = last ? c : E.next;
-        eval_cell<STAGE, COLOR, HALF, DEG>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        if (TABLE && FUSED_SH) n_sh -= table_hits<1>(S, cQ, 0, tags);
         trace_cell<TRACE>(S, O, r, n_samples, cQ);
         ++n_samples;
         const float sQ = E.sigma, mQ = E.mmin;
@@ -600,8 +718,12 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
         }
         if (STAGE >= 2 && w > P.w_thresh) {
             if constexpr (!BLEND) {
-                if (!hasP) color_lazy<HALF, DEG>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
-                color_lazy<HALF, DEG>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                if (!hasP) {
+                    color_lazy<HALF, DEG, TABLE>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
+                    if (TABLE) n_sh -= table_hits<1>(S, cP, 0, tags);
+                }
+                color_lazy<HALF, DEG, TABLE>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                if (TABLE) n_sh -= table_hits<1>(S, cQ, 0, tags);
                 hasQ = true;
             }
 #pragma unroll
@@ -730,7 +852,7 @@ __device__ int walk_group(const FoamScene& S, int c, int g, float x0, float x1, 
 }
 
 // eval_cell for lane g of a group: the lane's share of the neighbourhood, then the group reductions.
-template <int STAGE, int COLOR, bool HALF, int DEG, int G>
+template <int STAGE, int COLOR, bool HALF, int DEG, int G, bool TABLE>
 __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, const float (&o)[3],
                                 const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
                                 bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
@@ -747,7 +869,7 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
     float4 edn;
     int kn = 0;
     if constexpr (PREF) {
-        const int ef = min(e0 + g, e1 - 1);
+        const int ef = entry_in(e0 + g, e1);
         edn = S.edge[ef], kn = S.nbr[ef];
     }
     for (int e = e0 + g; e < e1; e += G) {
@@ -779,19 +901,22 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
                 const float lb = r2 * cut.y;
                 if (BLEND) {
                     const float lim = R.B.m + P.color_cut;
-                    if (lb <= lim) {
-                        const float m = maha_f(q.q2, q.q3, v0, v1, v2);
-                        if (m <= lim) {
-                            float c3[3];
-                            if (COLOR == kBaked) {
-                                const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
-                                c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
-                            } else {
-                                ++n_sh;
-                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
-                            }
-                            blend_add(R.B, m, c3[0], c3[1], c3[2]);
+                    float m = kInf;
+                    if (lb <= lim) m = maha_f(q.q2, q.q3, v0, v1, v2);
+                    const bool look = lb <= lim && m <= lim;
+                    if (COLOR != kBaked) {
+                        if constexpr (TABLE) n_sh += look ? 1 : 0;  // the pass's hits come off in table_hits
+                        else n_sh += group_tag_miss<G>(cache, g, look, k);  // the group's lanes converged
+                    }
+                    if (look) {
+                        float c3[3];
+                        if (COLOR == kBaked) {
+                            const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
+                            c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
+                        } else {
+                            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
                         }
+                        blend_add(R.B, m, c3[0], c3[1], c3[2]);
                     }
                 } else if (lb < R.mmin) {
                     R.mmin = fminf(R.mmin, maha_f(q.q2, q.q3, v0, v1, v2));
@@ -807,7 +932,7 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
 
 // color_lazy for lane g of a group: weights relative to the group's mmin, so the colour-cut tests are those of a
 // sequential scan; the weighted sums are combined at the end.
-template <bool HALF, int DEG, int G>
+template <bool HALF, int DEG, int G, bool TABLE>
 __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, float mmin,
                                  const float (&o)[3], const float (&d)[3], const float (&b)[16],
                                  ColorCache<kLazy>& cache, float (&C)[3], int& n_sh) {
@@ -823,14 +948,16 @@ __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c,
         const float4 q2 = a[2], q3 = a[3];
         float v0, v1, v2, r2;
         offset_of(x, ed, v0, v1, v2, r2);
-        if (r2 * cutoffs(ed.w).y <= cut) {
-            const float m = maha_f(q2, q3, v0, v1, v2);
-            if (m <= cut) {
-                float c3[3];
-                ++n_sh;
-                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
-                accumulate(A, r, gr, bl, weight_of(m, mmin), c3);
-            }
+        const bool near_enough = r2 * cutoffs(ed.w).y <= cut;
+        float m = kInf;
+        if (near_enough) m = maha_f(q2, q3, v0, v1, v2);
+        const bool look = near_enough && m <= cut;
+        if constexpr (TABLE) n_sh += look ? 1 : 0;
+        else n_sh += group_tag_miss<G>(cache, g, look, k);  // the group's lanes converged
+        if (look) {
+            float c3[3];
+            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+            accumulate(A, r, gr, bl, weight_of(m, mmin), c3);
         }
     }
     A = group_sum<G>(A), r = group_sum<G>(r), gr = group_sum<G>(gr), bl = group_sum<G>(bl);
@@ -839,14 +966,15 @@ __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c,
 }
 
 // foam_infer_kernel with a group of G lanes per ray; same outputs (the group's lane 0 writes them).
-template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, int G>
-__global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, int G, bool TABLE>
+__global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock / G, TABLE>(STAGE >= 2 && COLOR != kBaked)))
     foam_group_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
-    __shared__ float4 cache_lds[cache_vec4<COLOR>(kSH)];
+    constexpr bool FUSED_SH = BLEND && COLOR != kBaked;
+    __shared__ float4 cache_lds[cache_vec4<COLOR, kBlock / G, TABLE>(kSH)];
     ColorCache<COLOR> cache{};  // set up by every lane of the block before any returns
-    if (kSH) cache = make_cache<COLOR>(cache_lds);
+    if (kSH) cache = make_cache<COLOR, kBlock / G, TABLE>(cache_lds, static_cast<int>(threadIdx.x) / G);
     const int g = static_cast<int>(threadIdx.x) % G;
     const int64_t i = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
     if (i >= R.n) return;  // whole groups leave together
@@ -873,9 +1001,12 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
     if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
+    SlotTags<G> tags;
+    tags_init(tags);
     int c = walk_group<G>(S, start, g, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2], walk_steps);
     CellEval E;
-    eval_cell_group<STAGE, COLOR, HALF, DEG, G>(S, P, c, g, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    eval_cell_group<STAGE, COLOR, HALF, DEG, G, TABLE>(S, P, c, g, t_near, o, d, b, cache, true, E, n_dens, n_sh);
+    if (TABLE && FUSED_SH) n_sh -= table_hits<G>(S, c, g, tags);
     if (writer) trace_cell<TRACE>(S, O, r, 0, c);
     float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
     bool hasP = false;
@@ -890,7 +1021,8 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
         const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
         const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
         const int cQ = last ? c : E.next;
-        eval_cell_group<STAGE, COLOR, HALF, DEG, G>(S, P, cQ, g, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        eval_cell_group<STAGE, COLOR, HALF, DEG, G, TABLE>(S, P, cQ, g, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
+        if (TABLE && FUSED_SH) n_sh -= table_hits<G>(S, cQ, g, tags);
         if (writer) trace_cell<TRACE>(S, O, r, n_samples, cQ);
         ++n_samples;
         const float sQ = E.sigma, mQ = E.mmin;
@@ -905,8 +1037,12 @@ __global__ void __launch_bounds__(kBlock, Tune<COLOR>::waves)
         }
         if (STAGE >= 2 && w > P.w_thresh) {
             if constexpr (!BLEND) {
-                if (!hasP) color_lazy_group<HALF, DEG, G>(S, P, cP, g, tP, mP, o, d, b, cache, CP, n_sh);
-                color_lazy_group<HALF, DEG, G>(S, P, cQ, g, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                if (!hasP) {
+                    color_lazy_group<HALF, DEG, G, TABLE>(S, P, cP, g, tP, mP, o, d, b, cache, CP, n_sh);
+                    if (TABLE) n_sh -= table_hits<G>(S, cP, g, tags);
+                }
+                color_lazy_group<HALF, DEG, G, TABLE>(S, P, cQ, g, tQ, mQ, o, d, b, cache, CQ, n_sh);
+                if (TABLE) n_sh -= table_hits<G>(S, cQ, g, tags);
                 hasQ = true;
             }
 #pragma unroll
@@ -948,70 +1084,117 @@ __global__ void __launch_bounds__(256) index_pack_kernel(const int* __restrict__
     if (j >= 20 * n_sites) return;
     const int64_t k = j / 20;
     const int col = static_cast<int>(j - 20 * k);
-    attr_i[j] = col == 7 ? edge[offsets[k]].w : attr[j];
+    if (col != 7) {
+        attr_i[j] = attr[j];
+    } else {  // the self entry's word; 0 for a site without entries (never a neighbour of a consistent graph)
+        const int e0 = offsets[k];
+        attr_i[j] = e0 < offsets[k + 1] && e0 < n_edges ? edge[e0].w : 0.f;
+    }
 }
 
 // The fused blend over the indexed edge records: one ray per lane.
-template <bool HALF, bool TRACE>
+template <bool HALF, bool TRACE, bool TABLE>
 int launch_indexed(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
     const dim3 grid(grid_for(R.n, kBlock)), block(kBlock);
     switch (P.sh_deg) {
-        case 0: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 0, TRACE>), grid, block, 0, stream, S, P, R, O); break;
-        case 1: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 1, TRACE>), grid, block, 0, stream, S, P, R, O); break;
-        case 2: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 2, TRACE>), grid, block, 0, stream, S, P, R, O); break;
-        default: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 3, TRACE>), grid, block, 0, stream, S, P, R, O);
+        case 0: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 0, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
+        case 1: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 1, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
+        case 2: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 2, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
+        default: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 3, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O);
     }
     return launch_status("foam_infer_kernel (indexed edges)");
 }
 
 // lanes: 1 = one ray per lane (foam_infer_kernel), 2, 4 or 8 = a group of that many lanes per ray
-// (foam_group_kernel).
-template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE>
+// (foam_group_kernel). TABLE: the reference's cache tags from the slot table (colour cut-off +inf).
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, bool TABLE = false>
 int launch(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes,
            hipStream_t stream) {
     if (lanes == 2) {
-        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 2>), dim3(grid_for(R.n, kBlock / 2)),
-                           dim3(kBlock), 0, stream, S, P, R, O);
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 2, TABLE>),
+                           dim3(grid_for(R.n, kBlock / 2)), dim3(kBlock), 0, stream, S, P, R, O);
         return launch_status("foam_group_kernel");
     }
     if (lanes == 4) {
-        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 4>), dim3(grid_for(R.n, kBlock / 4)),
-                           dim3(kBlock), 0, stream, S, P, R, O);
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 4, TABLE>),
+                           dim3(grid_for(R.n, kBlock / 4)), dim3(kBlock), 0, stream, S, P, R, O);
         return launch_status("foam_group_kernel");
     }
     if (lanes == 8) {
-        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 8>), dim3(grid_for(R.n, kBlock / 8)),
-                           dim3(kBlock), 0, stream, S, P, R, O);
+        hipLaunchKernelGGL((foam_group_kernel<STAGE, COLOR, HALF, DEG, TRACE, 8, TABLE>),
+                           dim3(grid_for(R.n, kBlock / 8)), dim3(kBlock), 0, stream, S, P, R, O);
         return launch_status("foam_group_kernel");
     }
-    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, DEG, TRACE>), dim3(grid_for(R.n, kBlock)), dim3(kBlock),
-                       0, stream, S, P, R, O);
+    hipLaunchKernelGGL((foam_infer_kernel<STAGE, COLOR, HALF, DEG, TRACE, TABLE>), dim3(grid_for(R.n, kBlock)),
+                       dim3(kBlock), 0, stream, S, P, R, O);
     return launch_status("foam_infer_kernel");
 }
 
-// Kernels with SH colours are specialised on the SH degree (block size and basis known at compile time).
-template <int COLOR, bool HALF, bool TRACE>
-int launch_sh(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes,
-              hipStream_t stream) {
+// Kernels with SH colours are specialised on the SH degree (block size and basis known at compile time) and on how
+// they keep the reference's cache tags.
+template <int COLOR, bool HALF, bool TRACE, bool TABLE>
+int launch_deg(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes,
+               hipStream_t stream) {
     switch (P.sh_deg) {
-        case 0: return launch<2, COLOR, HALF, 0, TRACE>(S, P, R, O, lanes, stream);
-        case 1: return launch<2, COLOR, HALF, 1, TRACE>(S, P, R, O, lanes, stream);
-        case 2: return launch<2, COLOR, HALF, 2, TRACE>(S, P, R, O, lanes, stream);
-        default: return launch<2, COLOR, HALF, 3, TRACE>(S, P, R, O, lanes, stream);
+        case 0: return launch<2, COLOR, HALF, 0, TRACE, TABLE>(S, P, R, O, lanes, stream);
+        case 1: return launch<2, COLOR, HALF, 1, TRACE, TABLE>(S, P, R, O, lanes, stream);
+        case 2: return launch<2, COLOR, HALF, 2, TRACE, TABLE>(S, P, R, O, lanes, stream);
+        default: return launch<2, COLOR, HALF, 3, TRACE, TABLE>(S, P, R, O, lanes, stream);
     }
+}
+
+template <int COLOR, bool HALF, bool TRACE>
+int launch_sh(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, int lanes, bool table,
+              hipStream_t stream) {
+    return table ? launch_deg<COLOR, HALF, TRACE, true>(S, P, R, O, lanes, stream)
+                 : launch_deg<COLOR, HALF, TRACE, false>(S, P, R, O, lanes, stream);
 }
 
 template <bool TRACE>
 int dispatch(int stage, int color_mode, bool half, const FoamScene& S, const FoamParams& P, const FoamRays& R,
-             const FoamOut& O, int lanes, hipStream_t stream) {
+             const FoamOut& O, int lanes, bool table, hipStream_t stream) {
     if (stage == 0) return launch<0, kLazy, false, 0, TRACE>(S, P, R, O, lanes, stream);
     if (stage == 1) return launch<1, kLazy, false, 0, TRACE>(S, P, R, O, lanes, stream);
     if (color_mode == kBaked) return launch<2, kBaked, false, 0, TRACE>(S, P, R, O, lanes, stream);
     if (color_mode == kLazy)
-        return half ? launch_sh<kLazy, true, TRACE>(S, P, R, O, lanes, stream)
-                    : launch_sh<kLazy, false, TRACE>(S, P, R, O, lanes, stream);
-    return half ? launch_sh<kFused, true, TRACE>(S, P, R, O, lanes, stream)
-                : launch_sh<kFused, false, TRACE>(S, P, R, O, lanes, stream);
+        return half ? launch_sh<kLazy, true, TRACE>(S, P, R, O, lanes, table, stream)
+                    : launch_sh<kLazy, false, TRACE>(S, P, R, O, lanes, table, stream);
+    return half ? launch_sh<kFused, true, TRACE>(S, P, R, O, lanes, table, stream)
+                : launch_sh<kFused, false, TRACE>(S, P, R, O, lanes, table, stream);
+}
+
+template <bool HALF>
+int dispatch_indexed(bool trace, bool table, const FoamScene& S, const FoamParams& P, const FoamRays& R,
+                     const FoamOut& O, hipStream_t s) {
+    if (trace) return table ? launch_indexed<HALF, true, true>(S, P, R, O, s) : launch_indexed<HALF, true, false>(S, P, R, O, s);
+    return table ? launch_indexed<HALF, false, true>(S, P, R, O, s) : launch_indexed<HALF, false, false>(S, P, R, O, s);
+}
+
+// Slot table of the reference's per-ray colour cache: for site k, the first and the last entry of every slot
+// (entry site j mod 8) of its self-first neighbourhood, in CSR order, -2 for a slot without entries; stored as
+// (F0, L0, F1, L1), ..., (F6, L6, F7, L7). One lane per site.
+__global__ void __launch_bounds__(256) slot_table_kernel(const int* __restrict__ offsets, const int* __restrict__ nbr,
+                                                         int64_t n_sites, int4* __restrict__ slots) {
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= n_sites) return;
+    int F[8], L[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) F[s] = L[s] = -2;
+    const int e1 = offsets[k + 1];
+    for (int e = offsets[k]; e < e1; ++e) {
+        const int j = nbr[e];
+        const int s = j & (kRayTagSlots - 1);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {  // static indices: the arrays stay in registers
+            if (u == s) {
+                F[u] = F[u] == -2 ? j : F[u];
+                L[u] = j;
+            }
+        }
+    }
+    int4* row = slots + 4 * k;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) row[q] = make_int4(F[2 * q], L[2 * q], F[2 * q + 1], L[2 * q + 1]);
 }
 
 // Lanes per ray of vgr_foam_infer and vgr_foam_infer_traced, the faster layout per path on config 3 (8.29M rays,
@@ -1032,7 +1215,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
                int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream,
-               const float* edge_i = nullptr, const float* attr_i = nullptr) {
+               const float* edge_i = nullptr, const float* attr_i = nullptr, const int32_t* slots = nullptr) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     // the indexed edge records serve the fused blend with one ray per lane (its default layout)
     const bool indexed = edge_i != nullptr && attr_i != nullptr && stage == 2 && color_mode == kFused &&
@@ -1063,6 +1246,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                       reinterpret_cast<const float4*>(indexed ? attr_i : attr),
                       needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
                       orig,
+                      reinterpret_cast<const int4*>(slots),
                       static_cast<int>(n_sites)};
     const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
                        static_cast<int>(sh_deg)};
@@ -1072,13 +1256,15 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
     // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
     if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
-    if (indexed) {
-        const bool half = sh_half != 0;
-        if (trace != nullptr) return half ? launch_indexed<true, true>(S, P, R, O, s) : launch_indexed<false, true>(S, P, R, O, s);
-        return half ? launch_indexed<true, false>(S, P, R, O, s) : launch_indexed<false, false>(S, P, R, O, s);
-    }
-    if (trace != nullptr) return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
-    return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), s);
+    // The slot table gives the reference's cache misses per pass when a pass looks up every entry: colour cut-off
+    // +inf (a pass with a finite cut-off skips entries, and keeps its tags in LDS per lookup).
+    const bool table = slots != nullptr && std::isinf(color_cut) && color_cut > 0;
+    if (indexed)
+        return sh_half != 0 ? dispatch_indexed<true>(trace != nullptr, table, S, P, R, O, s)
+                            : dispatch_indexed<false>(trace != nullptr, table, S, P, R, O, s);
+    if (trace != nullptr)
+        return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), table, s);
+    return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), table, s);
 }
 
 }  // namespace
@@ -1117,11 +1303,13 @@ extern "C" int vgr_foam_infer_lanes(const float* points, int64_t n_sites, const 
                                     double t_thresh, double w_thresh, double color_cut, int64_t color_mode,
                                     int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
                                     float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
-                                    const int32_t* order, int64_t lanes_per_ray, void* stream) {
+                                    const int32_t* order, int64_t lanes_per_ray, const int32_t* slots,
+                                    void* stream) {
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_lanes: trace needs trace_cap > 0");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
-                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream);
+                           T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream,
+                           nullptr, nullptr, slots);
 }
 
 extern "C" int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float* edge, const float* attr,
@@ -1145,11 +1333,23 @@ extern "C" int vgr_foam_infer_indexed(const float* points, int64_t n_sites, cons
                                       int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
                                       float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                                       const int32_t* order, int64_t lanes_per_ray, const float* edge_i,
-                                      const float* attr_i, void* stream) {
+                                      const float* attr_i, const int32_t* slots, void* stream) {
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_indexed: trace needs trace_cap > 0");
     VGR_REQUIRE(edge_i && attr_i, "foam_infer_indexed: edge_i and attr_i are required");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
                            T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream,
-                           edge_i, attr_i);
+                           edge_i, attr_i, slots);
+}
+
+extern "C" int vgr_foam_slot_table(const int32_t* offsets, const int32_t* nbr, int64_t n_sites, int64_t n_edges,
+                                   int32_t* slots, void* stream) {
+    VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "foam_slot_table: n_sites must be in [0, 2^31)");
+    VGR_REQUIRE(n_edges >= n_sites && n_edges <= INT_MAX, "foam_slot_table: n_edges must be in [N, 2^31)");
+    if (n_sites == 0) return VGR_OK;
+    VGR_REQUIRE(offsets && nbr && slots, "foam_slot_table: null pointer");
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(slots) % 16 == 0, "foam_slot_table: slots must be 16-byte aligned");
+    hipLaunchKernelGGL(vgr::slot_table_kernel, dim3(vgr::grid_for(n_sites, 256)), dim3(256), 0, vgr::as_stream(stream),
+                       offsets, nbr, n_sites, reinterpret_cast<int4*>(slots));
+    return vgr::launch_status("slot_table_kernel");
 }

@@ -13,6 +13,8 @@ RuntimeError; outputs are allocated here with torch on the input's device and th
 torch's current stream. density, color, conic, march and foam are autograd Functions whose backward runs the
 gradient kernels."""
 
+import os
+
 import torch
 
 from . import _lib
@@ -191,7 +193,8 @@ class _MarchExtension:
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 3) int32] (+ trace (B, trace_cap) when trace_cap > 0).
 		lanes: 1 ray per lane (1), 16 lanes per ray (16) or by batch size (0). work: optional uint8 device workspace
 		(at least vgr_march_work_size bytes); a training step passes the backward's, which then reuses its blocks.
-		order: optional int32 (B,) permutation, the order in which the rays are traced (ray_order); same results."""
+		order: optional int32 (B,) permutation of 0 .. B - 1, the order in which the rays are traced
+		(a ray it leaves out keeps uninitialised outputs; VGR_CHECK_ORDER=1 verifies it) (ray_order); same results."""
 		for t, n, dtp in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						  (adj, 'adj', torch.int32), (raw, 'raw', torch.float32), (dA, 'dA', torch.float32),
 						  (cA, 'cA', torch.float32), (sh, 'sh', torch.float32), (o, 'o', torch.float32),
@@ -264,14 +267,18 @@ class _MarchExtension:
 class _FoamInferExtension:
 	@staticmethod
 	def foam_infer(points, offsets, nbr, edge, attr, sh, sh_deg, o, d, start, near, far, t_thresh, w_thresh,
-				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None, order=None, indexed=None):
+				   color_cut, color_mode, stage, cap, orig, trace_cap=0, lanes=None, order=None, indexed=None,
+				   slots=None):
 		"""-> [rgb (B, 3), T (B,), depth (B,), stats (B, 5) int32] (+ trace (B, trace_cap) int32, the cell of
 		every sample in original numbering, -1 past the last sample, when trace_cap > 0). lanes: None for the
 		library's default layout, else 1 (one ray per lane) or 2 / 4 / 8 (that many lanes per ray,
-		vgr_foam_infer_lanes). order: optional int32 (B,) permutation, the order in which the rays are traced
+		vgr_foam_infer_lanes). order: optional int32 (B,) permutation of 0 .. B - 1, the order in which the rays are traced
+		(a ray it leaves out keeps uninitialised outputs; VGR_CHECK_ORDER=1 verifies it)
 		(ray_order); the results are the same. indexed: optional (edge_i, attr_i) from index_pack, read by the
 		fused rendering with one ray per lane in place of nbr / edge / attr (vgr_foam_infer_indexed, bit-identical
-		results); other stages, colour modes and layouts ignore it."""
+		results); other stages, colour modes and layouts ignore it. slots: optional int32 (N, 16) slot table
+		(slot_table) of the same pack: with color_cut = +inf the reference's colour-cache misses (stats[:, 4]) are
+		counted from it once per neighbourhood pass instead of per lookup (the same counts, faster)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
 						 (nbr, 'nbr', torch.int32), (edge, 'edge', torch.float32), (attr, 'attr', torch.float32),
 						 (o, 'o', torch.float32), (d, 'd', torch.float32), (start, 'start', torch.int32),
@@ -314,14 +321,17 @@ class _FoamInferExtension:
 			_check(attr_i, 'attr_i', torch.float32)
 			_require(edge_i.shape == edge.shape and attr_i.shape == attr.shape,
 					 'edge_i and attr_i must have the shapes of edge and attr')
+		if slots is not None:
+			_check(slots, 'slots', torch.int32)
+			_require(slots.dim() == 2 and slots.shape == (n, 16), 'slots must be (N, 16)')
 		with torch.cuda.device(dev):
 			if indexed is not None:
 				call('vgr_foam_infer_indexed', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(edge_i), ptr(attr_i),
-					 stream_of(dev))
-			elif lanes is not None or order is not None:
+					 ptr(slots), stream_of(dev))
+			elif lanes is not None or order is not None or slots is not None:
 				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
-					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), stream_of(dev))
+					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(slots), stream_of(dev))
 			elif trace is None:
 				call('vgr_foam_infer', *args, stream_of(dev))
 			else:
@@ -348,12 +358,36 @@ def index_pack(offsets, nbr, edge, attr):
 	return edge_i, attr_i
 
 
+def slot_table(offsets, nbr):
+	"""Slot table of a foam pack (vgr_foam_slot_table) -> int32 (N, 16): per site and slot s (site & 7) of its
+	self-first neighbourhood in CSR order, the first and the last entry at columns 2s, 2s + 1, -2 for an empty slot. foam_infer
+	counts the reference's per-ray colour-cache misses from it (foam_infer.cu:151-168). A snapshot of the pack."""
+	for t, name in ((offsets, 'offsets'), (nbr, 'nbr')):
+		_check(t, name, torch.int32)
+	n = offsets.numel() - 1
+	_require(n >= 0 and nbr.numel() >= n, 'offsets must be (N + 1) and nbr (E >= N)')
+	slots = torch.empty(n, 16, dtype=torch.int32, device=nbr.device)
+	with torch.cuda.device(nbr.device):
+		call('vgr_foam_slot_table', ptr(offsets), ptr(nbr), n, nbr.numel(), ptr(slots), stream_of(nbr.device))
+	return slots
+
+
+# Set VGR_CHECK_ORDER=1 to verify that every processing order is a permutation (a sort and a device sync per call).
+CHECK_ORDER = os.environ.get('VGR_CHECK_ORDER', '0') == '1'
+
+
 def _order(order, B, dev):
-	"""Checks an optional processing order (int32 CUDA tensor of B entries) -> the tensor or None."""
+	"""Checks an optional processing order (int32 CUDA tensor of B entries) -> the tensor or None. The order must be
+	a permutation of 0 .. B - 1: the kernels write the outputs of the rays it lists, so a ray left out keeps
+	uninitialised outputs and a ray listed twice is traced twice. Entries outside [0, B) are skipped by the kernels.
+	With VGR_CHECK_ORDER=1 the permutation is verified (RuntimeError otherwise)."""
 	if order is None:
 		return None
 	_check(order, 'order', torch.int32)
 	_require(order.numel() == B and order.device == dev, 'order must hold one entry per ray, on the rays\' device')
+	if CHECK_ORDER:
+		ok = bool(torch.equal(torch.sort(order.long())[0], torch.arange(B, device=dev)))
+		_require(ok, 'order must be a permutation of 0 .. B - 1')
 	return order
 
 
