@@ -196,6 +196,10 @@ def main():
 	ap.add_argument('--eps-color', type=float, default=0.0, help='skip colour terms of relative weight < eps')
 	ap.add_argument('--eps-density', type=float, default=0.0, help='skip density terms below eps')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
+	ap.add_argument('--no-rows', action='store_true',
+					help='group layouts read the 80-byte attr rows instead of the 64-byte site rows')
+	ap.add_argument('--no-slots', action='store_true',
+					help="no slot table: the reference's colour-cache misses counted with per-lookup tags in LDS")
 	ap.add_argument('--no-indexed', action='store_true',
 					help='fused colours: read the reference edge records (nbr + edge) instead of the indexed ones')
 	ap.add_argument('--tile', type=int, default=8, help='pixel tile edge (8: one 8x8 tile per wave64)')
@@ -283,17 +287,23 @@ def bench_foam(args):
 	lanes = args.lanes_per_ray or (8 if ordered else (4 if args.colors == 'exact' else 1))
 	# fused colours with one ray per lane read the indexed edge records (built once with the pack, untimed)
 	indexed = not args.no_indexed and mode == 2 and lanes == 1
-	if indexed:
-		render.index_pack(pack)  # also the slot table
-	elif args.colors != 'baked':  # the reference's colour-cache misses counted once per neighbourhood pass
+	# the derived records, built once with the pack (untimed): indexed edge records, the slot table of the reference's
+	# colour cache, the 64-byte site rows of the group layouts
+	if not args.no_indexed and args.colors != 'baked':
+		render.index_pack(pack)
+	elif args.colors != 'baked':
 		pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
+	if args.no_slots:
+		pack.pop('slots', None)
+	if args.no_rows or lanes == 1:
+		pack.pop('rows', None)
 
 	def launch(p, sel, m=mode, cut=color_cut):
 		order = ext.ray_order(o[sel], d[sel], dir_res, pos_bits) if ordered else None
 		return fi.foam_infer(p['points'], p['offsets'], p['nbr'], p['edge'], p['attr'], p['sh'], sc.sh_deg, o[sel],
 							 d[sel], start[sel], near[sel], far[sel], 1e-4, 1e-4, cut, m, 2, empty, p['orig'],
 							 lanes=lanes, order=order,
-							 indexed=(p['edge_i'], p['attr_i']) if 'edge_i' in p and m == 2 else None,
+							 indexed=(p['edge_i'], p['attr_i'], p.get('rows')) if 'edge_i' in p and m != 1 else None,
 							 slots=p.get('slots'))
 
 	if args.colors == 'baked':  # one launch per camera, each after baking that view's site colours
@@ -359,6 +369,8 @@ def bench_foam(args):
 		key += f'-sh{"16" if args.sh_half else "32"}-ec{args.eps_color:g}-ed{args.eps_density:g}'
 	if indexed:
 		key += '-idx'
+	if 'rows' in pack and lanes > 1:
+		key += '-rows64'
 	src = source_hash('foam_infer.hip')
 	log(f'kernel source hash (foam_infer.hip): {src}; workload key {key}')
 	roofline = hbm_roofline(ms, key, src, abytes,
@@ -390,13 +402,16 @@ def bench_foam(args):
 			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
 			'lanes_per_ray': lanes,
 			'edge_records': 'indexed (vgr_foam_infer_indexed)' if indexed else 'reference',
+			'site_rows': '64-byte rows' if 'rows' in pack and lanes > 1 else '80-byte attr rows',
+			'cache_misses': ('slot table, once per pass' if 'slots' in pack else 'per-lookup tags in LDS')
+			if args.colors != 'baked' else None,
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': (f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside '
 						  f'the timed step' if ordered else f'{args.tile}x{args.tile} tiles, {args.tile_curve} order'),
 			't_thresh': 1e-4, 'w_thresh': 1e-4,
 			'samples_per_ray': round(float(st[:, 0].mean()), 2),
 			'density_terms_per_ray': round(float(st[:, 3].mean()), 1),
-			'sh_evals_per_ray': round(float(st[:, 4].mean()), 1),
+			'sh_cache_misses_per_ray': round(float(st[:, 4].mean()), 1),
 			'distinct_blended_sites_per_ray': None if fast else round(u_sh, 1),
 			'distinct_sites_traced_rays': u_rays or None, 'quality': quality,
 			'mean_T': round(float(T.double().mean()), 4),

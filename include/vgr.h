@@ -351,8 +351,11 @@ int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float*
  * VGR_COLOR_FUSED) with one ray per lane (lanes_per_ray 0 or 1) reads edge_i and attr_i in place of nbr, edge and
  * attr, one record stream per neighbourhood entry instead of two. The outputs are bit-identical to
  * vgr_foam_infer_lanes on the same pack; every other stage, colour mode or layout runs vgr_foam_infer_lanes on the
- * reference records unchanged. slots as for vgr_foam_infer_lanes. No counterpart in the reference (same function as
- * vgr_foam_infer).
+ * reference records unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none) f32 (N, 16), 64-byte aligned:
+ * the first 16 columns of attr (density conic, min(raw, 30), the cut-off word or padding, colour conic), which the
+ * group layouts (lanes_per_ray 2, 4, 8) then read in place of the 80-byte attr rows: two whole rows per 128-byte
+ * line, where 3 in 8 attr rows straddle two lines (bit-identical results). No counterpart in the reference (same
+ * function as vgr_foam_infer).
  */
 int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                            const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
@@ -361,7 +364,7 @@ int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* 
                            int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
                            float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                            const int32_t* order, int64_t lanes_per_ray, const float* edge_i, const float* attr_i,
-                           const int32_t* slots, void* stream);
+                           const int32_t* slots, const float* rows, void* stream);
 
 /*
  * Slot table of a foam pack, for the `slots` argument of vgr_foam_infer_lanes and vgr_foam_infer_indexed. No

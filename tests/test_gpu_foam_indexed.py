@@ -160,3 +160,33 @@ def test_render_rays_with_indexed_pack(gpu, small):
 	with pytest.raises(RuntimeError, match='edge_i and attr_i'):
 		fi.foam_infer(*args, 3, o_, d_, pack['inv'][T(start).long()].int(), near, far, 1e-4, 1e-4, math.inf, 2, 2,
 					  e, pack['orig'], indexed=(pack['edge_i'][:-1], pack['attr_i']))
+
+
+@pytest.mark.parametrize('lanes', [2, 4, 8])
+def test_site_rows_identical_in_group_layouts(gpu, small, lanes):
+	"""The group layouts reading the 64-byte site rows (the first 16 record columns, rows of ext.foam_infer's indexed
+	argument) give every output bit-identical to the 80-byte attr rows: fused and exact colours, thresholds on and
+	off, renumbered or not, with the slot table and without."""
+	f, (o, d, start, near, _, far) = small
+	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=gpu)  # noqa: E731
+	empty = torch.empty(0, dtype=torch.int32, device=gpu)
+	for reorder in (False, True):
+		pk = f.pack(reorder=reorder)
+		st = pk['inv'][start].astype(np.int32) if reorder else start
+		tens = {k: t(pk[k]) for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh')}
+		ei, ai = ext.index_pack(tens['offsets'], tens['nbr'], tens['edge'], tens['attr'])
+		rows = ai[:, :16].contiguous()
+		slots = ext.slot_table(tens['offsets'], tens['nbr'])
+		orig = t(pk['orig']) if pk.get('orig') is not None and len(pk['orig']) else empty
+		for mode in (0, 2):
+			for tt, wt in ((1e-4, 1e-4), (0.0, -1.0)):
+				outs = []
+				for idx, sl in (((ei, ai), None), ((ei, ai, rows), None), ((ei, ai, rows), slots)):
+					out = ext.foam_infer_extension().foam_infer(
+						tens['points'], tens['offsets'], tens['nbr'], tens['edge'], tens['attr'], tens['sh'], 3, t(o),
+						t(d), t(st), t(near), t(far), tt, wt, math.inf, mode, 2, empty, orig, trace_cap=256,
+						lanes=lanes, indexed=idx, slots=sl)
+					torch.cuda.synchronize()
+					outs.append(dict(zip(FIELDS, [x.cpu().numpy() for x in out])))
+				assert_identical(outs[0], outs[1])
+				assert_identical(outs[0], outs[2])

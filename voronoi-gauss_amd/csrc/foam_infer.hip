@@ -36,6 +36,7 @@ struct FoamScene {
     const float4* __restrict__ sh;      // (N, 12) fp32 or (N, 6) fp16
     const int* __restrict__ orig;       // (N) or null
     const int4* __restrict__ slots;     // (N, 4) slot table (vgr_foam_slot_table) or null
+    const float4* __restrict__ rows;    // (N, 4) 64-byte site rows (the first 16 attr columns) or null
     int n_sites;
 };
 
@@ -383,12 +384,13 @@ __device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4
 
 // The ray's tags of the slots a lane keeps (all 8 with one ray per lane; g, g + G, ... in a group of G lanes), for
 // the slot-table accounting.
-// The tags stay in the lane's private (scratch) memory between passes: they are read and written once per pass, and
-// kept in registers they would push more of the neighbourhood loop's state out to scratch.
+// The tags live in registers (static slot indices). Measured on config 3 against keeping them in the lane's scratch
+// memory (read and written once per pass: 192.3 ms), in LDS (which takes colour-cache blocks: 201.5 ms) or packed
+// 20 bits per tag (181.2 ms): 180.0 ms, against 172.9 with no tag work.
 template <int G>
 struct SlotTags {
     static constexpr int n = kRayTagSlots / G;
-    volatile int t[n];
+    int t[n];
 };
 
 template <int G>
@@ -481,6 +483,22 @@ __device__ __forceinline__ void exit_candidate(const FoamScene& S, const float4&
 struct SiteRec {
     float4 q0, q1, q2, q3;
 };
+
+// The group layout's site records: the 64-byte rows when the caller gives them (one 128-byte line holds two whole
+// rows, where 3 of 8 of the 80-byte attr rows straddle two lines), else the attr rows.
+__device__ __forceinline__ const float4* group_row(const FoamScene& S, int k) {
+    return S.rows != nullptr ? S.rows + 4 * static_cast<int64_t>(k) : S.attr + 5 * static_cast<int64_t>(k);
+}
+
+template <int STAGE>
+__device__ __forceinline__ SiteRec group_site_rec(const FoamScene& S, int k) {
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    SiteRec r{zero4, zero4, zero4, zero4};
+    const float4* a = group_row(S, k);
+    if (STAGE >= 1) r.q0 = a[0], r.q1 = a[1];
+    if (STAGE >= 2) r.q2 = a[2], r.q3 = a[3];
+    return r;
+}
 
 template <int STAGE>
 __device__ __forceinline__ SiteRec site_rec(const FoamScene& S, int k) {
@@ -875,7 +893,7 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
     for (int e = e0 + g; e < e1; e += G) {
         const float4 ed = PREF ? edn : S.edge[e];
         const int k = PREF ? kn : S.nbr[e];
-        const SiteRec q = site_rec<STAGE>(S, k);
+        const SiteRec q = group_site_rec<STAGE>(S, k);
         if (want_exit && e > e0) {
             const float n0 = ed.x - pc.x, n1 = ed.y - pc.y, n2 = ed.z - pc.z;
             const float dn = n0 * d[0] + n1 * d[1] + n2 * d[2];
@@ -944,7 +962,7 @@ __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c,
     for (int e = e0 + g; e < e1; e += G) {
         const float4 ed = S.edge[e];
         const int k = S.nbr[e];
-        const float4* a = S.attr + 5 * static_cast<int64_t>(k);
+        const float4* a = group_row(S, k);
         const float4 q2 = a[2], q3 = a[3];
         float v0, v1, v2, r2;
         offset_of(x, ed, v0, v1, v2, r2);
@@ -1215,7 +1233,8 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                double t_thresh, double w_thresh, double color_cut, int64_t color_mode, int64_t stage,
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
                int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream,
-               const float* edge_i = nullptr, const float* attr_i = nullptr, const int32_t* slots = nullptr) {
+               const float* edge_i = nullptr, const float* attr_i = nullptr, const int32_t* slots = nullptr,
+               const float* rows = nullptr) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     // the indexed edge records serve the fused blend with one ray per lane (its default layout)
     const bool indexed = edge_i != nullptr && attr_i != nullptr && stage == 2 && color_mode == kFused &&
@@ -1247,6 +1266,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                       needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
                       orig,
                       reinterpret_cast<const int4*>(slots),
+                      indexed ? nullptr : reinterpret_cast<const float4*>(rows),
                       static_cast<int>(n_sites)};
     const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
                        static_cast<int>(sh_deg)};
@@ -1333,13 +1353,15 @@ extern "C" int vgr_foam_infer_indexed(const float* points, int64_t n_sites, cons
                                       int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
                                       float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                                       const int32_t* order, int64_t lanes_per_ray, const float* edge_i,
-                                      const float* attr_i, const int32_t* slots, void* stream) {
+                                      const float* attr_i, const int32_t* slots, const float* rows, void* stream) {
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_indexed: trace needs trace_cap > 0");
     VGR_REQUIRE(edge_i && attr_i, "foam_infer_indexed: edge_i and attr_i are required");
+    VGR_REQUIRE(rows == nullptr || reinterpret_cast<uintptr_t>(rows) % 64 == 0,
+                "foam_infer_indexed: rows must be 64-byte aligned");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
                            T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream,
-                           edge_i, attr_i, slots);
+                           edge_i, attr_i, slots, rows);
 }
 
 extern "C" int vgr_foam_slot_table(const int32_t* offsets, const int32_t* nbr, int64_t n_sites, int64_t n_edges,

@@ -276,7 +276,8 @@ class _FoamInferExtension:
 		(a ray it leaves out keeps uninitialised outputs; VGR_CHECK_ORDER=1 verifies it)
 		(ray_order); the results are the same. indexed: optional (edge_i, attr_i) from index_pack, read by the
 		fused rendering with one ray per lane in place of nbr / edge / attr (vgr_foam_infer_indexed, bit-identical
-		results); other stages, colour modes and layouts ignore it. slots: optional int32 (N, 16) slot table
+		results), or (edge_i, attr_i, rows) with the 64-byte site rows (N, 16) that the group layouts then read in
+		place of attr (bit-identical results); other stages, colour modes and layouts ignore them. slots: optional int32 (N, 16) slot table
 		(slot_table) of the same pack: with color_cut = +inf the reference's colour-cache misses (stats[:, 4]) are
 		counted from it once per neighbourhood pass instead of per lookup (the same counts, faster)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
@@ -315,12 +316,17 @@ class _FoamInferExtension:
 				None if baked else ptr(sh), int(half), int(sh_deg), ptr(o), ptr(d), ptr(start), ptr(near), ptr(far), B,
 				float(t_thresh), float(w_thresh), float(color_cut), int(color_mode), int(stage), ptr(cp), ptr(og),
 				ptr(rgb), ptr(T), ptr(depth), ptr(stats)]
+		rows = None
 		if indexed is not None:
-			edge_i, attr_i = indexed
+			edge_i, attr_i = indexed[0], indexed[1]
+			rows = indexed[2] if len(indexed) > 2 else None
 			_check(edge_i, 'edge_i', torch.float32)
 			_check(attr_i, 'attr_i', torch.float32)
 			_require(edge_i.shape == edge.shape and attr_i.shape == attr.shape,
 					 'edge_i and attr_i must have the shapes of edge and attr')
+			if rows is not None:
+				_check(rows, 'rows', torch.float32)
+				_require(rows.shape == (n, 16) and rows.data_ptr() % 64 == 0, 'rows must be (N, 16), 64-byte aligned')
 		if slots is not None:
 			_check(slots, 'slots', torch.int32)
 			_require(slots.dim() == 2 and slots.shape == (n, 16), 'slots must be (N, 16)')
@@ -328,7 +334,7 @@ class _FoamInferExtension:
 			if indexed is not None:
 				call('vgr_foam_infer_indexed', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(edge_i), ptr(attr_i),
-					 ptr(slots), stream_of(dev))
+					 ptr(slots), ptr(rows), stream_of(dev))
 			elif lanes is not None or order is not None or slots is not None:
 				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(slots), stream_of(dev))

@@ -319,9 +319,11 @@ def index_pack(pack):
 	"""Adds the indexed edge records (ext.index_pack: edge_i, attr_i) and the slot table of the reference's colour
 	cache (ext.slot_table: slots) to a GPU pack; render_rays_foam_infer then renders fused colours with one record
 	stream per neighbourhood entry, bit-identical to the reference records, and counts the cache misses of
-	stats[:, 4] once per neighbourhood pass. A snapshot: call again after changing the pack."""
+	stats[:, 4] once per neighbourhood pass; and the 64-byte site rows (rows: the first 16 columns of the records,
+	two whole rows per 128-byte line) that the group layouts read. A snapshot: call again after changing the pack."""
 	pack['edge_i'], pack['attr_i'] = ext.index_pack(pack['offsets'], pack['nbr'], pack['edge'], pack['attr'])
 	pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
+	pack['rows'] = pack['attr_i'][:, :16].contiguous()
 	return pack
 
 
@@ -363,7 +365,7 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 		o.float().contiguous(), d.float().contiguous(), start.int().contiguous(), t_near.contiguous(),
 		t_far.contiguous(), float(t_thresh), float(w_thresh), 2 * math.log(1 / eps_color) if eps_color > 0 else math.inf,
 		_COLOR_MODES[colors], int(stage), empty if cap is None else cap.int().contiguous(), pack['orig'],
-		trace_cap=trace_cap, indexed=(pack['edge_i'], pack['attr_i']) if 'edge_i' in pack else None,
+		trace_cap=trace_cap, indexed=(pack['edge_i'], pack['attr_i'], pack.get('rows')) if 'edge_i' in pack else None,
 		slots=pack.get('slots'))
 	fg, T, depth, stats = out[:4]
 	res = {'rgb': _with_background(model, fg, T), 'acc': 1.0 - T, 'depth': depth, 'stats': stats}
