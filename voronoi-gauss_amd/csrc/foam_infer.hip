@@ -1277,8 +1277,10 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
     if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
     // The slot table gives the reference's cache misses per pass when a pass looks up every entry: colour cut-off
-    // +inf (a pass with a finite cut-off skips entries, and keeps its tags in LDS per lookup).
-    const bool table = slots != nullptr && std::isinf(color_cut) && color_cut > 0;
+    // +inf (a pass with a finite cut-off skips entries, and keeps its tags in LDS per lookup). With 8 lanes per ray
+    // (incoherent batches, bound by DRAM) the table's reads cost more than the per-lookup tags, which need only
+    // 256 bytes of LDS per wave there: config 5's batch ran 2437.6 ms with the table, 2298.0 ms with the tags.
+    const bool table = slots != nullptr && std::isinf(color_cut) && color_cut > 0 && lanes != 8;
     if (indexed)
         return sh_half != 0 ? dispatch_indexed<true>(trace != nullptr, table, S, P, R, O, s)
                             : dispatch_indexed<false>(trace != nullptr, table, S, P, R, O, s);
