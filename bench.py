@@ -282,11 +282,17 @@ def bench_foam(args):
 
 	ordered = args.order == 'on' or (args.order == 'auto' and not sc.cameras)
 	dir_res, pos_bits = args.order_dir_res or 8, args.order_pos_bits or 7
-	# camera rays in 8x8 tiles: the library's default layout (one ray per lane; 4 lanes per ray for exact colours);
-	# an incoherent batch in coherence order: 8 lanes per ray, the fastest layout on config 5 for every colour mode
-	lanes = args.lanes_per_ray or (8 if ordered else (4 if args.colors == 'exact' else 1))
-	# fused colours with one ray per lane read the indexed edge records (built once with the pack, untimed)
-	indexed = not args.no_indexed and mode == 2 and lanes == 1
+	# exact colours with the colour cut-off +inf, the indexed records and the slot table run as the one-pass blend
+	# (one ray per lane); otherwise as two passes, 4 lanes per ray
+	blend_ok = not args.no_indexed and not args.no_slots and color_cut == math.inf
+	# camera rays in 8x8 tiles: the library's default layout (one ray per lane; 4 lanes per ray for exact colours
+	# in two passes); an incoherent batch in coherence order: 8 lanes per ray, the fastest layout on config 5 for
+	# every colour mode
+	lanes = args.lanes_per_ray or (8 if ordered else (4 if args.colors == 'exact' and not blend_ok else 1))
+	# fused colours (and exact colours by the blend) with one ray per lane read the indexed edge records (built once
+	# with the pack, untimed)
+	exact_blend = mode == 0 and lanes == 1 and blend_ok
+	indexed = not args.no_indexed and lanes == 1 and (mode == 2 or exact_blend)
 	# the derived records, built once with the pack (untimed): indexed edge records, the slot table of the reference's
 	# colour cache, the 64-byte site rows of the group layouts
 	if not args.no_indexed and args.colors != 'baked':
@@ -378,7 +384,7 @@ def bench_foam(args):
 							f'{80 if indexed else 84} B per neighbourhood edge + SH bytes per distinct blended site '
 							'(counts every L1/L2/LDS hit as a fetch, so it can exceed the HBM peak)',
 							'foam_infer_kernel' if lanes == 1 else 'foam_group_kernel')
-	if roofline['frac'] is not None and not fast and mode == 2 and lanes == 1:
+	if roofline['frac'] is not None and not fast and (mode == 2 or exact_blend) and lanes == 1:
 		roofline['limiter'] = ('not HBM: the texture data path is busy 94 % of the launch and the L2 serves 93 % of '
 							   'the gathers (profiles/foam_infer_config3_counters.md)')
 
@@ -402,6 +408,7 @@ def bench_foam(args):
 			'colors': args.colors, 'sh': 'f16' if args.sh_half else 'f32', 'sh_deg': sc.sh_deg,
 			'lanes_per_ray': lanes,
 			'edge_records': 'indexed (vgr_foam_infer_indexed)' if indexed else 'reference',
+			'exact_colours': (('one-pass blend' if exact_blend else 'two passes') if mode == 0 else None),
 			'site_rows': '64-byte rows' if 'rows' in pack and lanes > 1 else '80-byte attr rows',
 			'cache_misses': ('slot table, once per pass' if 'slots' in pack else 'per-lookup tags in LDS')
 			if args.colors != 'baked' else None,

@@ -350,8 +350,12 @@ int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float*
  * vgr_foam_infer_lanes with the indexed edge records of vgr_foam_index_pack: the full fused rendering (stage 2,
  * VGR_COLOR_FUSED) with one ray per lane (lanes_per_ray 0 or 1) reads edge_i and attr_i in place of nbr, edge and
  * attr, one record stream per neighbourhood entry instead of two. The outputs are bit-identical to
- * vgr_foam_infer_lanes on the same pack; every other stage, colour mode or layout runs vgr_foam_infer_lanes on the
- * reference records unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none) f32 (N, 16), 64-byte aligned:
+ * vgr_foam_infer_lanes on the same pack. Exact colours (VGR_COLOR_LAZY, stage 2) with one ray per lane, slots
+ * given and color_cut +inf run as that same fused blend: rgb, T, depth and stats[:, 0..3] bit-identical to
+ * VGR_COLOR_FUSED (rgb within rounding of the two-pass exact colour: the same normalised sum over every neighbour,
+ * kept relative to a running minimum), stats[:, 4] the exact mode's cache misses (its colour passes: segments of
+ * weight > w_thresh). Every other stage, colour mode or layout runs vgr_foam_infer_lanes on the reference records
+ * unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none) f32 (N, 16), 64-byte aligned:
  * the first 16 columns of attr (density conic, min(raw, 30), the cut-off word or padding, colour conic), which the
  * group layouts (lanes_per_ray 2, 4, 8) then read in place of the 80-byte attr rows: two whole rows per 128-byte
  * line, where 3 in 8 attr rows straddle two lines (bit-identical results). No counterpart in the reference (same

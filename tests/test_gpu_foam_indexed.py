@@ -1,7 +1,8 @@
 """GPU tests of the indexed edge records (vgr_foam_index_pack, vgr_foam_infer_indexed): the records' layout, and
 the fused rendering through them bit-identical to vgr_foam_infer_lanes with one ray per lane on the reference
-records (rgb, T, depth, statistics, traces), which the oracle pins in turn; every other stage, colour mode and ray
-layout falls back to the reference records unchanged."""
+records (rgb, T, depth, statistics, traces), which the oracle pins in turn; exact colours through them as the
+one-pass blend (with the slot table and the colour cut-off +inf); every other stage, colour mode and ray layout
+falls back to the reference records unchanged."""
 
 import math
 
@@ -108,9 +109,54 @@ def test_indexed_cap_bad_starts_and_default_layout(gpu, small):
 	assert (b['T'][:4] == 1).all() and (b['rgb'][:4] == 0).all() and (b['stats'][:4] == 0).all()
 
 
+@pytest.mark.parametrize('sh_deg', [0, 3])
+@pytest.mark.parametrize('sh_half', [False, True])
+def test_exact_colours_by_the_blend(gpu, small, sh_deg, sh_half):
+	"""Exact colours with the indexed records, the slot table and the colour cut-off +inf run as the one-pass blend
+	(one ray per lane): rgb, T, depth, traces and the first four statistics bit-identical to the fused mode through
+	the same records; stats[:, 4] the exact mode's cache misses, every statistic of every ray equal to the two-pass
+	kernel's (reference records, same table) with the thresholds off, and rgb within 1e-5 of it; against the oracle
+	in exact mode (its cache on) within the parity bar."""
+	f, (o, d, start, near, _, far) = small
+	for reorder in (False, True):
+		pk = f.pack(sh_half=sh_half, reorder=reorder)
+		st = pk['inv'][start].astype(np.int32) if reorder else start
+		for tt, wt in ((1e-4, 1e-4), (0.0, -1.0)):
+			kw = dict(t_thresh=tt, w_thresh=wt, trace_cap=512)
+			for lanes in (1, None):
+				blend = run(gpu, pk, sh_deg, o, d, st, near, far, color_mode=0, lanes=lanes, indexed=True, slots=True,
+							**kw)
+				fused = run(gpu, pk, sh_deg, o, d, st, near, far, color_mode=2, lanes=lanes, indexed=True, slots=True,
+							**kw)
+				for k in ('rgb', 'T', 'depth', 'trace'):
+					np.testing.assert_array_equal(blend[k].view(np.int32), fused[k].view(np.int32), err_msg=k)
+				np.testing.assert_array_equal(blend['stats'][:, :4], fused['stats'][:, :4])
+			two = run(gpu, pk, sh_deg, o, d, st, near, far, color_mode=0, lanes=1, slots=True, **kw)
+			np.testing.assert_allclose(blend['rgb'], two['rgb'], atol=1e-5, rtol=0)
+			np.testing.assert_array_equal(blend['T'].view(np.int32), two['T'].view(np.int32))
+			if tt == 0.0:
+				np.testing.assert_array_equal(blend['stats'], two['stats'])
+				np.testing.assert_array_equal(blend['trace'], two['trace'])
+			if not sh_half:
+				r = ref_foam(pk, sh_deg, o, d, st, near, far, tt, wt, color_mode=0, trace_cap=512)
+				compare(blend, r, exact_trace=tt == 0.0, stats_frac=1.0 if tt == 0.0 else 0.98)
+
+
+def test_exact_colours_blend_falls_back(gpu, small):
+	"""Exact colours run as two passes without the slot table, with a finite colour cut-off, or with a group of lanes
+	per ray, indexed records given or not: the same outputs either way."""
+	f, (o, d, start, near, _, far) = small
+	pk = f.pack()
+	for kw in (dict(slots=False), dict(slots=True, color_cut=2 * math.log(1e3)), dict(slots=True, lanes=4),
+			   dict(slots=True, lanes=2)):
+		a = run(gpu, pk, 3, o, d, start, near, far, color_mode=0, trace_cap=128, **kw)
+		b = run(gpu, pk, 3, o, d, start, near, far, color_mode=0, trace_cap=128, indexed=True, **kw)
+		assert_identical(a, b)
+
+
 def test_indexed_falls_back_outside_fused_one_lane(gpu, small):
-	"""Exact and baked colours, stages 0 and 1, and groups of lanes per ray ignore the indexed records: the same
-	outputs as without them."""
+	"""Exact colours without the slot table, baked colours, stages 0 and 1, and groups of lanes per ray ignore the
+	indexed records: the same outputs as without them."""
 	f, (o, d, start, near, _, far) = small
 	pk = f.pack()
 	pk['attr'][:, 16:19] = 0.25

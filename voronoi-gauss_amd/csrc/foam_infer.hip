@@ -668,9 +668,18 @@ __device__ __forceinline__ void trace_cell(const FoamScene& S, const FoamOut& O,
 // spills: 80 VGPRs, the rest of the ray's state (accumulated colour and depth, the basis) stored to scratch once
 // per sample, outside the neighbourhood loop; at 4 waves it needs no spills and ran 27 % slower, at 7 it spills
 // inside the loop.
-template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, bool TABLE>
+//
+// EXACT (fused colour modes, colour cut-off +inf, slot table): the exact (lazy) colour mode run by the one-pass blend.
+// The exact colour of a sample is sum_k exp(-(m_k - m_min) / 2) c_k / sum_k exp(-(m_k - m_min) / 2) over every
+// neighbour (the cut-off is +inf); the blend keeps the same two sums relative to the running minimum, rescaled as
+// it falls, so the colours agree to rounding. The statistics are the exact mode's: a colour pass counts only where
+// the exact mode runs one (segments with weight > w_thresh, for the segment's far sample and, when the segment
+// before was not coloured, its near sample), with that pass's lookups (every entry, as the blend's pass looks up)
+// and the ray's cache tags advanced by those passes alone.
+template <int STAGE, int COLOR, bool HALF, int DEG, bool TRACE, bool TABLE, bool EXACT = false>
 __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE >= 2 && COLOR != kBaked)))
     foam_infer_kernel(FoamScene S, FoamParams P, FoamRays R, FoamOut O) {
+    static_assert(!EXACT || (TABLE && STAGE == 2 && (COLOR == kFused || COLOR == kFusedIdx)), "exact via the blend");
     constexpr bool kSH = STAGE >= 2 && COLOR != kBaked;
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
     constexpr bool FUSED_SH = BLEND && COLOR != kBaked;
@@ -704,8 +713,11 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
     int c = walk_to<COLOR == kFusedIdx>(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2],
                                         walk_steps);
     CellEval E;
-    eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, c, t_near, o, d, b, cache, true, E, n_dens, n_sh);
-    if (TABLE && FUSED_SH) n_sh -= table_hits<1>(S, c, 0, tags);
+    int looks = 0, looksP = 0;  // EXACT: lookups of the latest pass and of the one before
+    bool litP = false;          // EXACT: the segment ending at the near sample was coloured
+    eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, c, t_near, o, d, b, cache, true, E, n_dens,
+                                              EXACT ? looks : n_sh);
+    if (TABLE && FUSED_SH && !EXACT) n_sh -= table_hits<1>(S, c, 0, tags);
     trace_cell<TRACE>(S, O, r, 0, c);
     float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
     bool hasP = false;
@@ -720,8 +732,10 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
         const bool last = E.next == INT_MAX || E.t_exit >= t_far || n_samples + 1 >= max_samples;
         const float tQ = last ? t_far : fmaxf(E.t_exit, tP);
         const int cQ = last ? c : E.next;
-        eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens, n_sh);
-        if (TABLE && FUSED_SH) n_sh -= table_hits<1>(S, cQ, 0, tags);
+        looksP = looks, looks = 0;
+        eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens,
+                                                  EXACT ? looks : n_sh);
+        if (TABLE && FUSED_SH && !EXACT) n_sh -= table_hits<1>(S, cQ, 0, tags);
         trace_cell<TRACE>(S, O, r, n_samples, cQ);
         ++n_samples;
         const float sQ = E.sigma, mQ = E.mmin;
@@ -734,7 +748,12 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
             const float inv = 1.f / E.B.a;
             CQ[0] = E.B.r * inv, CQ[1] = E.B.g * inv, CQ[2] = E.B.b * inv, hasQ = true;
         }
-        if (STAGE >= 2 && w > P.w_thresh) {
+        const bool lit = STAGE >= 2 && w > P.w_thresh;
+        if (lit) {
+            if constexpr (EXACT) {
+                if (!litP) n_sh += looksP - table_hits<1>(S, cP, 0, tags);
+                n_sh += looks - table_hits<1>(S, cQ, 0, tags);
+            }
             if constexpr (!BLEND) {
                 if (!hasP) {
                     color_lazy<HALF, DEG, TABLE>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
@@ -750,7 +769,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
             ++n_color;
         }
         T *= 1.f - alpha;
-        tP = tQ, sP = sQ, mP = mQ, hasP = hasQ, cP = cQ, c = cQ;
+        tP = tQ, sP = sQ, mP = mQ, hasP = hasQ, cP = cQ, c = cQ, litP = lit;
 #pragma unroll
         for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
         if (last || T < P.t_thresh) break;
@@ -1110,15 +1129,15 @@ __global__ void __launch_bounds__(256) index_pack_kernel(const int* __restrict__
     }
 }
 
-// The fused blend over the indexed edge records: one ray per lane.
-template <bool HALF, bool TRACE, bool TABLE>
+// The fused blend over the indexed edge records: one ray per lane (EXACT: the exact colour mode's statistics).
+template <bool HALF, bool TRACE, bool TABLE, bool EXACT>
 int launch_indexed(const FoamScene& S, const FoamParams& P, const FoamRays& R, const FoamOut& O, hipStream_t stream) {
     const dim3 grid(grid_for(R.n, kBlock)), block(kBlock);
     switch (P.sh_deg) {
-        case 0: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 0, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
-        case 1: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 1, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
-        case 2: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 2, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O); break;
-        default: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 3, TRACE, TABLE>), grid, block, 0, stream, S, P, R, O);
+        case 0: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 0, TRACE, TABLE, EXACT>), grid, block, 0, stream, S, P, R, O); break;
+        case 1: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 1, TRACE, TABLE, EXACT>), grid, block, 0, stream, S, P, R, O); break;
+        case 2: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 2, TRACE, TABLE, EXACT>), grid, block, 0, stream, S, P, R, O); break;
+        default: hipLaunchKernelGGL((foam_infer_kernel<2, kFusedIdx, HALF, 3, TRACE, TABLE, EXACT>), grid, block, 0, stream, S, P, R, O);
     }
     return launch_status("foam_infer_kernel (indexed edges)");
 }
@@ -1182,10 +1201,16 @@ int dispatch(int stage, int color_mode, bool half, const FoamScene& S, const Foa
 }
 
 template <bool HALF>
-int dispatch_indexed(bool trace, bool table, const FoamScene& S, const FoamParams& P, const FoamRays& R,
+int dispatch_indexed(bool trace, bool table, bool exact, const FoamScene& S, const FoamParams& P, const FoamRays& R,
                      const FoamOut& O, hipStream_t s) {
-    if (trace) return table ? launch_indexed<HALF, true, true>(S, P, R, O, s) : launch_indexed<HALF, true, false>(S, P, R, O, s);
-    return table ? launch_indexed<HALF, false, true>(S, P, R, O, s) : launch_indexed<HALF, false, false>(S, P, R, O, s);
+    if (exact)  // always with the slot table
+        return trace ? launch_indexed<HALF, true, true, true>(S, P, R, O, s)
+                     : launch_indexed<HALF, false, true, true>(S, P, R, O, s);
+    if (trace)
+        return table ? launch_indexed<HALF, true, true, false>(S, P, R, O, s)
+                     : launch_indexed<HALF, true, false, false>(S, P, R, O, s);
+    return table ? launch_indexed<HALF, false, true, false>(S, P, R, O, s)
+                 : launch_indexed<HALF, false, false, false>(S, P, R, O, s);
 }
 
 // Slot table of the reference's per-ray colour cache: for site k, the first and the last entry of every slot
@@ -1236,9 +1261,13 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                const float* edge_i = nullptr, const float* attr_i = nullptr, const int32_t* slots = nullptr,
                const float* rows = nullptr) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
-    // the indexed edge records serve the fused blend with one ray per lane (its default layout)
-    const bool indexed = edge_i != nullptr && attr_i != nullptr && stage == 2 && color_mode == kFused &&
-                         (lanes == kDefaultLanes || lanes == 1);
+    // The indexed edge records serve the fused blend with one ray per lane (its default layout), and with the slot
+    // table and the colour cut-off +inf the exact colours too, run by that blend (foam_infer_kernel, EXACT).
+    const bool one_lane = lanes == kDefaultLanes || lanes == 1;
+    const bool exact_blend = edge_i != nullptr && attr_i != nullptr && slots != nullptr && stage == 2 &&
+                             color_mode == kLazy && one_lane && std::isinf(color_cut) && color_cut > 0;
+    const bool indexed = exact_blend || (edge_i != nullptr && attr_i != nullptr && stage == 2 &&
+                                         color_mode == kFused && one_lane);
     if (indexed) lanes = 1;
     if (lanes == kDefaultLanes) lanes = default_lanes(stage, color_mode);
     VGR_REQUIRE(lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8,
@@ -1282,8 +1311,8 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     // 256 bytes of LDS per wave there: config 5's batch ran 2437.6 ms with the table, 2298.0 ms with the tags.
     const bool table = slots != nullptr && std::isinf(color_cut) && color_cut > 0 && lanes != 8;
     if (indexed)
-        return sh_half != 0 ? dispatch_indexed<true>(trace != nullptr, table, S, P, R, O, s)
-                            : dispatch_indexed<false>(trace != nullptr, table, S, P, R, O, s);
+        return sh_half != 0 ? dispatch_indexed<true>(trace != nullptr, table, exact_blend, S, P, R, O, s)
+                            : dispatch_indexed<false>(trace != nullptr, table, exact_blend, S, P, R, O, s);
     if (trace != nullptr)
         return dispatch<true>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), table, s);
     return dispatch<false>(int(stage), int(color_mode), sh_half != 0, S, P, R, O, int(lanes), table, s);

@@ -355,7 +355,8 @@ def render_rays_foam_infer(model, pack, o, d, start, near=0.02, far_radius=4.0, 
 	weight below it. start: sites in the model's numbering. -> dict rgb (with the background), acc, depth, stats
 	(B, 5): samples, coloured segments, walk steps, density terms, SH evaluations; with trace_cap > 0 also trace
 	(B, trace_cap), each sample's cell in the model's numbering. A pack with indexed records (index_pack) renders
-	fused colours through them."""
+	fused colours through them, and exact colours with eps_color = 0 too, as the one-pass blend (the same normalised
+	sum over the neighbours, kept relative to a running minimum; the statistics are the exact mode's)."""
 	t_near, _, t_far = ray_bounds(o, d, near, far_radius)
 	if pack['inv'] is not None:
 		start = pack['inv'][start.long()]
