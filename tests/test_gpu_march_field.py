@@ -131,6 +131,33 @@ def test_density_color_conic_vs_oracle(gpu):
 	assert empty.shape == (0,)
 
 
+def test_color_wide_batches(gpu):
+	"""color_forward runs 4 lanes per sample below 2^22 samples and one lane per sample from there: a batch of
+	1100 distinct samples repeated past 2^22 gives every copy the same colours (within 1e-6 of the small batch, whose
+	lanes add their partial sums in another order) and the oracle's within 1e-5, with records and without."""
+	f = Field(seed=6, n=300, lo=-1.0, hi=1.0, raw_mu=0.0, ls_mu=-1.2)
+	rng = np.random.default_rng(10)
+	n0 = 1100
+	x = rng.uniform(-1, 1, (n0, 3)).astype(np.float32)
+	site = f.tree.query(x)[1].astype(np.int32)
+	dirs = rng.normal(size=(n0, 3)).astype(np.float32)
+	reps = (1 << 22) // n0 + 1
+	e = ext.extension()
+	args = [T(a, gpu) for a in (f.points, f.offsets, f.adj)]
+	for deg in (0, 3):
+		r = oracle.color(f.points, f.offsets, f.adj, f.c_log_scale, f.c_quat, f.sh, deg, x, dirs, site)
+		for rec in (True, False):
+			call = lambda xs, ds, ss: e.color_forward(*args, T(f.c_log_scale, gpu), T(f.c_quat, gpu), T(f.sh, gpu),  # noqa: E731
+													   deg, xs, ds, ss, records=rec)
+			small = call(T(x, gpu), T(dirs, gpu), T(site, gpu)).cpu().numpy()
+			big = call(T(x, gpu).repeat(reps, 1), T(dirs, gpu).repeat(reps, 1), T(site, gpu).repeat(reps))
+			big = big.view(reps, n0, 3).cpu().numpy()
+			assert big.shape[0] * n0 >= 1 << 22
+			np.testing.assert_array_equal(big, np.broadcast_to(big[0], big.shape))
+			np.testing.assert_allclose(big[0], small, atol=1e-6, rtol=0)
+			np.testing.assert_allclose(big[0], r, atol=1e-5)
+
+
 def test_density_color_records_bit_identical(gpu):
 	"""density_forward / color_forward with per-site Gaussian records (a call of m >= N / 8 samples given scratch)
 	and without (no scratch, or a call too small for them) give the same bits."""

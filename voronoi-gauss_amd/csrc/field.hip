@@ -260,8 +260,11 @@ __global__ void __launch_bounds__(kBlock)
     sigma[t] = s;
 }
 
-// ------------------------------------------------------------------ colour: 4 lanes per sample
-constexpr int kColourLanes = 4;
+// ------------------------------------------------------------------ colour: 1 or 4 lanes per sample
+// Lanes per sample by batch size: below kColourWide samples a lane per sample would leave the GPU's 256 CUs short of
+// waves, so 4 lanes share a sample's neighbourhood; above it one lane per sample skips the group merges.
+constexpr int64_t kColourWide = int64_t(1) << 22;
+__host__ __device__ constexpr int colour_lanes(int64_t m) { return m >= kColourWide ? 1 : 4; }
 
 // Partial online softmax of a lane's share of the neighbourhood: running minimum m of the Mahalanobis distances, and
 // sum a of exp(-(m_k - m) / 2) and of those weights times the clamped colours.
@@ -314,17 +317,19 @@ __device__ __forceinline__ void sh_colour(const float4* __restrict__ row, const 
 
 // Colour at sample t: the normalised blend of max(SH_k(d) + 1/2, 0) over k in {i} U adj(i) with weights
 // exp(-(m_k - m_min) / 2). REC: m_k from the per-site records (gauss_pack_kernel), else from (log_scale, quat).
-template <int DEG, bool REC>
+// L lanes per sample (1 or 4): lane l takes positions l, l + L, ... of the neighbourhood.
+template <int DEG, bool REC, int L>
 __global__ void __launch_bounds__(kBlock)
     colour_group_kernel(Graph g, Gauss H, const float4* __restrict__ rec, const float4* __restrict__ sh,
                         const float* __restrict__ x, const float* __restrict__ dirs, const int* __restrict__ site,
                         int64_t m, float* __restrict__ rgb) {
-    const int lane = static_cast<int>(threadIdx.x) % kColourLanes;
-    const int64_t t = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) / kColourLanes;
+    static_assert(L == 1 || L == 4, "lanes per sample");
+    const int lane = static_cast<int>(threadIdx.x) % L;
+    const int64_t t = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) / L;
     if (t >= m) return;  // whole groups leave together
     const int i = site[t];
     if (i < 0 || i >= g.n_sites) {
-        if (lane < 3) rgb[3 * t + lane] = 0.f;
+        for (int c = lane; c < 3; c += L) rgb[3 * t + c] = 0.f;
         return;
     }
     const float px = x[3 * t], py = x[3 * t + 1], pz = x[3 * t + 2];
@@ -335,7 +340,7 @@ __global__ void __launch_bounds__(kBlock)
     sh_basis(u[0], u[1], u[2], DEG, b);
     Softmax P{kInf, 0.f, 0.f, 0.f, 0.f};
     const int e0 = g.offsets[i], e1 = g.offsets[i + 1];
-    for (int e = e0 - 1 + lane; e < e1; e += kColourLanes) {  // position e0 - 1 stands for the site itself
+    for (int e = e0 - 1 + lane; e < e1; e += L) {  // position e0 - 1 stands for the site itself
         const int k = e < e0 ? i : g.adj[e];
         float mk;
         if constexpr (REC) {
@@ -348,12 +353,11 @@ __global__ void __launch_bounds__(kBlock)
         sh_colour<DEG>(sh + 12 * static_cast<int64_t>(k), b, c);
         softmax_add(P, mk, c);
     }
-    softmax_merge<kXor1>(P);
-    softmax_merge<kXor2>(P);
-    if (lane < 3) {
-        const float num = lane == 0 ? P.r : (lane == 1 ? P.g : P.b);
-        rgb[3 * t + lane] = num / P.a;
+    if constexpr (L == 4) {
+        softmax_merge<kXor1>(P);
+        softmax_merge<kXor2>(P);
     }
+    for (int c = lane; c < 3; c += L) rgb[3 * t + c] = (c == 0 ? P.r : (c == 1 ? P.g : P.b)) / P.a;
 }
 
 __global__ void __launch_bounds__(kBlock)
@@ -382,15 +386,25 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
-template <int DEG>
-void launch_colour(bool rec, dim3 grid, hipStream_t st, const Graph& g, const Gauss& H, const float4* R,
-                   const float4* sh, const float* x, const float* dirs, const int* site, int64_t m, float* rgb) {
+template <int DEG, int L>
+void launch_colour_l(bool rec, hipStream_t st, const Graph& g, const Gauss& H, const float4* R, const float4* sh,
+                     const float* x, const float* dirs, const int* site, int64_t m, float* rgb) {
+    const dim3 grid(grid_for(m * L, kBlock));
     if (rec)
-        hipLaunchKernelGGL((colour_group_kernel<DEG, true>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site, m,
-                           rgb);
+        hipLaunchKernelGGL((colour_group_kernel<DEG, true, L>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site,
+                           m, rgb);
     else
-        hipLaunchKernelGGL((colour_group_kernel<DEG, false>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site, m,
-                           rgb);
+        hipLaunchKernelGGL((colour_group_kernel<DEG, false, L>), grid, dim3(kBlock), 0, st, g, H, R, sh, x, dirs, site,
+                           m, rgb);
+}
+
+template <int DEG>
+void launch_colour(bool rec, hipStream_t st, const Graph& g, const Gauss& H, const float4* R, const float4* sh,
+                   const float* x, const float* dirs, const int* site, int64_t m, float* rgb) {
+    if (colour_lanes(m) == 1)
+        launch_colour_l<DEG, 1>(rec, st, g, H, R, sh, x, dirs, site, m, rgb);
+    else
+        launch_colour_l<DEG, 4>(rec, st, g, H, R, sh, x, dirs, site, m, rgb);
 }
 
 // The records pay for themselves once a call has about N / 8 samples (their build reads and writes each site once;
@@ -469,7 +483,7 @@ extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int
     const Graph g{points, offsets, adj, int(n_sites)};
     const Gauss H{log_scale, reinterpret_cast<const float4*>(quat)};
     const float4* s4 = reinterpret_cast<const float4*>(sh);
-    const dim3 grid(grid_for(m * kColourLanes, kBlock)), block(kBlock);
+    const dim3 block(kBlock);
     const hipStream_t st = as_stream(stream);
     const bool rec = use_records(work, work_bytes, n_sites, m);
     const float4* R = static_cast<const float4*>(work);
@@ -477,10 +491,10 @@ extern "C" int vgr_color_forward(const float* points, int64_t n_sites, const int
         hipLaunchKernelGGL(gauss_pack_kernel, dim3(grid_for(n_sites, kBlock)), block, 0, st, g, H, nullptr, 1.f,
                            static_cast<float4*>(work));
     switch (sh_deg) {
-        case 0: launch_colour<0>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
-        case 1: launch_colour<1>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
-        case 2: launch_colour<2>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
-        default: launch_colour<3>(rec, grid, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        case 0: launch_colour<0>(rec, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        case 1: launch_colour<1>(rec, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        case 2: launch_colour<2>(rec, st, g, H, R, s4, x, dirs, site, m, rgb); break;
+        default: launch_colour<3>(rec, st, g, H, R, s4, x, dirs, site, m, rgb); break;
     }
     return launch_status("colour_group_kernel");
 }

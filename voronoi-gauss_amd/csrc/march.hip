@@ -127,22 +127,22 @@ __device__ __forceinline__ float color_m(const float4& c0, const float4& c1, con
     return maha(c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, v[0], v[1], v[2]);
 }
 
-// 1/2 + sum_{j < (deg+1)^2} b_j sh_kj per channel, reading only the float4 that hold those coefficients, kShChunk
+// 1/2 + sum_{j < (deg+1)^2} b_j sh_kj per channel, reading only the float4 that hold those coefficients, CHUNK
 // float4 at a time (the scheduling barrier keeps the next chunk's loads from being hoisted, which bounds the
-// registers the loads occupy).
+// registers the loads occupy; CHUNK = NV requests the whole row at once).
 constexpr int kShChunk = 4;
 
-template <int NV>
+template <int NV, int CHUNK = kShChunk>
 __device__ __forceinline__ void sh_eval_n(const float4* __restrict__ s, const float (&b)[16], int nb, float (&c)[3]) {
     c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
-    for (int q0 = 0; q0 < NV; q0 += kShChunk) {
-        float4 f[kShChunk];
+    for (int q0 = 0; q0 < NV; q0 += CHUNK) {
+        float4 f[CHUNK];
 #pragma unroll
-        for (int q = 0; q < kShChunk; ++q)
+        for (int q = 0; q < CHUNK; ++q)
             if (q0 + q < NV) f[q] = s[q0 + q];
 #pragma unroll
-        for (int q = 0; q < kShChunk; ++q) {
+        for (int q = 0; q < CHUNK; ++q) {
             if (q0 + q < NV) {
                 const float fv[4] = {f[q].x, f[q].y, f[q].z, f[q].w};
 #pragma unroll
@@ -152,7 +152,7 @@ __device__ __forceinline__ void sh_eval_n(const float4* __restrict__ s, const fl
                 }
             }
         }
-        if (q0 + kShChunk < NV) __builtin_amdgcn_sched_barrier(0);
+        if (q0 + CHUNK < NV) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -170,13 +170,14 @@ __device__ __forceinline__ void sample_at(float near, float mid, float far, int 
     }
 }
 
-// Samples are resolved kBatch at a time: one pass over the neighbourhood {i} U adj(i) of site i evaluates, for
-// each of the next kBatch sample points x_j, the lexicographic argmin of (|x_j - p_k|^2, k) (the greedy walk's
-// test), the density sum and the smallest colour Mahalanobis distance. Sample j + 1's walk starts at sample j's
-// site, so every leading sample at which i wins is resolved by this one pass exactly as by a pass of its own (same
-// neighbours, same order, same roundings); the first sample at which i loses walks on from its argmin, and the
-// pass at the next site covers it and the samples after it. Each quantity accumulates over the neighbours in the
-// same order as the reference's separate passes.
+// Samples are resolved several at a time: one pass over the neighbourhood {i} U adj(i) of site i evaluates, for
+// each of the next sample points x_j, the lexicographic argmin of (|x_j - p_k|^2, k) (the greedy walk's test), the
+// density sum and the colour terms. Sample j + 1's walk starts at sample j's site, so every leading sample at which i
+// wins is resolved by this one pass exactly as by a pass of its own (same neighbours, same order, same roundings);
+// the first sample at which i loses walks on from its argmin, and the pass at the next site covers it and the
+// samples after it. Each quantity accumulates over the neighbours in the same order as the reference's separate
+// passes. The backward's pass (cell_pass, kBatch samples) takes the smallest colour Mahalanobis distance of each
+// sample, for a colour pass of its own; the forward's (fwd_pass below) blends the colours in the same pass.
 constexpr int kBatch = 6;
 
 struct CellPass {
@@ -221,99 +222,119 @@ __device__ void cell_pass(const MarchField& F, int i, const float (&o)[3], const
     for (int j = 0; j < kBatch; ++j) R.best[j] = bk[j], R.sigma[j] = s[j], R.mmin[j] = mm[j];
 }
 
-// Coloured samples of one neighbourhood pass (all in one cell), blended together by one colour pass, so each
-// neighbour's colour max(SH_k(d) + 1/2, 0), which depends only on the site and the ray direction, is evaluated once
-// for all of them.
-constexpr int kPend = kBatch;
+// The forward's pass: kFwd samples, their walk tests and densities as in cell_pass, and each sample's colour blend
+// in the same pass, so that a neighbour's block (its record line and SH line) is read once per cell visit, where a
+// separate colour pass would fetch the record line again (3 random lines per neighbour of a coloured visit, now 2).
+// Each sample keeps a running blend relative to its smallest colour Mahalanobis distance so far, m: the sums of
+// exp(-(m_k - m) / 2) and of those weights times the colours max(SH_k(d) + 1/2, 0), both rescaled by
+// exp(-(m_old - m_new) / 2) when m falls, which after the pass is the normalised blend with weights
+// exp(-(m_k - m_min) / 2) up to rounding. Samples past the first that walks on are blended for nothing; the next pass
+// redoes them.
+//
+// Registers: the blend sums of the samples (a float4 each) and the ray's SH basis live in the wave's LDS, one float4
+// per lane per row (consecutive lanes, consecutive 16 bytes: no bank conflicts); a neighbour's 12 SH float4 are
+// requested with its record, one round trip per neighbour. kFwd = 8 at 3 waves per SIMD.
+constexpr int kFwd = 8;
+constexpr int kFwdWaves = 3;
+constexpr int kFwdLds = 4 + kFwd;  // float4 rows per lane: the basis (4), then the samples' sums
 
-struct Pending {
-    float t[kPend], w[kPend], mmin[kPend];
-    int n, cell;
+struct FwdPass {
+    int best[kFwd];
+    float sigma[kFwd];
+    float4 blend[kFwd];  // (sum a, sum a r, sum a g, sum a b)
 };
 
-// Blends the pending samples' colours (per sample: weights exp(-(m_k - m_min) / 2) over the neighbours in order,
-// then the normalised sum) and adds w C and w t of each, in sample order, to the ray's colour and depth.
-template <int NV>
-__device__ void flush(const MarchField& F, const float (&o)[3], const float (&d)[3], Pending& P, float (&acc)[3],
-                      float& dep) {
-    if (P.n == 0) return;
-    const int i = P.cell;
+// lds: this lane's first row; row q at lds[kBlock q].
+template <int BLK, int NV>
+__device__ void fwd_pass(const MarchField& F, int i, const float (&o)[3], const float (&d)[3],
+                         const float (&t)[kFwd], float4* lds, FwdPass& R) {
     const int e0 = F.offsets[i], n = F.offsets[i + 1] - e0 + 1;
     const int nb = (F.sh_deg + 1) * (F.sh_deg + 1);
-    float b[16];
-    sh_basis(d[0], d[1], d[2], F.sh_deg, b);
-    float A[kPend], cr[kPend], cg[kPend], cb[kPend];
+    float4* sums = lds + 4 * kBlock;
+    float bd[kFwd], s[kFwd], mm[kFwd];
+    int bk[kFwd];
 #pragma unroll
-    for (int s = 0; s < kPend; ++s) A[s] = cr[s] = cg[s] = cb[s] = 0.f;
+    for (int j = 0; j < kFwd; ++j) {
+        bd[j] = kInf, s[j] = 0.f, mm[j] = kInf, bk[j] = INT_MAX;
+        sums[kBlock * j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     int k = i;
     int kn = neighbor(F, i, e0, min(1, n - 1));
     for (int e = 0; e < n; ++e) {
-        const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));
-        const float4* r = F.rec + block_vec4(NV) * static_cast<int64_t>(k);
-        const float4 p = r[0], c0 = r[2], c1 = r[3];
+        const int k2 = neighbor(F, i, e0, min(e + 2, n - 1));  // in flight: the neighbour after next
+        const float4* blk = F.rec + BLK * static_cast<int64_t>(k);
+        const SiteRec rc = {blk[0], blk[1], blk[2], blk[3]};
         float c[3];
-        sh_eval_n<NV>(r + kRec, b, nb, c);
+        {
+            float b[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = lds[kBlock * q];
+                b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+            }
+            sh_eval_n<NV, NV>(blk + kRec, b, nb, c);
+        }
         c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
 #pragma unroll
-        for (int s = 0; s < kPend; ++s) {
-            if (s < P.n) {
-                float x[3], v[3];
-                float ts = P.t[s];
-                asm volatile("" : "+v"(ts));  // recompute x per neighbour (registers)
-                point_at(o, d, ts, x);
-                offset_to(p, x, v);
-                const float a = fexp(-0.5f * (color_m(c0, c1, v) - P.mmin[s]));
-                A[s] += a, cr[s] += a * c[0], cg[s] += a * c[1], cb[s] += a * c[2];
-            }
+        for (int j = 0; j < kFwd; ++j) {
+            float x[3], v[3];
+            float tj = t[j];
+            asm volatile("" : "+v"(tj));  // recompute x per neighbour: 3 fewer live registers per sample
+            point_at(o, d, tj, x);
+            offset_to(rc.q0, x, v);
+            const float dk = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+            if (dk < bd[j] || (dk == bd[j] && k < bk[j])) bd[j] = dk, bk[j] = k;
+            s[j] += fexp(rc.q0.w - 0.5f * density_m(rc, v));
+            const float mc = color_m(rc.q2, rc.q3, v);
+            const bool lower = mc < mm[j];  // a new minimum: the sums so far scale down, this term weighs 1
+            const float ex = fexp(-0.5f * (lower ? mm[j] - mc : mc - mm[j]));
+            const float keep = lower ? ex : 1.f, add = lower ? 1.f : ex;
+            float4 a = sums[kBlock * j];
+            a.x = a.x * keep + add;
+            a.y = a.y * keep + add * c[0], a.z = a.z * keep + add * c[1], a.w = a.w * keep + add * c[2];
+            sums[kBlock * j] = a;
+            mm[j] = fminf(mm[j], mc);
         }
         k = kn, kn = k2;
     }
 #pragma unroll
-    for (int s = 0; s < kPend; ++s) {
-        if (s < P.n) {
-            const float inv_a = 1.f / A[s];
-            const float C[3] = {cr[s] * inv_a, cg[s] * inv_a, cb[s] * inv_a};
-#pragma unroll
-            for (int a = 0; a < 3; ++a) acc[a] += P.w[s] * C[a];
-            dep += P.w[s] * P.t[s];
-        }
-    }
-    P.n = 0;
+    for (int j = 0; j < kFwd; ++j) R.best[j] = bk[j], R.sigma[j] = s[j], R.blend[j] = sums[kBlock * j];
 }
 
 template <int NV, bool TRACE>
 __device__ void march_ray(const MarchField& F, const MarchParams& M, const MarchRays& R, const MarchOut& O, int64_t r,
-                          int cur) {
+                          int cur, float4* lds) {
     const float o[3] = {R.o[3 * r], R.o[3 * r + 1], R.o[3 * r + 2]};
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
     const float near = R.t_near[r], mid = R.t_mid[r], far = R.t_far[r];
     const int n_in = mid > near ? static_cast<int>(ceilf((mid - near) / M.dt)) : 0;
     const int n_total = n_in + M.n_bg;
+    {  // the ray's SH basis, read by every colour evaluation of its passes
+        float b[16];
+        sh_basis(d[0], d[1], d[2], F.sh_deg, b);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds[kBlock * q] = make_float4(b[4 * q], b[4 * q + 1], b[4 * q + 2], b[4 * q + 3]);
+    }
     int n_samples = 0, n_color = 0, walk_steps = 0;
     float T = 1.f, acc[3] = {0.f, 0.f, 0.f}, dep = 0.f;
     // k: first unresolved sample; moves: greedy-walk steps taken so far for sample k
     int k = 0, moves = 0;
     bool live = true;
     while (live && k < n_total) {
-        float ts[kBatch];
+        float ts[kFwd];
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
+        for (int j = 0; j < kFwd; ++j) {
             float unused;
             sample_at(near, mid, far, n_in, M, min(k + j, n_total - 1), ts[j], unused);
         }
-        CellPass C;
-        cell_pass<block_vec4(NV)>(F, cur, o, d, ts, C);
+        FwdPass C;
+        fwd_pass<block_vec4(NV), NV>(F, cur, o, d, ts, lds, C);
         // walk bound reached: the sample takes the current site, unverified
         const bool force = moves >= kWalkCap;
         int nres = 0, next = cur;
         bool run = true;
-        // the coloured samples this pass resolves, all in site cur, blended by one colour pass right after
-        Pending P;
-        P.n = 0, P.cell = cur;
 #pragma unroll
-        for (int s = 0; s < kPend; ++s) P.t[s] = P.w[s] = P.mmin[s] = 0.f;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
+        for (int j = 0; j < kFwd; ++j) {
             if (!run || k + j >= n_total) {
                 run = false;
             } else if (C.best[j] == cur || (j == 0 && force)) {
@@ -324,10 +345,11 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
                 const float w = T * alpha;
                 ++n_samples, ++nres;
                 if (w > M.w_thresh) {
+                    const float inv_a = 1.f / C.blend[j].x;
+                    const float Cs[3] = {C.blend[j].y * inv_a, C.blend[j].z * inv_a, C.blend[j].w * inv_a};
 #pragma unroll
-                    for (int s = 0; s < kPend; ++s)
-                        if (s == P.n) P.t[s] = t, P.w[s] = w, P.mmin[s] = C.mmin[j];
-                    ++P.n;
+                    for (int a = 0; a < 3; ++a) acc[a] += w * Cs[a];
+                    dep += w * t;
                     ++n_color;
                 }
                 T *= 1.f - alpha;
@@ -336,7 +358,6 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
                 next = C.best[j], run = false;
             }
         }
-        flush<NV>(F, o, d, P, acc, dep);
         k += nres;
         moves = nres > 0 ? 0 : moves;
         if (live && k < n_total && next != cur) cur = next, ++walk_steps, ++moves;
@@ -348,13 +369,10 @@ __device__ void march_ray(const MarchField& F, const MarchParams& M, const March
     O.stats[3 * r] = n_samples, O.stats[3 * r + 1] = n_color, O.stats[3 * r + 2] = walk_steps;
 }
 
-// Minimum waves per SIMD the register allocation must allow. At 4 the colour pass spills about 17 VGPRs to scratch
-// and the kernel is still 5 % faster than at its natural 3 waves (146 VGPRs): it is bound by the gathers in flight.
-constexpr int kMarchWaves = 4;
-
 template <bool TRACE>
-__global__ void __launch_bounds__(kBlock, kMarchWaves)
+__global__ void __launch_bounds__(kBlock, kFwdWaves)
     march_forward_kernel(MarchField F, MarchParams M, MarchRays R, MarchOut O) {
+    __shared__ float4 fwd_lds[kFwdLds * kBlock];
     const int64_t i = xcd_block_id() * kBlock + threadIdx.x;
     if (i >= R.n) return;
     const int64_t r = R.order != nullptr ? R.order[i] : i;
@@ -367,10 +385,10 @@ __global__ void __launch_bounds__(kBlock, kMarchWaves)
         return;
     }
     switch (F.sh_deg) {
-        case 0: march_ray<sh_vec4_f32(0), TRACE>(F, M, R, O, r, cur); break;
-        case 1: march_ray<sh_vec4_f32(1), TRACE>(F, M, R, O, r, cur); break;
-        case 2: march_ray<sh_vec4_f32(2), TRACE>(F, M, R, O, r, cur); break;
-        default: march_ray<sh_vec4_f32(3), TRACE>(F, M, R, O, r, cur); break;
+        case 0: march_ray<sh_vec4_f32(0), TRACE>(F, M, R, O, r, cur, fwd_lds + threadIdx.x); break;
+        case 1: march_ray<sh_vec4_f32(1), TRACE>(F, M, R, O, r, cur, fwd_lds + threadIdx.x); break;
+        case 2: march_ray<sh_vec4_f32(2), TRACE>(F, M, R, O, r, cur, fwd_lds + threadIdx.x); break;
+        default: march_ray<sh_vec4_f32(3), TRACE>(F, M, R, O, r, cur, fwd_lds + threadIdx.x); break;
     }
 }
 
