@@ -301,7 +301,7 @@ def bench_foam(args):
 		pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
 	if args.no_slots:
 		pack.pop('slots', None)
-	if args.no_rows or lanes == 1:
+	if args.no_rows or lanes == 1 or mode != 2:  # the 64-byte rows serve the group layouts' fused blend
 		pack.pop('rows', None)
 
 	def launch(p, sel, m=mode, cut=color_cut):

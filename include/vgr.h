@@ -357,8 +357,8 @@ int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float*
  * weight > w_thresh). Every other stage, colour mode or layout runs vgr_foam_infer_lanes on the reference records
  * unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none) f32 (N, 16), 64-byte aligned:
  * the first 16 columns of attr (density conic, min(raw, 30), the cut-off word or padding, colour conic), which the
- * group layouts (lanes_per_ray 2, 4, 8) then read in place of the 80-byte attr rows: two whole rows per 128-byte
- * line, where 3 in 8 attr rows straddle two lines (bit-identical results). No counterpart in the reference (same
+ * group layouts (lanes_per_ray 2, 4, 8) with fused colours then read in place of the 80-byte attr rows: two whole
+ * rows per 128-byte line, where 3 in 8 attr rows straddle two lines (bit-identical results). No counterpart in the reference (same
  * function as vgr_foam_infer).
  */
 int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,

@@ -1287,6 +1287,10 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     VGR_REQUIRE(rgb && T && depth && stats, "foam_infer: null output pointer");
     const bool needs_sh = stage == 2 && color_mode != kBaked;
     VGR_REQUIRE(!needs_sh || sh != nullptr, "foam_infer: sh is required unless colors are baked");
+    // The 64-byte site rows serve the group layouts' fused blend (config 5's 8-lane batch: 2538.6 -> 2437.6 ms); the
+    // two-pass exact colours with 4 lanes per ray ran slower on them (268.9 against 258.3 ms on config 3) and keep
+    // the attr rows, as the one-ray-per-lane kernels do.
+    const bool rows_used = rows != nullptr && !indexed && stage == 2 && color_mode == kFused;
     const FoamScene S{reinterpret_cast<const float4*>(points),
                       offsets,
                       nbr,
@@ -1295,7 +1299,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                       needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
                       orig,
                       reinterpret_cast<const int4*>(slots),
-                      indexed ? nullptr : reinterpret_cast<const float4*>(rows),
+                      rows_used ? reinterpret_cast<const float4*>(rows) : nullptr,
                       static_cast<int>(n_sites)};
     const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
                        static_cast<int>(sh_deg)};
