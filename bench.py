@@ -410,7 +410,8 @@ def bench_foam(args):
 			'edge_records': 'indexed (vgr_foam_infer_indexed)' if indexed else 'reference',
 			'exact_colours': (('one-pass blend' if exact_blend else 'two passes') if mode == 0 else None),
 			'site_rows': '64-byte rows' if 'rows' in pack and lanes > 1 else '80-byte attr rows',
-			'cache_misses': ('slot table, once per pass' if 'slots' in pack else 'per-lookup tags in LDS')
+			'cache_misses': ('slot table, once per pass' if 'slots' in pack and lanes != 8 and math.isinf(color_cut)
+							 else 'per-lookup tags in LDS')
 			if args.colors != 'baked' else None,
 			'eps_color': args.eps_color, 'eps_density': args.eps_density, 'morton_reorder': not args.no_reorder,
 			'ray_order': (f'vgr_ray_order ({dir_res}x{dir_res} direction bins, {pos_bits}-bit origin Z-order) inside '

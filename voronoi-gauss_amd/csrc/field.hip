@@ -12,9 +12,10 @@
 //   reloads. The first-found rule of the sequential scan is the lexicographic minimum of (distance, CSR position),
 //   which the butterfly computes in any order, so sites and step counts are those of a sequential scan.
 // - density: one sample per lane over per-site Gaussian records built once per call (gauss_pack_kernel).
-// - colour: a group of 4 lanes per sample (16 samples per wave): lane g blends the entries g, g + 4, ... of the
-//   neighbourhood into a partial online softmax (its own running minimum), and the group merges the partials in a
-//   butterfly; four lanes keep four neighbours' SH rows in flight where one lane per sample keeps one.
+// - colour: below 2^22 samples a group of 4 lanes per sample (16 samples per wave): lane g blends the entries
+//   g, g + 4, ... of the neighbourhood into a partial online softmax (its own running minimum), and the group merges
+//   the partials in a butterfly, so that a small batch still fills the GPU; from 2^22 samples one lane per sample
+//   blends its whole neighbourhood (no merges).
 // - conic: one site per lane.
 #include "vgr_abi.h"
 #include "vgr_device.h"
