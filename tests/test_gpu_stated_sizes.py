@@ -180,9 +180,10 @@ def check_config5_bench_layout(s, sel, r):
 
 
 def test_foam_traces_and_exact_colours(stated):
-	"""On the subset: the fused render's cell sequences (common prefixes with the thresholds on), exact (two-pass)
-	colours within 1e-4, and with the thresholds off the stage-0 traversal and the full stage-2 render bit-exact
-	in their cells with every statistic equal."""
+	"""On the subset: the fused render's cell sequences (common prefixes with the thresholds on), exact colours
+	within 1e-4 both as two passes and as the one-pass blend (indexed records with the slot table, the path of
+	render_rays_foam_infer on an index_pack'ed pack), and with the thresholds off the stage-0 traversal and the full
+	stage-2 render bit-exact in their cells with every statistic equal."""
 	s = stated
 	sel = s.subset(SUBSET[s.config])
 	g = s.foam(sel, trace_cap=2048)
@@ -192,6 +193,17 @@ def test_foam_traces_and_exact_colours(stated):
 	r = s.oracle(sel, mode=0)
 	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
 	assert psnr(g['rgb'], r['rgb']) >= 60.0
+	p = s.pack
+	idx = ext.index_pack(p['offsets'], p['nbr'], p['edge'], p['attr'])
+	blend = s.foam(sel, mode=0, indexed=idx, slots=ext.slot_table(p['offsets'], p['nbr']))
+	del idx
+	compare(blend, r, stats_frac=0.995, t_max=s.sc.far_radius)
+	assert psnr(blend['rgb'], r['rgb']) >= 60.0
+	same = (blend['stats'] == g['stats']).all(1)
+	np.testing.assert_allclose(blend['rgb'][same], g['rgb'][same], atol=1e-5, rtol=0)
+	progress(f'[stated sizes] config {s.config}: exact colours, two passes / one-pass blend against the oracle on '
+			 f'{len(sel)} rays: max |rgb| {np.abs(g["rgb"] - r["rgb"]).max():.2e} / '
+			 f'{np.abs(blend["rgb"] - r["rgb"]).max():.2e}')
 	few = sel[::8]
 	for stage in (0, 2):
 		g = s.foam(few, stage=stage, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1)
