@@ -265,7 +265,8 @@ def bench_foam(args):
 	log(f'scene config {args.config}: {sc.n_sites} sites, {len(sc.adj)} adjacency entries ({time.time() - t0:.0f} s)')
 	model = VoronoiGaussField.from_scene(sc, dev)
 	fast = args.sh_half or args.eps_color > 0 or args.eps_density > 0 or args.colors == 'baked'
-	pack = render.pack_foam(model, reorder=not args.no_reorder, sh_half=args.sh_half, eps_density=args.eps_density)
+	pack = render.pack_foam(model, reorder=not args.no_reorder, sh_half=args.sh_half, eps_density=args.eps_density,
+							index=False)
 	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile, curve=args.tile_curve)
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	start = torch.from_numpy(start_np).to(dev)
@@ -347,7 +348,7 @@ def bench_foam(args):
 	sh_bytes = (6 if args.sh_half else 12) * (sc.sh_deg + 1) ** 2 if args.colors != 'baked' else 0
 	if fast:  # SH bytes per SH evaluation (an upper bound of the distinct sites); quality against the exact image
 		u_sh, u_rays = float(stats[:, 4].double().mean()), 0
-		exact = render.pack_foam(model, reorder=not args.no_reorder)
+		exact = render.pack_foam(model, reorder=not args.no_reorder, index=False)
 		ref = launch(exact, slice(None), 2, math.inf)
 		bg = 0.5
 		img, img_ref = rgb + T[:, None] * bg, ref[0] + ref[1][:, None] * bg
@@ -869,7 +870,7 @@ def bench_traverse(args):
 	dev = torch.device('cuda:0')
 	sc = scenes.make_scene(args.config, scale=args.scale, log=log)
 	model = VoronoiGaussField.from_scene(sc, dev)
-	pack = render.pack_foam(model, reorder=True)
+	pack = render.pack_foam(model, reorder=True, index=False)
 	o_np, d_np, start_np, _ = sc.camera_rays(tile=args.tile, curve=args.tile_curve)
 	o, d = torch.from_numpy(o_np).to(dev), torch.from_numpy(d_np).to(dev)
 	start = pack['inv'][torch.from_numpy(start_np).to(dev).long()].int()
@@ -947,7 +948,7 @@ def bench_pack(args):
 	torch.cuda.synchronize()
 	torch.cuda.reset_peak_memory_stats()
 	base = torch.cuda.memory_allocated()
-	launch_ms, pk, wall = time_steps(lambda: render.pack_foam(model, reorder=True), args.steps, args.warmup, stream)
+	launch_ms, pk, wall = time_steps(lambda: render.pack_foam(model, reorder=True, index=False), args.steps, args.warmup, stream)
 	peak = (torch.cuda.max_memory_allocated() - base) / 2 ** 30
 	ms = float(np.mean(launch_ms))
 	log(f'pack_foam (reorder) of {N} sites, {M} adjacency entries: mean {ms:.3f} ms, wall {wall:.3f} ms/step, '
@@ -968,7 +969,7 @@ def bench_pack(args):
 		t0 = time.perf_counter()
 		render.pack_foam_arrays(*hin, reorder=True)
 		t_cpu = time.perf_counter() - t0
-		g0, r0 = render.pack_foam(model, reorder=False), render.pack_foam_arrays(*hin, reorder=False)
+		g0, r0 = render.pack_foam(model, reorder=False, index=False), render.pack_foam_arrays(*hin, reorder=False)
 		# copied fields must match bit for bit; the cut-off words come from torch exp on two devices (a few ulps
 		# apart) rounded to half, so a rare one may differ in its last half bit
 		same = all(torch.equal(g0[k].cpu(), r0[k]) for k in ('points', 'offsets', 'nbr', 'attr', 'sh'))

@@ -189,7 +189,8 @@ def test_render_rays_with_indexed_pack(gpu, small):
 	model = SimpleNamespace(graph=ext.Graph(T(f.points), T(f.offsets), T(f.adj)), raw=T(f.raw),
 							d_log_scale=T(f.d_log_scale), d_quat=T(f.d_quat), c_log_scale=T(f.c_log_scale),
 							c_quat=T(f.c_quat), sh=lambda: T(f.sh), sh_deg=3, bg_logit=torch.zeros(3, device=gpu))
-	pack = render.pack_foam(model, reorder=True)
+	pack = render.pack_foam(model, reorder=True, index=False)
+	assert 'edge_i' not in pack and 'edge_i' in render.pack_foam(model, reorder=True)  # pack_foam indexes by default
 	a = render.render_rays_foam_infer(model, pack, T(o), T(d), T(start), far_radius=2.0, colors='fused',
 									  trace_cap=128)
 	render.index_pack(pack)

@@ -51,7 +51,7 @@ class Stated:
 		self.sc = sc = scenes.make_scene(config, log=None)
 		assert sc.n_sites >= 0.999 * scenes.SITE_COUNTS[config]
 		self.model = VoronoiGaussField.from_scene(sc, dev)
-		self.pack = render.pack_foam(self.model, reorder=True)
+		self.pack = render.pack_foam(self.model, reorder=True, index=False)
 		self.pk = {k: self.pack[k].cpu().numpy() for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh', 'orig')}
 		o, d, start, _ = sc.camera_rays(tile=8)
 		self.o, self.d = o, d

@@ -291,12 +291,14 @@ def pack_foam_arrays(points, offsets, adj, raw, d_log_scale, c_log_scale, dA, cA
 
 
 @torch.no_grad()
-def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=False):
+def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=False, index=True):
 	"""The inference renderer's records for a field (render.py:179-225), built on the GPU by vgr_pack_foam (the
 	renumbering's Z-order sort by torch): self-first neighbourhoods (offsets (N + 1), nbr (E)), one float4 per
 	neighbourhood entry (p_j, half2(r2_j, lam_j)), attr (N, 20) = (density conic, min(raw, 30), colour conic,
 	baked rgb), sh in fp32 or fp16; reorder renumbers the sites along a Z-order curve (perm: new -> old, inv: old ->
-	new, orig: the tie order of the original numbering)."""
+	new, orig: the tie order of the original numbering). index (an addition to the reference's arguments): also
+	build the derived records of index_pack (+16 B per neighbourhood entry and 208 B per site), through which
+	render_rays_foam_infer renders fused and exact colours fastest; index=False gives the reference's pack alone."""
 	g = model.graph
 	dA = ext.conic(model.d_log_scale, model.d_quat, scale_floor)
 	cA = ext.conic(model.c_log_scale, model.c_quat, scale_floor)
@@ -309,9 +311,10 @@ def pack_foam(model, scale_floor=0.0, eps_density=0.0, sh_half=False, reorder=Fa
 		model.raw, model.d_log_scale, model.c_log_scale, dA, cA)], model.sh().detach().float().contiguous(), perm,
 		scale_floor, eps_density, sh_half)
 	empty = torch.empty(0, device=g.points.device)
-	return {'points': out['points'], 'offsets': out['offsets'], 'nbr': out['nbr'], 'edge': out['edge'],
+	pack = {'points': out['points'], 'offsets': out['offsets'], 'nbr': out['nbr'], 'edge': out['edge'],
 			'attr': out['attr'], 'sh': out['sh16'] if sh_half else out['sh32'], 'sh32': out['sh32'], 'perm': perm,
 			'inv': inv, 'orig': (empty if perm is None else perm).int().contiguous(), 'baked_center': None}
+	return index_pack(pack) if index else pack
 
 
 @torch.no_grad()
