@@ -13,6 +13,7 @@
 // neighbourhood over the group's lanes; it is the faster one for traversal, density and lazy colours, one ray per
 // lane for fused and baked colours (default_lanes).
 #include <cmath>
+#include <type_traits>
 
 #include "vgr_abi.h"
 #include "vgr_device.h"
@@ -429,6 +430,46 @@ __device__ __forceinline__ int table_hits(const FoamScene& S, int c, int g, Slot
     return hits;
 }
 
+// One ray per lane with fused colours (one pass per sample): the cells of the passes whose cache hits are still to
+// be counted, and the ray's 8 tags, in the lane's private memory (the log is written at a varying index, so it and
+// the tags stay out of registers); every kPassLog passes, and at the end of the ray, the logged passes are counted
+// in order with the tags in registers for the while. Measured on config 3 against the tags in registers: 179.4 and
+// 179.3 ms (16 and 32 passes) against 179.8, 24 spilled VGPRs against 44; 64 passes 208.9 ms; for exact colours,
+// whose passes follow the samples' weights, 227.4 against 182.8 ms, so they keep the tags in registers.
+constexpr int kPassLog = 16;
+struct PassLog {
+    int mem[kPassLog + kRayTagSlots];  // cells of the logged passes, then the tags
+    int n;
+};
+
+__device__ __forceinline__ int log_flush(const FoamScene& S, PassLog& L) {
+    SlotTags<1> T;
+#pragma unroll
+    for (int s = 0; s < kRayTagSlots; ++s) T.t[s] = L.mem[kPassLog + s];
+    int hits = 0;
+    for (int i = 0; i < L.n; ++i) hits += table_hits<1>(S, L.mem[i], 0, T);
+#pragma unroll
+    for (int s = 0; s < kRayTagSlots; ++s) L.mem[kPassLog + s] = T.t[s];
+    L.n = 0;
+    return hits;
+}
+
+// The slot-table count of one ray per lane, with the tags behind a pass log (above) or in registers: set-up, a pass
+// over cell c that looked up every entry (returns the hits counted now: all of the log's when it fills up), and the
+// end of the ray (the hits not counted yet).
+__device__ __forceinline__ void tags_init(PassLog& L) {
+    L.n = 0;
+#pragma unroll
+    for (int s = 0; s < kRayTagSlots; ++s) L.mem[kPassLog + s] = -1;
+}
+__device__ __forceinline__ int tags_pass(const FoamScene& S, PassLog& L, int c) {
+    L.mem[L.n] = c;
+    return ++L.n == kPassLog ? log_flush(S, L) : 0;
+}
+__device__ __forceinline__ int tags_finish(const FoamScene& S, PassLog& L) { return log_flush(S, L); }
+__device__ __forceinline__ int tags_pass(const FoamScene& S, SlotTags<1>& T, int c) { return table_hits<1>(S, c, 0, T); }
+__device__ __forceinline__ int tags_finish(const FoamScene&, SlotTags<1>&) { return 0; }
+
 // Number of float4 a colour fetch reads: the blocks holding coefficients of degree <= DEG (the others multiply a
 // zero basis value, so leaving them out changes no finite colour).
 template <bool HALF, int DEG>
@@ -708,7 +749,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
     if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
-    SlotTags<1> tags;
+    std::conditional_t<TABLE && FUSED_SH && !EXACT, PassLog, SlotTags<1>> tags;
     tags_init(tags);
     int c = walk_to<COLOR == kFusedIdx>(S, start, o[0] + t_near * d[0], o[1] + t_near * d[1], o[2] + t_near * d[2],
                                         walk_steps);
@@ -717,7 +758,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
     bool litP = false;          // EXACT: the segment ending at the near sample was coloured
     eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, c, t_near, o, d, b, cache, true, E, n_dens,
                                               EXACT ? looks : n_sh);
-    if (TABLE && FUSED_SH && !EXACT) n_sh -= table_hits<1>(S, c, 0, tags);
+    if (TABLE && FUSED_SH && !EXACT) n_sh -= tags_pass(S, tags, c);
     trace_cell<TRACE>(S, O, r, 0, c);
     float sP = E.sigma, mP = E.mmin, tP = t_near, CP[3] = {0.f, 0.f, 0.f};
     bool hasP = false;
@@ -735,7 +776,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
         looksP = looks, looks = 0;
         eval_cell<STAGE, COLOR, HALF, DEG, TABLE>(S, P, cQ, tQ, o, d, b, cache, !last, E, n_dens,
                                                   EXACT ? looks : n_sh);
-        if (TABLE && FUSED_SH && !EXACT) n_sh -= table_hits<1>(S, cQ, 0, tags);
+        if (TABLE && FUSED_SH && !EXACT) n_sh -= tags_pass(S, tags, cQ);
         trace_cell<TRACE>(S, O, r, n_samples, cQ);
         ++n_samples;
         const float sQ = E.sigma, mQ = E.mmin;
@@ -751,16 +792,16 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
         const bool lit = STAGE >= 2 && w > P.w_thresh;
         if (lit) {
             if constexpr (EXACT) {
-                if (!litP) n_sh += looksP - table_hits<1>(S, cP, 0, tags);
-                n_sh += looks - table_hits<1>(S, cQ, 0, tags);
+                if (!litP) n_sh += looksP - tags_pass(S, tags, cP);
+                n_sh += looks - tags_pass(S, tags, cQ);
             }
             if constexpr (!BLEND) {
                 if (!hasP) {
                     color_lazy<HALF, DEG, TABLE>(S, P, cP, tP, mP, o, d, b, cache, CP, n_sh);
-                    if (TABLE) n_sh -= table_hits<1>(S, cP, 0, tags);
+                    if (TABLE) n_sh -= tags_pass(S, tags, cP);
                 }
                 color_lazy<HALF, DEG, TABLE>(S, P, cQ, tQ, mQ, o, d, b, cache, CQ, n_sh);
-                if (TABLE) n_sh -= table_hits<1>(S, cQ, 0, tags);
+                if (TABLE) n_sh -= tags_pass(S, tags, cQ);
                 hasQ = true;
             }
 #pragma unroll
@@ -774,6 +815,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock, TABLE>(STAGE
         for (int a = 0; a < 3; ++a) CP[a] = CQ[a];
         if (last || T < P.t_thresh) break;
     }
+    if (TABLE && kSH) n_sh -= tags_finish(S, tags);
 #pragma unroll
     for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
     O.T[r] = T;
