@@ -197,7 +197,10 @@ def main():
 	ap.add_argument('--eps-density', type=float, default=0.0, help='skip density terms below eps')
 	ap.add_argument('--no-reorder', action='store_true', help='keep the generator order of the sites')
 	ap.add_argument('--no-rows', action='store_true',
-					help='group layouts read the 80-byte attr rows instead of the 64-byte site rows')
+					help='group layouts read the 80-byte attr rows instead of the site rows')
+	ap.add_argument('--site-rows', type=int, default=256, choices=[64, 256],
+					help="group layouts' site rows: 256-byte site blocks holding the fp32 SH row (the default with "
+						 'fp32 SH), or the 64-byte rows beside the SH rows')
 	ap.add_argument('--no-slots', action='store_true',
 					help="no slot table: the reference's colour-cache misses counted with per-lookup tags in LDS")
 	ap.add_argument('--no-indexed', action='store_true',
@@ -295,15 +298,19 @@ def bench_foam(args):
 	exact_blend = mode == 0 and lanes == 1 and blend_ok
 	indexed = not args.no_indexed and lanes == 1 and (mode == 2 or exact_blend)
 	# the derived records, built once with the pack (untimed): indexed edge records, the slot table of the reference's
-	# colour cache, the 64-byte site rows of the group layouts
+	# colour cache, the site rows of the group layouts
 	if not args.no_indexed and args.colors != 'baked':
 		render.index_pack(pack)
 	elif args.colors != 'baked':
 		pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
 	if args.no_slots:
 		pack.pop('slots', None)
-	if args.no_rows or lanes == 1 or mode != 2:  # the 64-byte rows serve the group layouts' fused blend
+	if args.no_rows or lanes == 1 or mode != 2:  # the site rows serve the group layouts' fused blend
 		pack.pop('rows', None)
+	elif args.site_rows == 64 and 'rows' in pack and pack['rows'].size(1) == 64:
+		pack['rows'] = pack['rows'][:, :16].contiguous()
+	row_kind = None if 'rows' not in pack else '64-byte rows' if pack['rows'].size(1) == 16 else \
+		'256-byte site blocks (record + fp32 SH row)'
 
 	def launch(p, sel, m=mode, cut=color_cut):
 		order = ext.ray_order(o[sel], d[sel], dir_res, pos_bits) if ordered else None
@@ -376,8 +383,8 @@ def bench_foam(args):
 		key += f'-sh{"16" if args.sh_half else "32"}-ec{args.eps_color:g}-ed{args.eps_density:g}'
 	if indexed:
 		key += '-idx'
-	if 'rows' in pack and lanes > 1:
-		key += '-rows64'
+	if row_kind is not None:
+		key += '-rows64' if pack['rows'].size(1) == 16 else '-blocks256'
 	src = source_hash('foam_infer.hip')
 	log(f'kernel source hash (foam_infer.hip): {src}; workload key {key}')
 	roofline = hbm_roofline(ms, key, src, abytes,
@@ -410,7 +417,7 @@ def bench_foam(args):
 			'lanes_per_ray': lanes,
 			'edge_records': 'indexed (vgr_foam_infer_indexed)' if indexed else 'reference',
 			'exact_colours': (('one-pass blend' if exact_blend else 'two passes') if mode == 0 else None),
-			'site_rows': '64-byte rows' if 'rows' in pack and lanes > 1 else '80-byte attr rows',
+			'site_rows': row_kind or '80-byte attr rows',
 			'cache_misses': ('slot table, once per pass' if 'slots' in pack and lanes != 8 and math.isinf(color_cut)
 							 else 'per-lookup tags in LDS')
 			if args.colors != 'baked' else None,

@@ -355,11 +355,14 @@ int vgr_foam_index_pack(const int32_t* offsets, const int32_t* nbr, const float*
  * VGR_COLOR_FUSED (rgb within rounding of the two-pass exact colour: the same normalised sum over every neighbour,
  * kept relative to a running minimum), stats[:, 4] the exact mode's cache misses (its colour passes: segments of
  * weight > w_thresh). Every other stage, colour mode or layout runs vgr_foam_infer_lanes on the reference records
- * unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none) f32 (N, 16), 64-byte aligned:
- * the first 16 columns of attr (density conic, min(raw, 30), the cut-off word or padding, colour conic), which the
- * group layouts (lanes_per_ray 2, 4, 8) with fused colours then read in place of the 80-byte attr rows: two whole
- * rows per 128-byte line, where 3 in 8 attr rows straddle two lines (bit-identical results). No counterpart in the reference (same
- * function as vgr_foam_infer).
+ * unchanged. slots as for vgr_foam_infer_lanes. rows (NULL = none): site rows of row_floats floats each, the first
+ * 16 being the first 16 columns of attr (density conic, min(raw, 30), the cut-off word or padding, colour conic),
+ * which the group layouts (lanes_per_ray 2, 4, 8) with fused colours then read in place of the 80-byte attr rows
+ * (bit-identical results). row_floats 16: f32 (N, 16), 64-byte aligned, two whole rows per 128-byte line, where
+ * 3 in 8 attr rows straddle two lines. row_floats 64: 256-byte site blocks f32 (N, 64), 256-byte aligned, whose
+ * last 48 floats are the site's fp32 SH row as in sh (sh_half must be 0); those kernels then read the SH rows
+ * from the blocks too, so that a neighbour visit's record and SH row take two 128-byte lines instead of three.
+ * No counterpart in the reference (same function as vgr_foam_infer).
  */
 int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* offsets, const int32_t* nbr,
                            const float* edge, int64_t n_edges, const float* attr, const void* sh, int32_t sh_half,
@@ -368,7 +371,7 @@ int vgr_foam_infer_indexed(const float* points, int64_t n_sites, const int32_t* 
                            int64_t color_mode, int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb,
                            float* T, float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                            const int32_t* order, int64_t lanes_per_ray, const float* edge_i, const float* attr_i,
-                           const int32_t* slots, const float* rows, void* stream);
+                           const int32_t* slots, const float* rows, int64_t row_floats, void* stream);
 
 /*
  * Slot table of a foam pack, for the `slots` argument of vgr_foam_infer_lanes and vgr_foam_infer_indexed. No

@@ -110,10 +110,16 @@ def test_indexed_records_arguments_without_a_gpu():
 	assert pack(10, 20) == 1 and b'null pointer' in lib.vgr_last_error()
 	assert pack(0, 0) == 0
 	args = [None, 10, None, None, None, 10, None, None, 0, 3, None, None, None, None, None, 5, 1e-4, 1e-4, 1e30, 2, 2,
-			None, None, None, None, None, None, None, 0, None, 0, None, None, None, None, None]
+			None, None, None, None, None, None, None, 0, None, 0, None, None, None, None, 16, None]
 	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'edge_i and attr_i' in lib.vgr_last_error()
 	args[27], args[28] = 1, 0  # a trace sink without a capacity
 	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'trace_cap' in lib.vgr_last_error()
+	# site blocks (row_floats 64) must sit on 256-byte boundaries, 64-byte rows on 64-byte ones
+	args[27], args[28] = None, 0
+	args[31], args[32], args[34], args[35] = 4096, 8192, 64, 64
+	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'256-byte aligned' in lib.vgr_last_error()
+	args[34], args[35] = 64 + 32, 16
+	assert lib.vgr_foam_infer_indexed(*args) == 1 and b'64-byte aligned' in lib.vgr_last_error()
 
 
 def test_slot_table_arguments_without_a_gpu():

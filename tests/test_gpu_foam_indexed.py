@@ -212,8 +212,9 @@ def test_render_rays_with_indexed_pack(gpu, small):
 @pytest.mark.parametrize('lanes', [2, 4, 8])
 def test_site_rows_identical_in_group_layouts(gpu, small, lanes):
 	"""The group layouts reading the 64-byte site rows (the first 16 record columns, rows of ext.foam_infer's indexed
-	argument) give every output bit-identical to the 80-byte attr rows: fused and exact colours, thresholds on and
-	off, renumbered or not, with the slot table and without."""
+	argument), or the 256-byte site blocks that hold the fp32 SH row after them (read in place of sh too), give every
+	output bit-identical to the 80-byte attr rows: fused and exact colours, thresholds on and off, renumbered or not,
+	with the slot table and without. Site blocks with fp16 SH are refused."""
 	f, (o, d, start, near, _, far) = small
 	t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=gpu)  # noqa: E731
 	empty = torch.empty(0, dtype=torch.int32, device=gpu)
@@ -223,17 +224,24 @@ def test_site_rows_identical_in_group_layouts(gpu, small, lanes):
 		tens = {k: t(pk[k]) for k in ('points', 'offsets', 'nbr', 'edge', 'attr', 'sh')}
 		ei, ai = ext.index_pack(tens['offsets'], tens['nbr'], tens['edge'], tens['attr'])
 		rows = ai[:, :16].contiguous()
+		blocks = torch.cat([rows, tens['sh'].reshape(-1, 48)], 1).contiguous()
+		assert blocks.data_ptr() % 256 == 0
 		slots = ext.slot_table(tens['offsets'], tens['nbr'])
 		orig = t(pk['orig']) if pk.get('orig') is not None and len(pk['orig']) else empty
 		for mode in (0, 2):
 			for tt, wt in ((1e-4, 1e-4), (0.0, -1.0)):
 				outs = []
-				for idx, sl in (((ei, ai), None), ((ei, ai, rows), None), ((ei, ai, rows), slots)):
+				for idx, sl in (((ei, ai), None), ((ei, ai, rows), None), ((ei, ai, rows), slots),
+								((ei, ai, blocks), None), ((ei, ai, blocks), slots)):
 					out = ext.foam_infer_extension().foam_infer(
 						tens['points'], tens['offsets'], tens['nbr'], tens['edge'], tens['attr'], tens['sh'], 3, t(o),
 						t(d), t(st), t(near), t(far), tt, wt, math.inf, mode, 2, empty, orig, trace_cap=256,
 						lanes=lanes, indexed=idx, slots=sl)
 					torch.cuda.synchronize()
 					outs.append(dict(zip(FIELDS, [x.cpu().numpy() for x in out])))
-				assert_identical(outs[0], outs[1])
-				assert_identical(outs[0], outs[2])
+				for other in outs[1:]:
+					assert_identical(outs[0], other)
+	with pytest.raises(RuntimeError, match='float32'):
+		ext.foam_infer_extension().foam_infer(
+			tens['points'], tens['offsets'], tens['nbr'], tens['edge'], tens['attr'], tens['sh'].half(), 3, t(o), t(d),
+			t(st), t(near), t(far), 1e-4, 1e-4, math.inf, 2, 2, empty, orig, lanes=lanes, indexed=(ei, ai, blocks))

@@ -167,8 +167,17 @@ def check_config5_bench_layout(s, sel, r):
 	direction bins, 7-bit origins), over the whole batch; against the oracle's rays `sel` (results r), and the same
 	cells and statistics as the one-ray-per-lane kernel with the thresholds off."""
 	order = ext.ray_order(s.t(s.o), s.t(s.d), 8, 7)
-	g = rows(s.foam(lanes=8, order=order, slots=ext.slot_table(s.pack['offsets'], s.pack['nbr'])), sel)
+	slots = ext.slot_table(s.pack['offsets'], s.pack['nbr'])
+	full = s.foam(lanes=8, order=order, slots=slots)
+	g = rows(full, sel)
 	compare(g, r, stats_frac=0.995, t_max=s.sc.far_radius)
+	# the bench's site blocks (record + fp32 SH row in 256 bytes): every output bit-identical
+	ei, ai = ext.index_pack(s.pack['offsets'], s.pack['nbr'], s.pack['edge'], s.pack['attr'])
+	blocks = torch.cat([ai[:, :16], s.pack['sh'].reshape(-1, 48)], 1).contiguous()
+	fb = s.foam(lanes=8, order=order, slots=slots, indexed=(ei, ai, blocks))
+	del ei, ai, blocks
+	for k in ('rgb', 'T', 'depth', 'stats'):
+		np.testing.assert_array_equal(fb[k], full[k], err_msg=k)
 	assert psnr(g['rgb'], r['rgb']) >= 60.0
 	few = sel[::8]
 	g8 = s.foam(few, stage=0, t_thresh=0.0, w_thresh=-1.0, trace_cap=MAX_CELLS + 1, lanes=8)

@@ -37,8 +37,10 @@ struct FoamScene {
     const float4* __restrict__ sh;      // (N, 12) fp32 or (N, 6) fp16
     const int* __restrict__ orig;       // (N) or null
     const int4* __restrict__ slots;     // (N, 4) slot table (vgr_foam_slot_table) or null
-    const float4* __restrict__ rows;    // (N, 4) 64-byte site rows (the first 16 attr columns) or null
+    const float4* __restrict__ rows;    // site rows (the first 16 attr columns) or null, row_stride float4 apart
     int n_sites;
+    int row_stride;  // float4 from one site row to the next: 4 (64-byte rows) or 16 (256-byte site blocks)
+    int sh_stride;   // float4 from one SH row to the next: 12 (fp32), 6 (fp16) or 16 (the SH rows of site blocks)
 };
 
 struct FoamParams {
@@ -308,7 +310,7 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // Wave barriers separate the phases: the lanes of a phase act on what every lane did in the phase before, and the
 // barrier is convergent, so the compiler cannot merge one-sided stores across it.
 template <bool HALF, int NV, int COLOR>
-__device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4* __restrict__ sh, int k,
+__device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4* __restrict__ sh, int stride, int k,
                                               const float (&b)[16], float (&c)[3]) {
     constexpr int SLOTS = Tune<COLOR>::slots, OVF = Tune<COLOR>::overflow, BLOCKS = SLOTS + OVF;
     const int lane = static_cast<int>(threadIdx.x);
@@ -359,7 +361,7 @@ __device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4
                 if (j < total) {
                     const int r = j / NV, q = j - r * NV;
                     const int kr = C.req_k[r];
-                    C.data[q * BLOCKS + C.req_b[r]] = sh[(HALF ? 6 : 12) * static_cast<int64_t>(kr) + q];
+                    C.data[q * BLOCKS + C.req_b[r]] = sh[stride * static_cast<int64_t>(kr) + q];
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -525,10 +527,12 @@ struct SiteRec {
     float4 q0, q1, q2, q3;
 };
 
-// The group layout's site records: the 64-byte rows when the caller gives them (one 128-byte line holds two whole
-// rows, where 3 of 8 of the 80-byte attr rows straddle two lines), else the attr rows.
+// The group layout's site records: the site rows when the caller gives them, else the attr rows. The rows are 64
+// bytes apart (one 128-byte line holds two whole rows, where 3 of 8 of the 80-byte attr rows straddle two lines), or
+// 256 bytes apart in site blocks whose last 192 bytes hold the site's fp32 SH row: the record and the SH row of a
+// neighbour visit then take two 128-byte lines, where a row and a separate 192-byte SH row take three.
 __device__ __forceinline__ const float4* group_row(const FoamScene& S, int k) {
-    return S.rows != nullptr ? S.rows + 4 * static_cast<int64_t>(k) : S.attr + 5 * static_cast<int64_t>(k);
+    return S.rows != nullptr ? S.rows + S.row_stride * static_cast<int64_t>(k) : S.attr + 5 * static_cast<int64_t>(k);
 }
 
 template <int STAGE>
@@ -634,7 +638,7 @@ __device__ void eval_cell(const FoamScene& S, const FoamParams& P, int c, float 
                             } else {
                                 if constexpr (TABLE) ++n_sh;  // the pass's hits come off in table_hits
                                 else n_sh += ray_tag_miss(cache, k);
-                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, HALF ? 6 : 12, k, b, c3);
                             }
                             blend_add(R.B, m, c3[0], c3[1], c3[2]);
                         }
@@ -689,7 +693,7 @@ __device__ void color_lazy(const FoamScene& S, const FoamParams& P, int c, float
                 float c3[3];
                 if constexpr (TABLE) ++n_sh;
                 else n_sh += ray_tag_miss(cache, k);
-                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, HALF ? 6 : 12, k, b, c3);
                 accumulate(A, r, g, bl, weight_of(m, mmin), c3);
             }
         }
@@ -993,7 +997,7 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
                             const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
                             c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
                         } else {
-                            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+                            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
                         }
                         blend_add(R.B, m, c3[0], c3[1], c3[2]);
                     }
@@ -1035,7 +1039,7 @@ __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c,
         else n_sh += group_tag_miss<G>(cache, g, look, k);  // the group's lanes converged
         if (look) {
             float c3[3];
-            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, k, b, c3);
+            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
             accumulate(A, r, gr, bl, weight_of(m, mmin), c3);
         }
     }
@@ -1301,7 +1305,7 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
                const int32_t* cap, const int32_t* orig, float* rgb, float* T, float* depth, int32_t* stats,
                int32_t* trace, int64_t trace_cap, const int32_t* order, int64_t lanes, void* stream,
                const float* edge_i = nullptr, const float* attr_i = nullptr, const int32_t* slots = nullptr,
-               const float* rows = nullptr) {
+               const float* rows = nullptr, int64_t row_floats = 16) {
     VGR_REQUIRE(n_rays >= 0, "foam_infer: n_rays must be >= 0 (got %lld)", static_cast<long long>(n_rays));
     // The indexed edge records serve the fused blend with one ray per lane (its default layout), and with the slot
     // table and the colour cut-off +inf the exact colours too, run by that blend (foam_infer_kernel, EXACT).
@@ -1329,28 +1333,38 @@ int foam_entry(const float* points, int64_t n_sites, const int32_t* offsets, con
     VGR_REQUIRE(rgb && T && depth && stats, "foam_infer: null output pointer");
     const bool needs_sh = stage == 2 && color_mode != kBaked;
     VGR_REQUIRE(!needs_sh || sh != nullptr, "foam_infer: sh is required unless colors are baked");
-    // The 64-byte site rows serve the group layouts' fused blend (config 5's 8-lane batch: 2538.6 -> 2437.6 ms); the
-    // two-pass exact colours with 4 lanes per ray ran slower on them (268.9 against 258.3 ms on config 3) and keep
-    // the attr rows, as the one-ray-per-lane kernels do.
-    const bool rows_used = rows != nullptr && !indexed && stage == 2 && color_mode == kFused;
+    VGR_REQUIRE(row_floats == 16 || row_floats == 64, "foam_infer: row_floats must be 16 or 64 (got %lld)",
+                static_cast<long long>(row_floats));
+    VGR_REQUIRE(row_floats == 16 || rows == nullptr || sh_half == 0,
+                "foam_infer: site blocks (row_floats 64) hold fp32 SH rows; sh_half must be 0");
+    // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
+    // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
+    if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
+    // The site rows serve the group layouts' fused blend (config 5's 8-lane batch: 2538.6 -> 2437.6 ms with the
+    // 64-byte rows); the two-pass exact colours with 4 lanes per ray ran slower on them (268.9 against 258.3 ms on
+    // config 3) and keep the attr rows, as the one-ray-per-lane kernels do. Site blocks also supply those kernels'
+    // SH rows, 16 float4 apart after each 4-float4 record.
+    const bool rows_used = rows != nullptr && !indexed && stage == 2 && color_mode == kFused && lanes > 1;
+    const bool blocks = rows_used && row_floats == 64;
     const FoamScene S{reinterpret_cast<const float4*>(points),
                       offsets,
                       nbr,
                       reinterpret_cast<const float4*>(indexed ? edge_i : edge),
                       reinterpret_cast<const float4*>(indexed ? attr_i : attr),
-                      needs_sh ? reinterpret_cast<const float4*>(sh) : nullptr,
+                      !needs_sh ? nullptr
+                      : blocks  ? reinterpret_cast<const float4*>(rows) + 4
+                                : reinterpret_cast<const float4*>(sh),
                       orig,
                       reinterpret_cast<const int4*>(slots),
                       rows_used ? reinterpret_cast<const float4*>(rows) : nullptr,
-                      static_cast<int>(n_sites)};
+                      static_cast<int>(n_sites),
+                      static_cast<int>(row_floats / 4),
+                      blocks ? 16 : sh_half != 0 ? 6 : 12};
     const FoamParams P{static_cast<float>(t_thresh), static_cast<float>(w_thresh), static_cast<float>(color_cut),
                        static_cast<int>(sh_deg)};
     const FoamRays R{o, d, start, near_t, far_t, cap, n_rays, order};
     const FoamOut O{rgb, T, depth, stats, trace, trace_cap};
     const hipStream_t s = as_stream(stream);
-    // Fused and baked blends with a finite colour cut skip a neighbour against the running minimum of the terms
-    // before it in edge order; a lane of a group sees only its own share of them, so these run one ray per lane.
-    if (stage == 2 && color_mode != kLazy && !(color_cut > 1e30)) lanes = 1;
     // The slot table gives the reference's cache misses per pass when a pass looks up every entry: colour cut-off
     // +inf (a pass with a finite cut-off skips entries, and keeps its tags in LDS per lookup). With 8 lanes per ray
     // (incoherent batches, bound by DRAM) the table's reads cost more than the per-lookup tags, which need only
@@ -1430,15 +1444,16 @@ extern "C" int vgr_foam_infer_indexed(const float* points, int64_t n_sites, cons
                                       int64_t stage, const int32_t* cap, const int32_t* orig, float* rgb, float* T,
                                       float* depth, int32_t* stats, int32_t* trace, int64_t trace_cap,
                                       const int32_t* order, int64_t lanes_per_ray, const float* edge_i,
-                                      const float* attr_i, const int32_t* slots, const float* rows, void* stream) {
+                                      const float* attr_i, const int32_t* slots, const float* rows,
+                                      int64_t row_floats, void* stream) {
     VGR_REQUIRE(trace == nullptr || trace_cap > 0, "foam_infer_indexed: trace needs trace_cap > 0");
     VGR_REQUIRE(edge_i && attr_i, "foam_infer_indexed: edge_i and attr_i are required");
-    VGR_REQUIRE(rows == nullptr || reinterpret_cast<uintptr_t>(rows) % 64 == 0,
-                "foam_infer_indexed: rows must be 64-byte aligned");
+    VGR_REQUIRE(rows == nullptr || reinterpret_cast<uintptr_t>(rows) % (row_floats == 64 ? 256 : 64) == 0,
+                "foam_infer_indexed: rows must be 64-byte aligned, site blocks 256-byte aligned");
     return vgr::foam_entry(points, n_sites, offsets, nbr, edge, n_edges, attr, sh, sh_half, sh_deg, o, d, start,
                            near_t, far_t, n_rays, t_thresh, w_thresh, color_cut, color_mode, stage, cap, orig, rgb,
                            T, depth, stats, trace, trace == nullptr ? 0 : trace_cap, order, lanes_per_ray, stream,
-                           edge_i, attr_i, slots, rows);
+                           edge_i, attr_i, slots, rows, row_floats);
 }
 
 extern "C" int vgr_foam_slot_table(const int32_t* offsets, const int32_t* nbr, int64_t n_sites, int64_t n_edges,

@@ -60,7 +60,8 @@ SIGNATURES = {
 	'vgr_ray_order': [_P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
 	'vgr_foam_index_pack': [_P, _P, _P, _P, _I64, _I64, _P, _P, _P],
 	'vgr_foam_infer_indexed': [_P, _I64, _P, _P, _P, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _I64, _F64,
-							   _F64, _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P, _P],
+							   _F64, _F64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P, _I64,
+							   _P],
 	'vgr_foam_slot_table': [_P, _P, _I64, _I64, _P, _P],
 	'vgr_grid_build_noalloc': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P],
 	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
@@ -68,7 +69,7 @@ SIGNATURES = {
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 24
+ABI_VERSION = 25
 _lib = None
 
 

@@ -276,8 +276,10 @@ class _FoamInferExtension:
 		(a ray it leaves out keeps uninitialised outputs; VGR_CHECK_ORDER=1 verifies it)
 		(ray_order); the results are the same. indexed: optional (edge_i, attr_i) from index_pack, read by the
 		fused rendering with one ray per lane in place of nbr / edge / attr (vgr_foam_infer_indexed, bit-identical
-		results), or (edge_i, attr_i, rows) with the 64-byte site rows (N, 16) that the group layouts then read in
-		place of attr (bit-identical results); other stages, colour modes and layouts ignore them. slots: optional int32 (N, 16) slot table
+		results), or (edge_i, attr_i, rows) with site rows that the group layouts' fused blend then reads in place
+		of attr (bit-identical results): the 64-byte rows (N, 16), or 256-byte site blocks (N, 64) whose last 48
+		floats are the fp32 SH row (sh must then be float32), read in place of sh too; other stages, colour modes
+		and layouts ignore them. slots: optional int32 (N, 16) slot table
 		(slot_table) of the same pack: with color_cut = +inf the reference's colour-cache misses (stats[:, 4]) are
 		counted from it once per neighbourhood pass instead of per lookup (the same counts, faster)."""
 		for t, n, dt in ((points, 'points', torch.float32), (offsets, 'offsets', torch.int32),
@@ -326,7 +328,11 @@ class _FoamInferExtension:
 					 'edge_i and attr_i must have the shapes of edge and attr')
 			if rows is not None:
 				_check(rows, 'rows', torch.float32)
-				_require(rows.shape == (n, 16) and rows.data_ptr() % 64 == 0, 'rows must be (N, 16), 64-byte aligned')
+				blocks = rows.dim() == 2 and rows.shape == (n, 64)
+				_require((rows.dim() == 2 and rows.shape == (n, 16) and rows.data_ptr() % 64 == 0) or
+						 (blocks and rows.data_ptr() % 256 == 0),
+						 'rows must be (N, 16) 64-byte aligned, or site blocks (N, 64) 256-byte aligned')
+				_require(not blocks or not half, 'site blocks hold fp32 SH rows: sh must be float32')
 		if slots is not None:
 			_check(slots, 'slots', torch.int32)
 			_require(slots.dim() == 2 and slots.shape == (n, 16), 'slots must be (N, 16)')
@@ -334,7 +340,7 @@ class _FoamInferExtension:
 			if indexed is not None:
 				call('vgr_foam_infer_indexed', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(edge_i), ptr(attr_i),
-					 ptr(slots), ptr(rows), stream_of(dev))
+					 ptr(slots), ptr(rows), 16 if rows is None else rows.size(1), stream_of(dev))
 			elif lanes is not None or order is not None or slots is not None:
 				call('vgr_foam_infer_lanes', *args, ptr(trace), int(trace_cap) if trace is not None else 0,
 					 ptr(_order(order, B, dev)), 0 if lanes is None else int(lanes), ptr(slots), stream_of(dev))

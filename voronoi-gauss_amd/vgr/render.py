@@ -322,11 +322,17 @@ def index_pack(pack):
 	"""Adds the indexed edge records (ext.index_pack: edge_i, attr_i) and the slot table of the reference's colour
 	cache (ext.slot_table: slots) to a GPU pack; render_rays_foam_infer then renders fused colours with one record
 	stream per neighbourhood entry, bit-identical to the reference records, and counts the cache misses of
-	stats[:, 4] once per neighbourhood pass; and the 64-byte site rows (rows: the first 16 columns of the records,
-	two whole rows per 128-byte line) that the group layouts read. A snapshot: call again after changing the pack."""
+	stats[:, 4] once per neighbourhood pass; and the site rows that the group layouts' fused blend reads (rows:
+	the first 16 columns of the records; with fp32 SH, 256-byte site blocks (N, 64) that hold the SH row after
+	them, so a neighbour visit reads two 128-byte lines for both, else 64-byte rows (N, 16), two per line). A
+	snapshot: call again after changing the pack."""
 	pack['edge_i'], pack['attr_i'] = ext.index_pack(pack['offsets'], pack['nbr'], pack['edge'], pack['attr'])
 	pack['slots'] = ext.slot_table(pack['offsets'], pack['nbr'])
-	pack['rows'] = pack['attr_i'][:, :16].contiguous()
+	n = pack['attr_i'].size(0)
+	if pack['sh'].dtype == torch.float32:
+		pack['rows'] = torch.cat([pack['attr_i'][:, :16], pack['sh'].reshape(n, 48)], 1).contiguous()
+	else:
+		pack['rows'] = pack['attr_i'][:, :16].contiguous()
 	return pack
 
 
