@@ -136,11 +136,11 @@ __device__ __forceinline__ void accumulate(float& A, float& r, float& g, float& 
 
 // Adds blocks q0 .. q0 + 3 (those below nv) of a site's SH coefficients (fp32, or fp16 pairs) to c: the colour
 // SH_k(d) accumulates over the coefficients in storage order, coefficient i of channel i mod 3 times basis i / 3.
-template <bool HALF>
-__device__ __forceinline__ void sh_accumulate(const float4 (&f)[4], int q0, int nv, const float (&b)[16],
+template <bool HALF, int CH = 4>
+__device__ __forceinline__ void sh_accumulate(const float4 (&f)[CH], int q0, int nv, const float (&b)[16],
                                               float (&c)[3]) {
 #pragma unroll
-    for (int uq = 0; uq < 4; ++uq) {
+    for (int uq = 0; uq < CH; ++uq) {
         const int q = q0 + uq;
         if (q >= nv) break;
         const float fv[4] = {f[uq].x, f[uq].y, f[uq].z, f[uq].w};
@@ -295,6 +295,31 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // max(SH_k(d) + 1/2, 0) for every active lane (the lanes that need a colour now; control flow is uniform across
 // them), site k's coefficient block read through the wave cache.
 //
+// The SH basis of the ray's direction that a colour evaluation multiplies: held in registers for the whole ray, or,
+// with 8 lanes per ray (memory-bound batches), evaluated at each lookup from the direction, which takes 16 registers
+// out of the sample loop. The empty asm keeps the compiler from hoisting that evaluation out of the loops. Measured
+// on config 5's 8-lane batch: 2271 -> 2207 ms (24 -> 12 spilled VGPRs), and 2171 ms (5, none stored in the sample
+// loop) with the block read two float4 at a time in that evaluation. The one-ray-per-lane kernels keep the basis and
+// four float4 at a time: two gave 20 spilled VGPRs instead of 24 there but 183.0 against 179.6 ms on config 3.
+constexpr int kLateBasisLanes = 8;  // lanes per ray of the layout that evaluates the basis per lookup
+
+template <int DEG>
+struct LateBasis {
+    float x, y, z;
+};
+
+__device__ __forceinline__ void basis_fill(const float (&b)[16], float (&out)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[i] = b[i];
+}
+
+template <int DEG>
+__device__ __forceinline__ void basis_fill(const LateBasis<DEG>& L, float (&out)[16]) {
+    float x = L.x, y = L.y, z = L.z;
+    asm volatile("" : "+v"(x), "+v"(y), "+v"(z));
+    sh_basis(x, y, z, DEG, out);
+}
+
 // The texture path and LDS charge a wave-wide load the same cycles however few of its lanes are active, and the
 // evaluation (12 LDS reads, 48 FMAs) costs the wave the same however few of its lanes take part, so a lookup aims
 // to serve every lane in one pass. Each pass:
@@ -309,9 +334,9 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // every pass serves at least one lane, so the loop ends (after the first pass in about 4 lookups of 5 on config 3).
 // Wave barriers separate the phases: the lanes of a phase act on what every lane did in the phase before, and the
 // barrier is convergent, so the compiler cannot merge one-sided stores across it.
-template <bool HALF, int NV, int COLOR>
+template <bool HALF, int NV, int COLOR, class BASIS>
 __device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4* __restrict__ sh, int stride, int k,
-                                              const float (&b)[16], float (&c)[3]) {
+                                              const BASIS& basis, float (&c)[3]) {
     constexpr int SLOTS = Tune<COLOR>::slots, OVF = Tune<COLOR>::overflow, BLOCKS = SLOTS + OVF;
     const int lane = static_cast<int>(threadIdx.x);
     const int home = slot_of<SLOTS>(k);
@@ -367,14 +392,18 @@ __device__ __forceinline__ void cached_colour(ColorCache<COLOR>& C, const float4
             __builtin_amdgcn_wave_barrier();
         }
         if (served) {
+            float b[16];
+            basis_fill(basis, b);
+            // with the basis evaluated here, two float4 of the block at a time (else four)
+            constexpr int CH = std::is_same_v<BASIS, float[16]> ? 4 : 2;
             c[0] = c[1] = c[2] = 0.5f;
 #pragma unroll
-            for (int q0 = 0; q0 < NV; q0 += 4) {
-                float4 f[4];
+            for (int q0 = 0; q0 < NV; q0 += CH) {
+                float4 f[CH];
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < CH; ++u)
                     if (q0 + u < NV) f[u] = C.data[(q0 + u) * BLOCKS + block];
-                sh_accumulate<HALF>(f, q0, NV, b, c);
+                sh_accumulate<HALF, CH>(f, q0, NV, b, c);
                 __builtin_amdgcn_sched_barrier(0);  // one chunk of the block in registers at a time
             }
             c[0] = fmaxf(c[0], 0.f), c[1] = fmaxf(c[1], 0.f), c[2] = fmaxf(c[2], 0.f);
@@ -997,7 +1026,11 @@ __device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, 
                             const float4 q4 = S.attr[5 * static_cast<int64_t>(k) + 4];
                             c3[0] = q4.x, c3[1] = q4.y, c3[2] = q4.z;
                         } else {
-                            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
+                            if constexpr (G == kLateBasisLanes)
+                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k,
+                                                                         LateBasis<DEG>{d[0], d[1], d[2]}, c3);
+                            else
+                                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
                         }
                         blend_add(R.B, m, c3[0], c3[1], c3[2]);
                     }
@@ -1039,7 +1072,11 @@ __device__ void color_lazy_group(const FoamScene& S, const FoamParams& P, int c,
         else n_sh += group_tag_miss<G>(cache, g, look, k);  // the group's lanes converged
         if (look) {
             float c3[3];
-            cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
+            if constexpr (G == kLateBasisLanes)
+                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, LateBasis<DEG>{d[0], d[1], d[2]},
+                                                         c3);
+            else
+                cached_colour<HALF, sh_vec4<HALF, DEG>()>(cache, S.sh, S.sh_stride, k, b, c3);
             accumulate(A, r, gr, bl, weight_of(m, mmin), c3);
         }
     }
@@ -1078,10 +1115,10 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock / G, TABLE>(S
     const float d[3] = {R.d[3 * r], R.d[3 * r + 1], R.d[3 * r + 2]};
     const float t_near = R.t_near[r], t_far = R.t_far[r];
     const int max_samples = R.cap != nullptr ? R.cap[r] : INT_MAX;
-    float b[16];
+    float b[16];  // unused with 8 lanes per ray, which evaluate it per lookup
 #pragma unroll
     for (int i = 0; i < 16; ++i) b[i] = 0.f;
-    if (kSH) sh_basis(d[0], d[1], d[2], DEG, b);
+    if (kSH && G != kLateBasisLanes) sh_basis(d[0], d[1], d[2], DEG, b);
 
     int walk_steps = 0, n_dens = 0, n_sh = 0;
     SlotTags<G> tags;
