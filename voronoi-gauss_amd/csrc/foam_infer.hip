@@ -303,6 +303,14 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // four float4 at a time: two gave 20 spilled VGPRs instead of 24 there but 183.0 against 179.6 ms on config 3.
 constexpr int kLateBasisLanes = 8;  // lanes per ray of the layout that evaluates the basis per lookup
 
+// This lane's index in its wave, read from the hardware where it is needed (mbcnt over a full mask). Inside an asm
+// statement the compiler cannot keep it in a register across loops, nor spill and reload it there.
+__device__ __forceinline__ int lane_fresh() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 template <int DEG>
 struct LateBasis {
     float x, y, z;
@@ -965,10 +973,12 @@ __device__ int walk_group(const FoamScene& S, int c, int g, float x0, float x1, 
 
 // eval_cell for lane g of a group: the lane's share of the neighbourhood, then the group reductions.
 template <int STAGE, int COLOR, bool HALF, int DEG, int G, bool TABLE>
-__device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, int g, float t, const float (&o)[3],
-                                const float (&d)[3], const float (&b)[16], ColorCache<COLOR>& cache,
-                                bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
+__device__ void eval_cell_group(const FoamScene& S, const FoamParams& P, int c, int g_in, float t,
+                                const float (&o)[3], const float (&d)[3], const float (&b)[16],
+                                ColorCache<COLOR>& cache, bool want_exit, CellEval& R, int& n_dens, int& n_sh) {
     constexpr bool BLEND = STAGE >= 2 && COLOR != kLazy;
+    // the lane's place in its group (blocks of one wave): with 8 lanes per ray read afresh, not held across samples
+    const int g = G == kLateBasisLanes ? lane_fresh() % G : g_in;
     const float4 pc = S.points[c];
     float x[3];
     sample_point(o, d, t, x);
@@ -1098,7 +1108,7 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock / G, TABLE>(S
     const int g = static_cast<int>(threadIdx.x) % G;
     const int64_t i = xcd_block_id() * (kBlock / G) + threadIdx.x / G;
     if (i >= R.n) return;  // whole groups leave together
-    const int64_t r = R.order != nullptr ? R.order[i] : i;
+    int64_t r = R.order != nullptr ? R.order[i] : i;
     if (r < 0 || r >= R.n) return;
     const bool writer = g == 0;
     const int start = R.start[r];
@@ -1177,6 +1187,10 @@ __global__ void __launch_bounds__(kBlock, (waves_for<COLOR, kBlock / G, TABLE>(S
         if (last || T < P.t_thresh) break;
     }
     n_dens = group_sum<G>(n_dens), n_sh = group_sum<G>(n_sh);
+    if (G == kLateBasisLanes && !TRACE) {  // the ray index read again rather than held across the sample loop
+        const int64_t i_end = xcd_block_id() * (kBlock / G) + lane_fresh() / G;
+        r = R.order != nullptr ? R.order[i_end] : i_end;
+    }
     if (writer) {
 #pragma unroll
         for (int a = 0; a < 3; ++a) O.rgb[3 * r + a] = acc[a];
