@@ -412,6 +412,25 @@ int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t stride, const
                      const int32_t* res, const int32_t* cell_start, const int32_t* cell_sites, const float* queries,
                      int64_t n_queries, int32_t* site, void* stream);
 
+/*
+ * A cell-ordered copy of the sites of a grid built by vgr_grid_build (or _noalloc), for vgr_grid_nearest_points:
+ * cell_points[s] = (x, y, z, bits of cell_sites[s]), so that the sites of a cell, and of a row of cells, lie in
+ * consecutive 16-byte records. A snapshot of the positions: build it again after moving the sites. No counterpart in
+ * the reference (part of the same replacement of nearest_sites, sites.py:38-39).
+ *   points f32 (N, stride), cell_sites i32 (N) -> cell_points f32 (N, 4), 16-byte aligned
+ */
+int vgr_grid_cell_points(const float* points, int64_t n_sites, int32_t stride, const int32_t* cell_sites,
+                         float* cell_points, void* stream);
+
+/*
+ * vgr_grid_nearest over the cell-ordered copy of vgr_grid_cell_points: the same answers bit for bit, with the
+ * candidate sites read in cell order instead of through their indices (one 128-byte line per candidate there).
+ *   cell_points f32 (N, 4), 16-byte aligned; queries f32 (m, 3) -> site i32 (m); the grid as built
+ */
+int vgr_grid_nearest_points(const float* cell_points, int64_t n_sites, const float* lo, const float* cell,
+                            const int32_t* res, const int32_t* cell_start, const float* queries, int64_t n_queries,
+                            int32_t* site, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,7 +32,7 @@ def test_header_declares_the_entry_points():
 			  'vgr_pack_foam', 'vgr_morton_work_size', 'vgr_morton_codes', 'vgr_bake_colors', 'vgr_grid_work_size',
 			  'vgr_grid_build', 'vgr_grid_nearest', 'vgr_ray_order_work_size', 'vgr_ray_order', 'vgr_last_error',
 			  'vgr_abi_version', 'vgr_foam_index_pack', 'vgr_foam_infer_indexed', 'vgr_grid_build_noalloc',
-			  'vgr_foam_slot_table'):
+			  'vgr_foam_slot_table', 'vgr_grid_cell_points', 'vgr_grid_nearest_points'):
 		assert n in names
 
 
@@ -72,6 +72,19 @@ def test_library_reports_argument_errors_without_a_gpu():
 	rc = lib.vgr_grid_build(None, 1, 3, f3(0, 0, 0), f3(1, 1, -1), i3(1, 1, 1), None, None, None, None)
 	assert rc == 1 and b'cell edge 2' in lib.vgr_last_error()
 	assert lib.vgr_grid_nearest(None, 1, 3, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, None, 0, None, None) == 0
+	# the cell-ordered copy and the queries over it: sizes, pointers and alignment checked on the host
+	assert lib.vgr_grid_cell_points(None, -1, 3, None, None, None) == 1 and b'n_sites' in lib.vgr_last_error()
+	assert lib.vgr_grid_cell_points(None, 10, 2, None, None, None) == 1 and b'stride' in lib.vgr_last_error()
+	assert lib.vgr_grid_cell_points(None, 10, 3, None, None, None) == 1 and b'null pointer' in lib.vgr_last_error()
+	fake = ctypes.c_void_p(1 << 20)
+	rc = lib.vgr_grid_cell_points(fake, 10, 3, fake, ctypes.c_void_p((1 << 20) + 8), None)
+	assert rc == 1 and b'16-byte aligned' in lib.vgr_last_error()
+	assert lib.vgr_grid_cell_points(None, 0, 3, None, None, None) == 0
+	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(0, 1, 1), None, None, 5, None, None)
+	assert rc == 1 and b'res[0]' in lib.vgr_last_error()
+	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 5, None, None)
+	assert rc == 1 and b'null pointer' in lib.vgr_last_error()
+	assert lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 0, None, None) == 0
 	# march: one line-aligned block per site in the caller's work buffer (record + SH: 128 B up to sh_deg 1, else
 	# 256 B), checked before the pack launch
 	assert lib.vgr_march_work_size(0, 3) == 0 and lib.vgr_march_work_size(1000, 4) == 0

@@ -1,5 +1,6 @@
-"""GPU start-cell locator (vgr.grid / vgr_grid_build, vgr_grid_nearest) against the exhaustive float64 oracle and
-scipy's cKDTree (the reference's nearest_sites, sites.py:38-39): identical site indices."""
+"""GPU start-cell locator (vgr.grid / vgr_grid_build, vgr_grid_cell_points, vgr_grid_nearest_points, and
+vgr_grid_nearest) against the exhaustive float64 oracle and scipy's cKDTree (the reference's nearest_sites,
+sites.py:38-39): identical site indices, the same from both query kernels."""
 
 import numpy as np
 import pytest
@@ -16,9 +17,13 @@ def T(a, dev):
 
 
 def gpu_nearest(dev, pts, q, **kw):
+	"""Nearest sites through the cell-ordered copy (SiteGrid.nearest), checked equal to the kernel that reads the
+	candidates through their indices (SiteGrid.nearest_indexed)."""
 	g = grid.SiteGrid(T(pts, dev), **kw)
 	out = g.nearest(T(q, dev))
+	via_index = g.nearest_indexed(T(q, dev))
 	torch.cuda.synchronize()
+	np.testing.assert_array_equal(out.cpu().numpy(), via_index.cpu().numpy())
 	return out.cpu().numpy(), g
 
 
@@ -34,6 +39,10 @@ def test_uniform_sites_inside_and_outside(gpu, per_cell):
 	cs = g.cell_start.cpu().numpy()
 	assert cs[0] == 0 and cs[-1] == len(pts) and (np.diff(cs) >= 0).all()
 	np.testing.assert_array_equal(np.sort(g.cell_sites.cpu().numpy()), np.arange(len(pts)))
+	# the cell-ordered copy: slot s holds site cell_sites[s], its position and the bits of its index
+	cp, sites_ = g.cell_points.cpu().numpy(), g.cell_sites.cpu().numpy()
+	np.testing.assert_array_equal(cp[:, :3], pts[sites_])
+	np.testing.assert_array_equal(cp[:, 3].view(np.int32), sites_)
 
 
 def test_clustered_and_shell_sites_match_ckdtree(gpu):

@@ -54,6 +54,16 @@ __global__ void __launch_bounds__(kBlock) grid_fill(int64_t n, const int* __rest
     cell_sites[atomicAdd(cursor + cell_of[i], 1)] = static_cast<int>(i);
 }
 
+// The build's cell-ordered copy of the sites: slot s of cell_sites gets (x, y, z, bits of the site index).
+__global__ void __launch_bounds__(kBlock) grid_cell_points(const float* __restrict__ pts, int stride, int64_t n,
+                                                           const int* __restrict__ cell_sites, float4* __restrict__ cp) {
+    const int64_t s = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (s >= n) return;
+    const int k = cell_sites[s];
+    const float* p = site_ptr(pts, stride, k);
+    cp[s] = make_float4(p[0], p[1], p[2], __int_as_float(k));
+}
+
 // Fills n ints with zero (the counters of a build; a kernel rather than hipMemsetAsync, so that a build is made of
 // kernel launches only).
 __global__ void __launch_bounds__(kBlock) zero_ints(int* __restrict__ a, int64_t n) {
@@ -97,11 +107,14 @@ int scratch_on_current_device(int** out) {
 // no unscanned site is closer than the distance lb from the query to the nearest such region (for a query outside
 // the grid, that includes its distance to the grid); the scan stops once the best distance is below lb (shrunk by
 // a margin covering the float32 rounding of cell assignment), or when the block covers the grid.
+// CP: the sites' positions come from the build's cell-ordered copy (grid_cell_points: the sites of a cell, and of a
+// row of cells, share lines) instead of through the site index into the point array (a line per site).
+template <bool CP>
 __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__ pts, int stride, Geom g,
                                                        const int* __restrict__ cell_start,
                                                        const int* __restrict__ cell_sites,
-                                                       const float* __restrict__ q, int64_t m, double margin,
-                                                       int* __restrict__ out) {
+                                                       const float4* __restrict__ cp, const float* __restrict__ q,
+                                                       int64_t m, double margin, int* __restrict__ out) {
     const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= m) return;
     const double qx = q[3 * i], qy = q[3 * i + 1], qz = q[3 * i + 2];
@@ -114,9 +127,17 @@ __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__
     const auto visit = [&](int x, int y, int z) {
         const int cell = (z * g.res[1] + y) * g.res[0] + x;
         for (int s = cell_start[cell], e = cell_start[cell + 1]; s < e; ++s) {
-            const int k = cell_sites[s];
-            const float* p = site_ptr(pts, stride, k);
-            const double dx = qx - p[0], dy = qy - p[1], dz = qz - p[2];
+            float px, py, pz;
+            int k;
+            if constexpr (CP) {
+                const float4 v = cp[s];
+                px = v.x, py = v.y, pz = v.z, k = __float_as_int(v.w);
+            } else {
+                k = cell_sites[s];
+                const float* p = site_ptr(pts, stride, k);
+                px = p[0], py = p[1], pz = p[2];
+            }
+            const double dx = qx - px, dy = qy - py, dz = qz - pz;
             const double d2 = dx * dx + dy * dy + dz * dz;
             if (d2 < best || (d2 == best && k < best_k)) best = d2, best_k = k;
         }
@@ -167,6 +188,15 @@ __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__
         if (lb > 0.0 && best < lb * lb) break;
     }
     out[i] = best_k;
+}
+
+// float32 cell assignment can put a site one rounding step across a cell face: the stopping bound shrinks by a few
+// float32 ulps of the grid's extent.
+double nearest_margin(const float* lo, const float* cell, const int32_t* res) {
+    double extent = 0.0;
+    for (int a = 0; a < 3; ++a)
+        extent = fmax(extent, fabs(double(lo[a])) + double(cell[a]) * res[a]);
+    return extent * 1e-6;
 }
 
 Geom make_geom(const float* lo, const float* cell, const int32_t* res) {
@@ -279,14 +309,44 @@ extern "C" int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t st
                 static_cast<long long>(n_sites));
     VGR_REQUIRE(stride >= 3, "grid_nearest: stride must be >= 3 floats (got %d)", stride);
     VGR_REQUIRE(points && cell_start && cell_sites && queries && site, "grid_nearest: null pointer");
-    // float32 cell assignment can put a site one rounding step across a cell face: shrink the stopping bound by
-    // a few float32 ulps of the grid's extent
-    double extent = 0.0;
-    for (int a = 0; a < 3; ++a)
-        extent = fmax(extent, fabs(double(lo[a])) + double(cell[a]) * res[a]);
-    const double margin = extent * 1e-6;
     const Geom g = make_geom(lo, cell, res);
-    hipLaunchKernelGGL(grid_nearest, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream), points,
-                       int(stride), g, cell_start, cell_sites, queries, n_queries, margin, site);
+    hipLaunchKernelGGL(grid_nearest<false>, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream),
+                       points, int(stride), g, cell_start, cell_sites, nullptr, queries, n_queries,
+                       nearest_margin(lo, cell, res), site);
     return launch_status("grid_nearest");
+}
+
+extern "C" int vgr_grid_cell_points(const float* points, int64_t n_sites, int32_t stride, const int32_t* cell_sites,
+                                    float* cell_points, void* stream) {
+    using namespace vgr;
+    VGR_REQUIRE(n_sites >= 0 && n_sites <= INT_MAX, "grid_cell_points: n_sites must be in [0, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    VGR_REQUIRE(stride >= 3, "grid_cell_points: stride must be >= 3 floats (got %d)", stride);
+    if (n_sites == 0) return VGR_OK;
+    VGR_REQUIRE(points && cell_sites && cell_points, "grid_cell_points: null pointer");
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(cell_points) % 16 == 0, "grid_cell_points: cell_points must be 16-byte "
+                "aligned");
+    hipLaunchKernelGGL(grid_cell_points, dim3(grid_for(n_sites, kBlock)), dim3(kBlock), 0, as_stream(stream), points,
+                       int(stride), n_sites, cell_sites, reinterpret_cast<float4*>(cell_points));
+    return launch_status("grid_cell_points");
+}
+
+extern "C" int vgr_grid_nearest_points(const float* cell_points, int64_t n_sites, const float* lo, const float* cell,
+                                       const int32_t* res, const int32_t* cell_start, const float* queries,
+                                       int64_t n_queries, int32_t* site, void* stream) {
+    using namespace vgr;
+    int64_t n_cells = 0;
+    if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
+    VGR_REQUIRE(n_queries >= 0, "grid_nearest_points: n_queries must be >= 0");
+    if (n_queries == 0) return VGR_OK;
+    VGR_REQUIRE(n_sites >= 1 && n_sites <= INT_MAX, "grid_nearest_points: n_sites must be in [1, 2^31) (got %lld)",
+                static_cast<long long>(n_sites));
+    VGR_REQUIRE(cell_points && cell_start && queries && site, "grid_nearest_points: null pointer");
+    VGR_REQUIRE(reinterpret_cast<uintptr_t>(cell_points) % 16 == 0, "grid_nearest_points: cell_points must be "
+                "16-byte aligned");
+    const Geom g = make_geom(lo, cell, res);
+    hipLaunchKernelGGL(grid_nearest<true>, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream),
+                       nullptr, 3, g, cell_start, nullptr, reinterpret_cast<const float4*>(cell_points), queries,
+                       n_queries, nearest_margin(lo, cell, res), site);
+    return launch_status("grid_nearest (cell points)");
 }

@@ -1,5 +1,5 @@
 """Start-cell locator on the GPU: a uniform grid over the sites and exact nearest-site queries (libvgr's
-vgr_grid_build / vgr_grid_nearest).
+vgr_grid_build, vgr_grid_cell_points, vgr_grid_nearest_points).
 
 It replaces the host-side cKDTree query of the reference's nearest_sites (sites.py:38-39), which finds the start
 site of the traversal per camera centre (bench_infer.py:60, eval_scene.py:69) and per ray origin of a ray batch.
@@ -49,9 +49,25 @@ class SiteGrid:
 		_lib.call('vgr_grid_build', _lib.ptr(points), n, self.stride, *self._geom, _lib.ptr(self.cell_start),
 				  _lib.ptr(self.cell_sites), _lib.ptr(work), _lib.stream_of(dev))
 		self._work = work  # released once the asynchronous build has run (caching allocator, same stream)
+		# the sites in cell order, (x, y, z, bits of the index) each, which the queries scan (a snapshot of points)
+		self.cell_points = torch.empty(n, 4, dtype=torch.float32, device=dev)
+		_lib.call('vgr_grid_cell_points', _lib.ptr(points), n, self.stride, _lib.ptr(self.cell_sites),
+				  _lib.ptr(self.cell_points), _lib.stream_of(dev))
 
 	def nearest(self, queries):
 		"""Index (int32) of the nearest site of every query point: queries (m, 3) float32 CUDA tensor."""
+		if not (isinstance(queries, torch.Tensor) and queries.is_cuda):
+			raise RuntimeError('queries must be a CUDA tensor')
+		if queries.dtype != torch.float32 or queries.dim() != 2 or queries.shape[1] != 3 or not queries.is_contiguous():
+			raise RuntimeError('queries must be a contiguous float32 (m, 3) tensor')
+		out = torch.empty(len(queries), dtype=torch.int32, device=queries.device)
+		_lib.call('vgr_grid_nearest_points', _lib.ptr(self.cell_points), self.n, *self._geom, _lib.ptr(self.cell_start),
+				  _lib.ptr(queries), len(queries), _lib.ptr(out), _lib.stream_of(queries.device))
+		return out
+
+	def nearest_indexed(self, queries):
+		"""nearest() reading the candidate sites through their indices into the point array (vgr_grid_nearest):
+		the same answers."""
 		if not (isinstance(queries, torch.Tensor) and queries.is_cuda):
 			raise RuntimeError('queries must be a CUDA tensor')
 		if queries.dtype != torch.float32 or queries.dim() != 2 or queries.shape[1] != 3 or not queries.is_contiguous():
