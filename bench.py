@@ -711,8 +711,10 @@ def mrays_per_s(B, ms):
 
 def bench_locate(args):
 	"""Start-cell location for config 5: the nearest of 4,000,000 sites for each of the 16,777,216 ray origins
-	(vgr_grid_nearest over a grid built once, outside the timed region). CPU baseline: the reference's own
-	nearest_sites (scipy cKDTree, sites.py:38-39, single-threaded as called there) on a bounded sample."""
+	(vgr_grid_nearest_points over a grid and its cell-ordered sites built once, outside the timed region; the
+	origins answered in their Z-order, computed inside the timed step, unless --order off). CPU baseline: the
+	reference's own nearest_sites (scipy cKDTree, sites.py:38-39, single-threaded as called there) on a bounded
+	sample."""
 	import numpy as np
 	import torch
 
@@ -726,7 +728,13 @@ def bench_locate(args):
 	stream = torch.cuda.current_stream(dev)
 	build_ms, g, _ = time_steps(lambda: grid.SiteGrid(pts), 3, 1, stream)
 	n_cells = g.res[0] * g.res[1] * g.res[2]
-	launch_ms, out, wall = time_steps(lambda: g.nearest(q), args.steps, args.warmup, stream)
+	ordered = args.order != 'off'  # the origins of a ray batch come in no spatial order
+	pos_bits = args.order_pos_bits or 8
+	if ordered:
+		step = lambda: g.nearest(q, order=grid.query_order(q, pos_bits))  # noqa: E731
+	else:
+		step = lambda: g.nearest(q)  # noqa: E731
+	launch_ms, out, wall = time_steps(step, args.steps, args.warmup, stream)
 	ms = float(np.mean(launch_ms))
 	log(f'grid {g.res} ({n_cells} cells) built in {np.mean(build_ms):.3f} ms; {args.steps} queries launches: '
 		f'mean {ms:.3f} ms, wall {wall:.3f} ms/step')
@@ -758,8 +766,10 @@ def bench_locate(args):
 		 'Mqueries/s', args, ms,
 		 {'workload': f'config 5 start cells: nearest of {N} sites (seeded uniform draw) for each of {B} ray '
 					  f'origins', 'sites': N, 'queries': B, 'grid_res': g.res,
-		  'grid_build_ms': round(float(np.mean(build_ms)), 3)},
-		 hbm_roofline(ms, f'config5-locate', source_hash('grid.hip'), abytes,
+		  'grid_build_ms': round(float(np.mean(build_ms)), 3),
+		  'query_order': (f'Z-order of the origins, {pos_bits} bits per axis (vgr_ray_order, one direction bin), '
+						  f'inside the timed step' if ordered else 'as given')},
+		 hbm_roofline(ms, 'config5-locate' + (f'-order{pos_bits}' if ordered else ''), source_hash('grid.hip'), abytes,
 					  'compulsory bytes: each query point, site and grid word read once, each answer written once',
 					  'grid_nearest'), cpu)
 

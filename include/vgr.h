@@ -425,11 +425,14 @@ int vgr_grid_cell_points(const float* points, int64_t n_sites, int32_t stride, c
 /*
  * vgr_grid_nearest over the cell-ordered copy of vgr_grid_cell_points: the same answers bit for bit, with the
  * candidate sites read in cell order instead of through their indices (one 128-byte line per candidate there).
- *   cell_points f32 (N, 4), 16-byte aligned; queries f32 (m, 3) -> site i32 (m); the grid as built
+ * order (NULL = 0 .. m - 1): a permutation of the queries, the order in which they are answered (a lane skips an
+ * entry outside [0, m)); a spatially coherent one (vgr_ray_order over the queries with dir_res 1, a Z-order of the
+ * points) lets the lanes of a wave share the cells they scan. The answers do not depend on it.
+ *   cell_points f32 (N, 4), 16-byte aligned; queries f32 (m, 3); order i32 (m) or NULL -> site i32 (m)
  */
 int vgr_grid_nearest_points(const float* cell_points, int64_t n_sites, const float* lo, const float* cell,
                             const int32_t* res, const int32_t* cell_start, const float* queries, int64_t n_queries,
-                            int32_t* site, void* stream);
+                            const int32_t* order, int32_t* site, void* stream);
 
 #ifdef __cplusplus
 }

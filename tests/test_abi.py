@@ -80,11 +80,12 @@ def test_library_reports_argument_errors_without_a_gpu():
 	rc = lib.vgr_grid_cell_points(fake, 10, 3, fake, ctypes.c_void_p((1 << 20) + 8), None)
 	assert rc == 1 and b'16-byte aligned' in lib.vgr_last_error()
 	assert lib.vgr_grid_cell_points(None, 0, 3, None, None, None) == 0
-	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(0, 1, 1), None, None, 5, None, None)
+	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(0, 1, 1), None, None, 5, None, None, None)
 	assert rc == 1 and b'res[0]' in lib.vgr_last_error()
-	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 5, None, None)
+	rc = lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 5, None, None, None)
 	assert rc == 1 and b'null pointer' in lib.vgr_last_error()
-	assert lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 0, None, None) == 0
+	assert lib.vgr_grid_nearest_points(None, 1, f3(0, 0, 0), f3(1, 1, 1), i3(1, 1, 1), None, None, 0, None, None,
+									   None) == 0
 	# march: one line-aligned block per site in the caller's work buffer (record + SH: 128 B up to sh_deg 1, else
 	# 256 B), checked before the pack launch
 	assert lib.vgr_march_work_size(0, 3) == 0 and lib.vgr_march_work_size(1000, 4) == 0

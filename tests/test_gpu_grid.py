@@ -1,6 +1,6 @@
 """GPU start-cell locator (vgr.grid / vgr_grid_build, vgr_grid_cell_points, vgr_grid_nearest_points, and
 vgr_grid_nearest) against the exhaustive float64 oracle and scipy's cKDTree (the reference's nearest_sites,
-sites.py:38-39): identical site indices, the same from both query kernels."""
+sites.py:38-39): identical site indices, the same from both query kernels and in a coherent query order."""
 
 import numpy as np
 import pytest
@@ -20,10 +20,13 @@ def gpu_nearest(dev, pts, q, **kw):
 	"""Nearest sites through the cell-ordered copy (SiteGrid.nearest), checked equal to the kernel that reads the
 	candidates through their indices (SiteGrid.nearest_indexed)."""
 	g = grid.SiteGrid(T(pts, dev), **kw)
-	out = g.nearest(T(q, dev))
-	via_index = g.nearest_indexed(T(q, dev))
+	qt = T(q, dev)
+	out = g.nearest(qt)
+	via_index = g.nearest_indexed(qt)
+	ordered = g.nearest(qt, order=grid.query_order(qt))
 	torch.cuda.synchronize()
 	np.testing.assert_array_equal(out.cpu().numpy(), via_index.cpu().numpy())
+	np.testing.assert_array_equal(out.cpu().numpy(), ordered.cpu().numpy())
 	return out.cpu().numpy(), g
 
 

@@ -28,4 +28,4 @@ int launch_status(const char* kernel) {
 
 extern "C" const char* vgr_last_error(void) { return vgr::g_error; }
 
-extern "C" int vgr_abi_version(void) { return 26; }
+extern "C" int vgr_abi_version(void) { return 27; }

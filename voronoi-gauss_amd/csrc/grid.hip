@@ -114,9 +114,12 @@ __global__ void __launch_bounds__(kBlock) grid_nearest(const float* __restrict__
                                                        const int* __restrict__ cell_start,
                                                        const int* __restrict__ cell_sites,
                                                        const float4* __restrict__ cp, const float* __restrict__ q,
-                                                       int64_t m, double margin, int* __restrict__ out) {
-    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= m) return;
+                                                       int64_t m, const int* __restrict__ order, double margin,
+                                                       int* __restrict__ out) {
+    const int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (t >= m) return;
+    const int64_t i = order != nullptr ? order[t] : t;  // the query this lane answers (a permutation entry)
+    if (i < 0 || i >= m) return;
     const double qx = q[3 * i], qy = q[3 * i + 1], qz = q[3 * i + 2];
     const int c[3] = {axis_cell(static_cast<float>(qx), g.lo[0], g.cell[0], g.res[0]),
                       axis_cell(static_cast<float>(qy), g.lo[1], g.cell[1], g.res[1]),
@@ -311,7 +314,7 @@ extern "C" int vgr_grid_nearest(const float* points, int64_t n_sites, int32_t st
     VGR_REQUIRE(points && cell_start && cell_sites && queries && site, "grid_nearest: null pointer");
     const Geom g = make_geom(lo, cell, res);
     hipLaunchKernelGGL(grid_nearest<false>, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream),
-                       points, int(stride), g, cell_start, cell_sites, nullptr, queries, n_queries,
+                       points, int(stride), g, cell_start, cell_sites, nullptr, queries, n_queries, nullptr,
                        nearest_margin(lo, cell, res), site);
     return launch_status("grid_nearest");
 }
@@ -333,7 +336,7 @@ extern "C" int vgr_grid_cell_points(const float* points, int64_t n_sites, int32_
 
 extern "C" int vgr_grid_nearest_points(const float* cell_points, int64_t n_sites, const float* lo, const float* cell,
                                        const int32_t* res, const int32_t* cell_start, const float* queries,
-                                       int64_t n_queries, int32_t* site, void* stream) {
+                                       int64_t n_queries, const int32_t* order, int32_t* site, void* stream) {
     using namespace vgr;
     int64_t n_cells = 0;
     if (int rc = check_geom(lo, cell, res, &n_cells)) return rc;
@@ -347,6 +350,6 @@ extern "C" int vgr_grid_nearest_points(const float* cell_points, int64_t n_sites
     const Geom g = make_geom(lo, cell, res);
     hipLaunchKernelGGL(grid_nearest<true>, dim3(grid_for(n_queries, kBlock)), dim3(kBlock), 0, as_stream(stream),
                        nullptr, 3, g, cell_start, nullptr, reinterpret_cast<const float4*>(cell_points), queries,
-                       n_queries, nearest_margin(lo, cell, res), site);
+                       n_queries, order, nearest_margin(lo, cell, res), site);
     return launch_status("grid_nearest (cell points)");
 }

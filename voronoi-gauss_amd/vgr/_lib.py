@@ -66,12 +66,12 @@ SIGNATURES = {
 	'vgr_grid_build_noalloc': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P],
 	'vgr_grid_nearest': [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P],
 	'vgr_grid_cell_points': [_P, _I64, _I32, _P, _P, _P],
-	'vgr_grid_nearest_points': [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P],
+	'vgr_grid_nearest_points': [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P],
 	'vgr_abi_version': [],
 	'vgr_last_error': [],
 }
 
-ABI_VERSION = 26
+ABI_VERSION = 27
 _lib = None
 
 

@@ -54,15 +54,20 @@ class SiteGrid:
 		_lib.call('vgr_grid_cell_points', _lib.ptr(points), n, self.stride, _lib.ptr(self.cell_sites),
 				  _lib.ptr(self.cell_points), _lib.stream_of(dev))
 
-	def nearest(self, queries):
-		"""Index (int32) of the nearest site of every query point: queries (m, 3) float32 CUDA tensor."""
+	def nearest(self, queries, order=None):
+		"""Index (int32) of the nearest site of every query point: queries (m, 3) float32 CUDA tensor. order:
+		optional int32 (m,) permutation of 0 .. m - 1, the order in which the queries are answered (query_order
+		gives a coherent one); the answers do not depend on it."""
 		if not (isinstance(queries, torch.Tensor) and queries.is_cuda):
 			raise RuntimeError('queries must be a CUDA tensor')
 		if queries.dtype != torch.float32 or queries.dim() != 2 or queries.shape[1] != 3 or not queries.is_contiguous():
 			raise RuntimeError('queries must be a contiguous float32 (m, 3) tensor')
+		if order is not None and not (isinstance(order, torch.Tensor) and order.is_cuda and order.dtype == torch.int32
+									  and order.shape == (len(queries),) and order.is_contiguous()):
+			raise RuntimeError('order must be a contiguous int32 CUDA tensor of one entry per query')
 		out = torch.empty(len(queries), dtype=torch.int32, device=queries.device)
 		_lib.call('vgr_grid_nearest_points', _lib.ptr(self.cell_points), self.n, *self._geom, _lib.ptr(self.cell_start),
-				  _lib.ptr(queries), len(queries), _lib.ptr(out), _lib.stream_of(queries.device))
+				  _lib.ptr(queries), len(queries), _lib.ptr(order), _lib.ptr(out), _lib.stream_of(queries.device))
 		return out
 
 	def nearest_indexed(self, queries):
@@ -77,6 +82,14 @@ class SiteGrid:
 				  _lib.ptr(self.cell_start), _lib.ptr(self.cell_sites), _lib.ptr(queries), len(queries), _lib.ptr(out),
 				  _lib.stream_of(queries.device))
 		return out
+
+
+def query_order(queries, pos_bits=8):
+	"""A spatially coherent processing order of query points for SiteGrid.nearest: int32 (m,) permutation sorting
+	them along the Z-order curve of pos_bits bits per axis over their bounding box (vgr_ray_order with one direction
+	bin). The lanes of a wave then scan neighbouring cells."""
+	from . import ext
+	return ext.ray_order(queries, queries, dir_res=1, pos_bits=pos_bits)
 
 
 def _floats(v):
