@@ -87,6 +87,10 @@ def test_nearest_sites_dispatch_and_errors(gpu):
 	dev = sites.nearest_sites(T(pts, gpu), T(q, gpu))
 	assert isinstance(host, np.ndarray) and dev.is_cuda and dev.dtype == torch.int32
 	np.testing.assert_array_equal(dev.cpu().numpy(), host)
+	# a batch above 65,536 queries is answered in its Z-order: the same answers
+	qb = rng.uniform(-1.2, 1.2, (100000, 3)).astype(np.float32)
+	np.testing.assert_array_equal(sites.nearest_sites(T(pts, gpu), T(qb, gpu)).cpu().numpy(),
+								  sites.nearest_sites(pts, qb))
 	with pytest.raises(RuntimeError, match='CUDA tensor'):
 		grid.SiteGrid(torch.as_tensor(pts))
 	with pytest.raises(RuntimeError, match='float32'):

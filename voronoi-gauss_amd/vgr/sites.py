@@ -26,10 +26,13 @@ def delaunay_graph(points, attempts=3):
 def nearest_sites(points, queries):
 	"""Index of the nearest site of every query point (sites.py:38-39). numpy arrays: scipy's cKDTree, as the
 	reference does; CUDA tensors: the GPU grid of vgr.grid.SiteGrid (the same answers up to exact distance ties,
-	which go to the smaller index), returned as an int32 CUDA tensor."""
+	which go to the smaller index; batches above 65,536 queries answered in their Z-order), returned as an int32 CUDA
+	tensor."""
 	if getattr(points, 'is_cuda', False):
-		from .grid import SiteGrid
-		return SiteGrid(points.contiguous()).nearest(queries.contiguous())
+		from .grid import SiteGrid, query_order
+		q = queries.contiguous()
+		# large batches (a ray batch's origins) are answered in their Z-order, which lets a wave's lanes share cells
+		return SiteGrid(points.contiguous()).nearest(q, order=query_order(q) if len(q) > 65536 else None)
 	return cKDTree(points).query(queries, workers=-1)[1].astype(np.int32)
 
 
